@@ -1,0 +1,466 @@
+"""Benchmark of the PESQ loss (forward + backward) on one MI355X.
+
+``python bench.py --gpus 1 --steps K --warmup W`` times K forward+backward
+steps of :class:`torch_pesq.PesqLossTriton` on BASELINE config c2 (B = 8 items
+of 8 s at 16 kHz, gradient w.r.t. the degraded signal) replayed from a HIP
+graph, and prints one JSON line with the metric, the eager time, the HBM
+roofline of the dominant kernel measured with HIP events on the stream the
+kernels run on, and a CPU baseline (the float32 restatement of the reference
+``PesqLoss``, timed on this host).
+
+Synthetic inputs: :func:`synthetic_config` (seeded voiced-speech generator of
+the five BASELINE configs).
+"""
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+PKG = ROOT / "triton-pesq_amd"
+
+# ---------------------------------------------------------------------------
+# synthetic inputs
+# ---------------------------------------------------------------------------
+
+#: (items, samples, sample_rate) of the five BASELINE configs
+CONFIGS = {
+    1: (1, 16000, 16000),
+    2: (8, 128000, 16000),
+    3: (16, 176400, 44100),
+    4: (4, 960000, 16000),
+    5: (256, 192000, 48000),
+}
+
+
+def _resonate(x, fc, bw, fs):
+    """Two-pole resonator at ``fc`` with bandwidth ``bw``, unit gain at ``fc``."""
+
+    from scipy.signal import lfilter
+
+    r = math.exp(-math.pi * bw / fs)
+    theta = 2 * math.pi * fc / fs
+    a = [1.0, -2 * r * math.cos(theta), r * r]
+    gain = abs(1 - 2 * r * math.cos(theta) * np.exp(-1j * theta) + r * r * np.exp(-2j * theta))
+    return lfilter([gain], a, x)
+
+
+def _harmonics(phase, kmax):
+    """``sum_k sin(k phase) / k`` for ``k = 1..kmax`` by the Chebyshev recurrence."""
+
+    two_cos = 2.0 * np.cos(phase)
+    prev, cur = np.zeros_like(phase), np.sin(phase)
+    out = cur.copy()
+    for k in range(2, kmax + 1):
+        prev, cur = cur, two_cos * cur - prev
+        out += cur / k
+    return out
+
+
+def speech(rng, n, fs, harmonic_only=False):
+    """Seeded voiced speech: harmonics of a vibrato f0, formants, syllabic AM.
+
+    f0 ~ U[100, 250] Hz with +-10 % vibrato at 5 Hz; harmonics up to 0.45 fs
+    with 1/k amplitude; three two-pole formant resonators at 500/1500/2500 Hz
+    (bandwidths 80/120/160 Hz); a 4 Hz raised cosine envelope whose syllables
+    are silent with probability 0.2; RMS 0.05.  ``harmonic_only`` skips the
+    formants and the envelope.
+    """
+
+    t = np.arange(n) / fs
+    f0 = rng.uniform(100.0, 250.0)
+    vib = rng.uniform(0.0, 2 * math.pi)
+    inst = f0 * (1.0 + 0.1 * np.sin(2 * math.pi * 5.0 * t + vib))
+    phase = 2 * math.pi * np.cumsum(inst) / fs + rng.uniform(0.0, 2 * math.pi)
+    kmax = max(1, int(0.45 * fs / (1.1 * f0)))
+    sig = _harmonics(phase, kmax)
+
+    if not harmonic_only:
+        sig = sum(_resonate(sig, fc, bw, fs) for fc, bw in ((500, 80), (1500, 120), (2500, 160)))
+        syll = np.floor(t * 4.0).astype(np.int64)
+        on = rng.uniform(size=int(syll[-1]) + 1) >= 0.2
+        env = 0.5 - 0.5 * np.cos(2 * math.pi * 4.0 * t)
+        sig = sig * env * on[syll]
+
+    rms = math.sqrt(float(np.mean(sig**2))) or 1.0
+    return sig * (0.05 / rms)
+
+
+def _pink(rng, n):
+    """Unit-RMS pink (1/f power) noise shaped in the frequency domain."""
+
+    spec = np.fft.rfft(rng.standard_normal(n))
+    freq = np.arange(spec.shape[0], dtype=np.float64)
+    freq[0] = 1.0
+    noise = np.fft.irfft(spec / np.sqrt(freq), n)
+    return noise / math.sqrt(float(np.mean(noise**2)))
+
+
+def _at_snr(sig, noise, snr_db):
+    power = float(np.mean(sig**2))
+    return noise * math.sqrt(power / 10 ** (snr_db / 10.0))
+
+
+def synthetic_item(config: int, item: int, samples: int = None):
+    """One (ref, deg) float32 pair of BASELINE config ``config``."""
+
+    _, n_default, fs = CONFIGS[config]
+    n = n_default if samples is None else samples
+    rng = np.random.default_rng([config, item])
+
+    harmonic_only = config == 5 and rng.uniform() < 0.25
+    ref = speech(rng, n, fs, harmonic_only=harmonic_only)
+
+    if config == 1:
+        deg = ref + _at_snr(ref, rng.standard_normal(n), 10.0)
+    elif config == 2:
+        deg = ref + _at_snr(ref, rng.standard_normal(n), rng.uniform(0.0, 20.0))
+    elif config == 3:
+        from scipy.signal import butter, lfilter
+
+        b, a = butter(2, rng.uniform(3000.0, 7000.0), fs=fs)
+        deg = lfilter(b, a, ref)
+        deg = deg + _at_snr(ref, _pink(rng, n), 5.0)
+    elif config == 4:
+        deg = ref + _at_snr(ref, _pink(rng, n), 0.0)
+        peak = 0.8 * float(np.abs(deg).max())
+        deg = np.clip(deg, -peak, peak)
+    else:
+        deg = ref + _at_snr(ref, rng.standard_normal(n), rng.uniform(-5.0, 20.0))
+        if rng.uniform() < 0.1:
+            gain = 10 ** (rng.uniform(-20.0, 6.0) / 20.0)
+            ref, deg = ref * gain, deg * gain
+
+    return ref.astype(np.float32), deg.astype(np.float32)
+
+
+def synthetic_config(config: int, items: int = None, samples: int = None):
+    """``(ref[B, N], deg[B, N], sample_rate)`` of a BASELINE config, float32."""
+
+    count, _, fs = CONFIGS[config]
+    count = count if items is None else items
+    pairs = [synthetic_item(config, i, samples) for i in range(count)]
+    ref = np.stack([p[0] for p in pairs])
+    deg = np.stack([p[1] for p in pairs])
+    return ref, deg, fs
+
+
+def speech_like_pair(batch: int, samples: int, seed: int = 0, noise: float = 0.2,
+                     fricative: float = 0.3, fs: int = 16000):
+    """Harmonic stack plus a broadband component, and a noisy copy of it.
+
+    The test signal of the reference's end to end tests
+    (``tests/test_triton_loss.py:60-98``): eleven harmonics of 120 Hz with
+    random phases under a 3 Hz envelope, plus ``fricative`` times the envelope
+    times white noise, peak normalised; the degraded signal adds ``noise``
+    times white noise.  It has no digital silence, so no hard decision of the
+    perceptual model sits on a knife edge.
+    """
+
+    rng = np.random.default_rng(seed)
+    t = np.arange(samples) / fs
+    env = 0.5 + 0.5 * np.sin(2 * math.pi * 3.0 * t)
+    ref = np.zeros((batch, samples))
+    for k in range(1, 12):
+        phase = rng.uniform(0, 6.28, size=(batch, 1))
+        ref += np.sin(2 * math.pi * 120.0 * k * t + phase) / k * env
+    ref = ref + fricative * env * rng.standard_normal((batch, samples))
+    ref = ref / np.abs(ref).max(axis=1, keepdims=True)
+    deg = ref + noise * rng.standard_normal((batch, samples))
+    return ref.astype(np.float32), deg.astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# measurement
+# ---------------------------------------------------------------------------
+
+METRIC = "fwd+bwd ms/step & signals/s at B=8×8s 16kHz (1 GPU); % HBM roofline; err vs fp64"
+HBM_PEAK = 8.0e12  # MI355X HBM3E, bytes/s
+
+
+def model_bytes(batch: int, samples: int):
+    """Algorithmic bytes of the canonical stage model, per fused stage.
+
+    S = 2 B N 4 (both signals, float32), Kb = 2 B T 49 4 (both Bark spectra).
+    Forward: peak 2S, power IIR 2S, align 3S, ramp 2S, pre IIR 2S, STFT S+Kb,
+    chain Kb; backward: chain 2Kb, STFT 2S+Kb, pre IIR 2S, ramp 2S, align 5S,
+    power IIR + accumulate 3S, peak (deg half) S.  27 S + 5 Kb per step.
+    """
+
+    padded = samples + samples % 256
+    frames = 1 + (padded - 512) // 256
+    s = 2 * batch * samples * 4
+    kb = 2 * batch * frames * 49 * 4
+    return {
+        "fwd_scans": 11 * s,   # peak + power IIR + align + ramp + pre IIR
+        "fwd_stft": s + kb,
+        "fwd_chain": kb,
+        "bwd_chain": 2 * kb,
+        "bwd_stft": 2 * s + kb,
+        "bwd_scans": 13 * s,   # pre IIR + ramp + align + power IIR + peak
+    }, 27 * s + 5 * kb
+
+
+#: fused stage -> (pass, stage bits, kernel names)
+STAGES = {
+    "fwd_scans": ("fwd", 0x3, ["iir_aggregate_kernel<5,1,PipeFwdMode>", "iir_output_kernel<5,1,PipeFwdMode>"]),
+    "fwd_stft": ("fwd", 0x4, ["stft_fwd_kernel<double>"]),
+    "fwd_chain": ("fwd", 0x18, ["chain_fwd_kernel", "chain_final_kernel"]),
+    "bwd_chain": ("bwd", 0x1, ["chain_bwd_kernel"]),
+    "bwd_stft": ("bwd", 0x2, ["stft_bwd_kernel<double>"]),
+    "bwd_scans": ("bwd", 0xC, ["iir_aggregate_kernel<5,1,PipeBwdMode>", "iir_output_kernel<5,1,PipeBwdMode>"]),
+}
+
+
+def _stage_times(model, ref, deg, repeats: int = 50):
+    """Average device time of every fused stage, HIP events on the launch stream."""
+
+    import torch
+    from torch_pesq import _lib
+    from torch_pesq.hip_ops.pipeline import pipeline_backward, pipeline_forward
+
+    lib = _lib.library()
+    batch, length = ref.shape
+    mask = _lib.GRAD_DEG
+    g_loss = torch.ones(batch, device=ref.device)
+    out, ws = pipeline_forward(ref, deg, model.model_table, 1.0, mask)
+    bw_bytes = _lib.size_query(lib.pesq_pipeline_backward_workspace, batch, length, mask)
+    scratch = torch.empty(bw_bytes, dtype=torch.uint8, device=ref.device)
+    g_deg = torch.empty_like(deg)
+    stream = _lib.stream_handle(ref.device)
+
+    def run(pass_, bits):
+        if pass_ == "fwd":
+            status = lib.pesq_pipeline_forward_stages(
+                _lib.ptr(ref), _lib.ptr(deg), batch, length, _lib.ptr(model.model_table), 1.0,
+                mask, *[_lib.ptr(o) for o in out], _lib.ptr(ws), bits, stream)
+        else:
+            status = lib.pesq_pipeline_backward_stages(
+                None, None, None, _lib.ptr(g_loss), batch, length, _lib.ptr(model.model_table),
+                1.0, mask, None, _lib.ptr(g_deg), _lib.ptr(ws), _lib.ptr(scratch), bits, stream)
+        _lib.check(status, "stage")
+
+    run("fwd", 0x1F)
+    run("bwd", 0xF)
+    times = {}
+    for name, (pass_, bits, _) in STAGES.items():
+        for _ in range(3):
+            run(pass_, bits)
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(repeats):
+            run(pass_, bits)
+        stop.record()
+        torch.cuda.synchronize()
+        times[name] = start.elapsed_time(stop) / repeats * 1e-3  # seconds
+    return times
+
+
+def cpu_baseline(ref_np, deg_np, gpu_outputs, budget_s: float = 12.0):
+    """Float32 CPU restatement of the reference PesqLoss (``oracle/pesq_port.py``).
+
+    Timed on this host on the full c2 batch (forward + backward w.r.t. deg),
+    repeated for about ``budget_s`` seconds; also the float64 oracle as the
+    accuracy checker of the GPU outputs and of the CPU port.
+    """
+
+    import platform
+
+    import torch
+
+    from oracle import pesq_oracle, pesq_port
+
+    r = torch.from_numpy(ref_np)
+    d = torch.from_numpy(deg_np)
+
+    def step():
+        dd = d.clone().requires_grad_(True)
+        loss = pesq_port.loss(r, dd)
+        loss.sum().backward()
+
+    step()
+    samples, start = [], time.perf_counter()
+    while len(samples) < 3 or (time.perf_counter() - start < budget_s and len(samples) < 50):
+        t0 = time.perf_counter()
+        step()
+        samples.append(time.perf_counter() - t0)
+    per_step = statistics.median(samples)
+
+    ds, da = pesq_oracle.pipeline(r, d)
+    mos, _ = pesq_oracle.epilogue(ds, da, 1.0)
+    port_ds, port_da = pesq_port.raw(r, d)
+
+    def rel(got, want):
+        return float(((torch.as_tensor(got).double() - want).abs() / want.abs()).max())
+
+    errors = {
+        "d_symm": rel(gpu_outputs[0], ds),
+        "d_asymm": rel(gpu_outputs[1], da),
+        "mos": rel(gpu_outputs[2], mos),
+        "cpu_port_d_symm": rel(port_ds, ds),
+        "cpu_port_d_asymm": rel(port_da, da),
+    }
+    cpu_model = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    baseline = {
+        "value": ref_np.shape[0] / per_step,
+        "unit": "signals/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (
+            f"full c2 batch ({ref_np.shape[0]} x {ref_np.shape[1]} @16 kHz) fwd+bwd w.r.t. deg, "
+            f"median of {len(samples)} steps ({per_step * 1e3:.0f} ms/step); float32 torch-CPU "
+            f"restatement of PesqLoss with a C direct-form-I lfilter; host {cpu_model}, "
+            f"os.cpu_count()={os.cpu_count()}"
+        ),
+    }
+    return baseline, errors
+
+
+def main(argv=None):
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=100)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = parser.parse_args(argv)
+
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU: the PESQ loss shards by batch item with no "
+            f"communication, so --gpus {args.gpus} is not a configuration this build runs.",
+            file=sys.stderr,
+        )
+        return 2
+
+    sys.path.insert(0, str(PKG))
+    sys.path.insert(0, str(ROOT))
+    import torch
+
+    from torch_pesq import PesqLossTriton
+
+    ref_np, deg_np, fs = synthetic_config(2)
+    batch, samples = ref_np.shape
+    device = torch.device("cuda:0")
+    model = PesqLossTriton(1.0, sample_rate=fs).to(device)
+    ref = torch.from_numpy(ref_np).to(device)
+    deg = torch.from_numpy(deg_np).to(device).requires_grad_(True)
+
+    def eager_step():
+        loss = model(ref, deg)
+        torch.autograd.grad(loss.sum(), deg)
+
+    for _ in range(args.warmup):
+        eager_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eager_step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) / args.steps * 1e3
+
+    graph_deg = deg.detach().clone().requires_grad_(True)
+    graphed = model.graphed(ref, graph_deg)
+
+    def graph_step():
+        loss = graphed(ref, graph_deg)
+        torch.autograd.grad(loss.sum(), graph_deg)
+
+    for _ in range(args.warmup):
+        graph_step()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        graph_step()
+    stop.record()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / args.steps * 1e3
+    device_ms = start.elapsed_time(stop) / args.steps
+
+    with torch.no_grad():
+        outputs = [o.double().cpu() for o in model._run(ref, deg.detach())]
+
+    stage_s = _stage_times(model, ref, deg.detach())
+    per_stage, total_bytes = model_bytes(batch, samples)
+    stages = {
+        name: {
+            "us": round(stage_s[name] * 1e6, 2),
+            "model_bytes": per_stage[name],
+            "achieved_GBps": round(per_stage[name] / stage_s[name] / 1e9, 1),
+            "frac": round(per_stage[name] / stage_s[name] / HBM_PEAK, 4),
+            "kernels": STAGES[name][2],
+        }
+        for name in STAGES
+    }
+    dominant = max(stage_s, key=stage_s.get)
+    achieved = per_stage[dominant] / stage_s[dominant]
+    roofline = {
+        "bound": "hbm",
+        "achieved": round(achieved / 1e9, 1),
+        "peak": HBM_PEAK / 1e9,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK, 4),
+        "traffic": None,
+        "kernel": " + ".join(STAGES[dominant][2]),
+        "stage": dominant,
+        "model_bytes_per_launch": per_stage[dominant],
+        "avg_launch_us": round(stage_s[dominant] * 1e6, 2),
+    }
+
+    line = {
+        "metric": METRIC,
+        "value": round(batch / (ms / 1e3), 1),
+        "unit": "signals/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f64",
+        "data": "synthetic",
+        "config": {
+            "workload": "BASELINE c2: 8 x 8 s @16 kHz, PesqLossTriton forward+backward w.r.t. deg, HIP graph replay",
+            "batch": batch,
+            "samples": samples,
+            "sample_rate": fs,
+            "io_dtype": "float32",
+            "parallelism": "single GPU",
+        },
+        "eager_ms_per_step": round(eager_ms, 4),
+        "device_ms_per_step": round(device_ms, 4),
+        "step_model_bytes": total_bytes,
+        "step_hbm_frac": round(total_bytes / (ms / 1e3) / HBM_PEAK, 4),
+        "roofline": roofline,
+        "stages": stages,
+    }
+    if not args.no_cpu_baseline:
+        baseline, errors = cpu_baseline(ref_np, deg_np, outputs, args.cpu_seconds)
+        line["cpu_baseline"] = baseline
+        line["err_vs_fp64"] = errors
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

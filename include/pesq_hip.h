@@ -1,0 +1,203 @@
+/*
+ * pesq_hip.h -- C ABI of the MI355X (gfx950) PESQ loss library.
+ *
+ * Every entry point takes device pointers to contiguous row-major float32
+ * arrays, int64 sizes, a device pointer to a constant table built by one of
+ * the *_pack functions, caller-owned workspace (size from the matching
+ * *_workspace query) and an explicit hipStream_t.  Entry points enqueue work on
+ * that stream and return; they never allocate, synchronise or read device
+ * memory on the host, so they can be captured into a HIP graph.  Reductions
+ * use a fixed order and no atomics: results are bitwise reproducible.
+ *
+ * Return value: PESQ_OK (0) or an error code; pesq_last_error() describes the
+ * last failure of the calling thread.
+ *
+ * Each function replaces the reference operator named in its comment
+ * (paths relative to the LarocheC/triton-pesq source tree).
+ */
+#ifndef PESQ_HIP_H
+#define PESQ_HIP_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PESQ_OK 0
+#define PESQ_ERR_ARGUMENT 1
+#define PESQ_ERR_HIP 2
+#define PESQ_ERR_UNSUPPORTED 3
+
+#define PESQ_IIR_MAX_SECTIONS 8
+#define PESQ_NBARKS 49
+#define PESQ_NFFT 512
+
+/* bit flags of the pipeline's grad_mask */
+#define PESQ_GRAD_REF 1
+#define PESQ_GRAD_DEG 2
+
+/* ----------------------------------------------------------------------- */
+/* library                                                                  */
+/* ----------------------------------------------------------------------- */
+
+/* Version of this ABI (incremented on any signature or layout change). */
+int pesq_abi_version(void);
+
+/* Message of the last error on the calling thread ("" if none). */
+const char *pesq_last_error(void);
+
+/* ----------------------------------------------------------------------- */
+/* constant tables (host side, no GPU call)                                 */
+/* ----------------------------------------------------------------------- */
+
+/* A causal IIR filter in parallel form: y = c0 x + sum_k s_k(x), section k a
+ * direct form II transposed biquad (b0[k] + b1[k] z^-1 + b2[k] z^-2) /
+ * (1 + a1[k] z^-1 + a2[k] z^-2) with zero initial state. */
+typedef struct pesq_iir_sections {
+    int32_t count; /* 1 .. PESQ_IIR_MAX_SECTIONS */
+    int32_t reserved;
+    double c0;
+    double b0[PESQ_IIR_MAX_SECTIONS];
+    double b1[PESQ_IIR_MAX_SECTIONS];
+    double b2[PESQ_IIR_MAX_SECTIONS];
+    double a1[PESQ_IIR_MAX_SECTIONS];
+    double a2[PESQ_IIR_MAX_SECTIONS];
+} pesq_iir_sections;
+
+/* Size in bytes of a packed IIR table. */
+size_t pesq_iir_table_bytes(void);
+
+/* Pack one filter into `out` (host memory, pesq_iir_table_bytes() bytes),
+ * including the chunk transfer powers of the scan.  Replaces the host side
+ * design of TritonIIR: torch_pesq/triton_ops/iir.py:520-667 (_state_space,
+ * _tables). */
+int pesq_iir_table_pack(const pesq_iir_sections *filter, void *out);
+
+/* Constants of the PESQ model (PesqLoss.__init__, torch_pesq/loss.py:61-108;
+ * BarkScale, torch_pesq/bark.py:131-173; Loudness, torch_pesq/loudness.py:44-55). */
+typedef struct pesq_model_constants {
+    pesq_iir_sections power_filter; /* level alignment band pass, loss.py:96-99 */
+    pesq_iir_sections pre_filter;   /* pre-emphasis, loss.py:102-108 */
+    float window[PESQ_NFFT];        /* analysis window (n_fft taps, centred) */
+    int32_t band_start[PESQ_NBARKS];/* Bark band i covers bins [start, end) */
+    int32_t band_end[PESQ_NBARKS];
+    double corr[PESQ_NBARKS];       /* pow_dens_correction */
+    double threshs[PESQ_NBARKS];    /* hearing thresholds */
+    double exps[PESQ_NBARKS];       /* Zwicker exponents */
+    double width[PESQ_NBARKS];      /* width_bark */
+    double total_width;             /* width_bark[1:].sum() */
+    double sl;                      /* loudness constant (0.1866055) */
+    int32_t nbarks;                 /* must be 49 */
+    int32_t n_fft;                  /* must be 512 */
+    int32_t hop;                    /* must be 256 */
+    int32_t reserved;
+} pesq_model_constants;
+
+/* Size in bytes of a packed model table. */
+size_t pesq_model_table_bytes(void);
+
+/* Pack the model constants into `out` (host memory, pesq_model_table_bytes()).
+ * Replaces the buffers registered by PesqLossTriton.__init__
+ * (torch_pesq/triton_ops/loss.py:60-92), TritonStftBark.__init__
+ * (spectral.py:634-734) and TritonPesqChain.__init__ (chain.py:1057-1078). */
+int pesq_model_table_pack(const pesq_model_constants *constants, void *out);
+
+/* ----------------------------------------------------------------------- */
+/* fused pipeline: PesqLossTriton.raw / mos / forward and their backward    */
+/* ----------------------------------------------------------------------- */
+
+/* Workspace of the forward pass.  It holds the state the backward reads and
+ * must stay untouched between pesq_pipeline_forward and
+ * pesq_pipeline_backward.  `len` is the 16 kHz row length. */
+int pesq_pipeline_forward_workspace(int64_t batch, int64_t len, int grad_mask, size_t *bytes);
+
+/* Scratch of the backward pass (free after the call has run). */
+int pesq_pipeline_backward_workspace(int64_t batch, int64_t len, int grad_mask, size_t *bytes);
+
+/* Distances, MOS and loss of `batch` pairs of 16 kHz signals [batch, len].
+ * Replaces PesqLossTriton.raw / mos / forward
+ * (torch_pesq/triton_ops/loss.py:104-147,203-215): peak normalisation,
+ * level alignment, pre-emphasis, STFT, Bark, perceptual chain and the MOS
+ * epilogue, in five kernels.  grad_mask (PESQ_GRAD_*) selects which inputs
+ * the backward will need; it must match the backward call.  Requires
+ * len >= 15 and at least 20 frames (1 + (len + len % 256 - 512) / 256). */
+int pesq_pipeline_forward(const float *ref, const float *deg, int64_t batch, int64_t len,
+                          const void *model_table, double factor, int grad_mask,
+                          float *d_symm, float *d_asymm, float *mos, float *loss,
+                          void *fwd_workspace, hipStream_t stream);
+
+/* Gradients w.r.t. ref and/or deg given the upstream gradients of any of the
+ * four outputs (NULL = zero).  g_ref / g_deg may be NULL when not requested
+ * by grad_mask.  Replaces the chain of backward kernels run by autograd
+ * through PesqLossTriton (torch_pesq/triton_ops/chain.py:780-1021,
+ * spectral.py:535-581, elementwise.py:233-269,607-652, iir.py:1248-1258). */
+int pesq_pipeline_backward(const float *g_symm, const float *g_asymm, const float *g_mos,
+                           const float *g_loss, int64_t batch, int64_t len,
+                           const void *model_table, double factor, int grad_mask,
+                           float *g_ref, float *g_deg, const void *fwd_workspace,
+                           void *bwd_workspace, hipStream_t stream);
+
+/* The same two passes restricted to a subset of their kernels, for per stage
+ * timing.  Forward bits: 1 scan aggregates, 2 scan outputs, 4 STFT/Bark,
+ * 8 chain, 16 overlapping sums + epilogue.  Backward bits: 1 chain, 2 STFT,
+ * 4 adjoint scan aggregates, 8 adjoint scan outputs.  A stage reads what the
+ * earlier stages wrote into the workspaces, so run the full pass first.  No
+ * counterpart in the reference (its stages are separate launches). */
+int pesq_pipeline_forward_stages(const float *ref, const float *deg, int64_t batch, int64_t len,
+                                 const void *model_table, double factor, int grad_mask,
+                                 float *d_symm, float *d_asymm, float *mos, float *loss,
+                                 void *fwd_workspace, unsigned stages, hipStream_t stream);
+int pesq_pipeline_backward_stages(const float *g_symm, const float *g_asymm, const float *g_mos,
+                                  const float *g_loss, int64_t batch, int64_t len,
+                                  const void *model_table, double factor, int grad_mask,
+                                  float *g_ref, float *g_deg, const void *fwd_workspace,
+                                  void *bwd_workspace, unsigned stages, hipStream_t stream);
+
+/* Byte offset and size of a named region of the forward workspace ("p",
+ * "f", "bark", "rowconst", ...), for inspection by tests.  Returns
+ * PESQ_ERR_ARGUMENT for an unknown name. */
+int pesq_pipeline_region(int64_t batch, int64_t len, int grad_mask, const char *name,
+                         size_t *offset, size_t *bytes);
+
+/* ----------------------------------------------------------------------- */
+/* IIR filter (TritonIIR, torch_pesq/triton_ops/iir.py:1266-1482)           */
+/* ----------------------------------------------------------------------- */
+
+int pesq_iir_workspace(int64_t rows, int64_t len, size_t *bytes);
+
+/* y = lfilter(x) along rows, zero initial state; reverse != 0 applies the
+ * time reversed filter, the adjoint (iir.py:1232-1258).  `sections` is the
+ * count of the packed filter (pesq_iir_sections.count). */
+int pesq_iir_apply(const float *x, float *y, int64_t rows, int64_t len, const void *iir_table,
+                   int sections, int reverse, void *workspace, hipStream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* resampler (TritonResample, torch_pesq/triton_ops/resample.py:442-574)    */
+/* ----------------------------------------------------------------------- */
+
+/* y[l new_step + j] = sum_k kernel[j, k] x[l orig_step + k - width] for the
+ * non-zero taps tap_lo[j] <= k < tap_hi[j] of each phase ([new_step] int32
+ * each); kernel is [new_step, width_total] float32, width_total =
+ * 2 width + orig_step; x reads as zero outside [0, n_in).  Replaces
+ * _resample_fwd_kernel (resample.py:113-175). */
+int pesq_resample_forward(const float *x, float *y, int64_t rows, int64_t n_in, int64_t n_out,
+                          const float *kernel, const int32_t *tap_lo, const int32_t *tap_hi,
+                          int64_t orig_step, int64_t new_step, int64_t width,
+                          int64_t width_total, hipStream_t stream);
+
+/* Adjoint of pesq_resample_forward, a gather over input samples; phase_lo /
+ * phase_hi ([width_total] int32) bound the phases with a non-zero tap k.
+ * Replaces _resample_bwd_kernel (resample.py:178-243). */
+int pesq_resample_backward(const float *grad_y, float *grad_x, int64_t rows, int64_t n_in,
+                           int64_t n_out, const float *kernel, const int32_t *phase_lo,
+                           const int32_t *phase_hi, int64_t orig_step, int64_t new_step,
+                           int64_t width, int64_t width_total, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PESQ_HIP_H */

@@ -1,0 +1,162 @@
+"""CPU checks of the C ABI library and of the host side of the package.
+
+No kernel is launched here: the library must load, export every entry point
+``include/pesq_hip.h`` declares, pack its constant tables, and reject invalid
+arguments before touching a GPU.
+"""
+
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+from scipy.signal import butter, lfilter
+
+from torch_pesq import BarkScale, Loudness, PesqLoss, _lib
+from torch_pesq import bark as bark_mod
+from torch_pesq import loudness as loud_mod
+from torch_pesq.hip_ops.iir import parallel_sections
+
+ROOT = Path(__file__).resolve().parents[1]
+TABLES = json.loads((ROOT / "tests" / "golden" / "tables.json").read_text())
+
+
+def _declared_symbols():
+    header = (ROOT / "include" / "pesq_hip.h").read_text()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(pesq_\w+)\s*\(", header, re.M)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.library()
+    declared = _declared_symbols()
+    assert len(declared) >= 15
+    for name in declared:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.pesq_abi_version() >= 1
+
+
+def test_product_tables_match_golden():
+    for key in (
+        "nr_of_hz_bands_per_bark_band_16k",
+        "centre_of_band_bark_16k",
+        "centre_of_band_hz_16k",
+        "width_of_band_bark_16k",
+        "width_of_band_hz_16k",
+        "pow_dens_correction_factor_16k",
+    ):
+        assert list(getattr(bark_mod, key)) == TABLES[key], key
+    assert bark_mod.Sp_16k == TABLES["Sp_16k"]
+    assert list(loud_mod.abs_thresh_power_16k) == TABLES["abs_thresh_power_16k"]
+    assert loud_mod.zwicker_power == TABLES["zwicker_power"]
+    assert loud_mod.Sl_16k == TABLES["Sl_16k"]
+
+
+def test_fbank_known_answer():
+    # tests/test_fbank.py:5-11 of the reference
+    fb = BarkScale()
+    assert torch.all(fb.fbank.sum(dim=1) == torch.tensor(bark_mod.nr_of_hz_bands_per_bark_band_16k))
+    assert torch.all(fb.fbank.sum(dim=0) == 1.0)
+    assert fb.pow_dens_correction.dtype == torch.float64
+    assert Loudness().exp.dtype == torch.float32
+
+
+def test_model_matches_oracle_constants():
+    from oracle import pesq_oracle as O
+
+    c = O.constants()
+    m = PesqLoss(1.0, sample_rate=16000)
+    assert torch.equal(m.power_filter.double(), torch.stack([c["power_b"], c["power_a"]]))
+    assert torch.equal(m.pre_filter.double(), torch.stack([c["pre_b"], c["pre_a"]]))
+    assert torch.equal(m.to_spec.window.double(), c["window"])
+    assert torch.equal(m.fbank.fbank.double(), c["fbank"])
+    assert torch.equal(m.fbank.pow_dens_correction, c["corr"])
+    assert torch.equal(m.loudness.threshs.flatten(), c["threshs"])
+    assert torch.equal(m.loudness.exp.double(), c["exp"])
+    assert float(m.fbank.total_width) == float(c["total_width"])
+
+
+@pytest.mark.parametrize(
+    "b,a",
+    [
+        butter(5, [325, 3250], fs=16000, btype="band"),
+        ([2.740826, -5.4816519, 2.740826], [1.0, -1.9444777, 0.94597794]),
+        butter(4, 0.2),
+        butter(3, [0.1, 0.4], btype="bandstop"),
+        ([0.5, 0.1], [1.0, -0.9]),
+        butter(8, 0.3),
+    ],
+)
+def test_parallel_realisation_reproduces_lfilter(b, a):
+    c0, secs = parallel_sections(b, a)
+    x = np.random.default_rng(0).standard_normal(5000)
+    want = lfilter(b, a, x)
+    got = c0 * x + sum(lfilter([s[0], s[1], s[2]], [1.0, s[3], s[4]], x) for s in secs)
+    assert np.abs(got - want).max() <= 1e-9 * np.abs(want).max()
+    assert len(secs) == (len(np.trim_zeros(np.asarray(a, float), "b")) - 1 + 1) // 2
+
+
+def test_parallel_realisation_rejects_repeated_poles():
+    # (1 - 0.5 z^-1)^-3: a triple real pole has no parallel first/second order form
+    a = np.poly([0.5, 0.5, 0.5])
+    with pytest.raises(RuntimeError):
+        parallel_sections([1.0], a)
+
+
+def test_iir_table_pack_validates():
+    lib = _lib.library()
+    s = _lib.IirSections()
+    s.count = 0
+    buf = (ctypes.c_ubyte * lib.pesq_iir_table_bytes())()
+    assert lib.pesq_iir_table_pack(ctypes.byref(s), buf) != 0
+    assert b"sections" in lib.pesq_last_error()
+    s.count = 1
+    s.b0[0], s.a1[0], s.a2[0] = 1.0, -0.5, 0.0
+    assert lib.pesq_iir_table_pack(ctypes.byref(s), buf) == 0
+
+
+def test_pipeline_workspace_queries_validate():
+    lib = _lib.library()
+    size = ctypes.c_size_t(0)
+    assert lib.pesq_pipeline_forward_workspace(8, 128000, 2, ctypes.byref(size)) == 0
+    assert size.value > 8 * 128000 * 2 * 4
+    # fewer than 20 frames
+    assert lib.pesq_pipeline_forward_workspace(1, 4000, 0, ctypes.byref(size)) != 0
+    assert b"20 frames" in lib.pesq_last_error()
+    assert lib.pesq_pipeline_forward_workspace(0, 16000, 0, ctypes.byref(size)) != 0
+    off, nbytes = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    assert lib.pesq_pipeline_region(2, 16000, 2, b"bark", ctypes.byref(off), ctypes.byref(nbytes)) == 0
+    assert nbytes.value >= 4 * 62 * 49 * 4
+    assert lib.pesq_pipeline_region(2, 16000, 2, b"nope", ctypes.byref(off), ctypes.byref(nbytes)) != 0
+
+
+def test_model_table_pack_rejects_bad_bands():
+    from torch_pesq.hip_ops.pipeline import pack_model_table
+
+    m = PesqLoss(1.0, sample_rate=16000)
+    fb = m.fbank.fbank.clone()
+    fb[3, 0] = 1.0  # band 3 reaches back into band 0's bin
+    with pytest.raises(ValueError):
+        pack_model_table(m.power_filter[0], m.power_filter[1], m.pre_filter[0], m.pre_filter[1],
+                         m.to_spec.window, fb, m.fbank.pow_dens_correction, m.loudness.threshs,
+                         m.loudness.exp, m.fbank.width_bark, m.fbank.total_width, 0.1866055)
+
+
+def test_cpu_inputs_and_bad_shapes_raise():
+    m = PesqLoss(1.0, sample_rate=16000)
+    ref = torch.zeros(2, 16000)
+    with pytest.raises(RuntimeError):
+        m(ref, ref)
+    with pytest.raises(ValueError):
+        m(ref, torch.zeros(2, 15000))
+    with pytest.raises(NotImplementedError):
+        PesqLoss(1.0, nbarks=32)
+
+
+def test_graft_entry_exposes_build_and_smoke():
+    import __graft_entry__ as entry
+
+    assert callable(entry.build) and callable(entry.smoke)

@@ -1,0 +1,295 @@
+"""Pins of the float64 CPU oracle (``oracle/pesq_oracle.py``).
+
+Each check is chosen so that a plausible mistake in the restatement (a wrong
+table entry, a dropped term, a wrong sign or index, a transposed operand)
+fails: known answers of the reference's own tests, closed forms, brute force
+evaluations on tiny inputs and finite differences.
+"""
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+from scipy.signal import butter, sosfilt, tf2sos
+
+from oracle import pesq_oracle as O
+
+TABLES = json.loads((Path(__file__).parent / "golden" / "tables.json").read_text())
+
+
+def test_tables_match_golden():
+    c = O.constants()
+    counts = TABLES["nr_of_hz_bands_per_bark_band_16k"]
+    assert sum(counts) == 256
+    # tests/test_fbank.py:5-11: every bin in exactly one band, band sizes as tabled
+    assert torch.equal(c["fbank"].sum(0), torch.ones(256, dtype=torch.float64))
+    assert torch.equal(c["fbank"].sum(1), torch.tensor(counts, dtype=torch.float64))
+    np.testing.assert_array_equal(c["threshs"].numpy(), np.array(TABLES["abs_thresh_power_16k"]))
+    np.testing.assert_array_equal(c["width_bark"].numpy(), np.array(TABLES["width_of_band_bark_16k"]))
+    np.testing.assert_allclose(
+        c["corr"].numpy(),
+        np.array(TABLES["pow_dens_correction_factor_16k"]) * TABLES["Sp_16k"],
+        rtol=1e-15,
+    )
+    # Zwicker exponents: clamp(6 / (c + 2), 1, 2)^0.15 * 0.23, float32 values
+    centre = np.array(TABLES["centre_of_band_bark_16k"])
+    want = np.clip(6 / (centre + 2), 1, 2) ** 0.15 * 0.23
+    np.testing.assert_allclose(c["exp"].numpy(), want, rtol=1e-6)
+    assert c["exp"].float().double().equal(c["exp"])
+
+
+def test_power_filter_is_the_float32_butterworth():
+    c = O.constants()
+    b, a = butter(5, [325, 3250], fs=16000, btype="band")
+    assert c["power_b"].numel() == 11 and c["power_a"].numel() == 11
+    np.testing.assert_array_equal(c["power_b"].numpy(), np.float32(b).astype(np.float64))
+    np.testing.assert_array_equal(c["power_a"].numpy(), np.float32(a).astype(np.float64))
+
+
+def _recursion(x, b, a):
+    """Textbook difference equation, pure Python, zero initial state."""
+
+    y = np.zeros_like(x)
+    for n in range(len(x)):
+        acc = sum(b[k] * x[n - k] for k in range(len(b)) if n - k >= 0)
+        acc -= sum(a[k] * y[n - k] for k in range(1, len(a)) if n - k >= 0)
+        y[n] = acc / a[0]
+    return y
+
+
+@pytest.mark.parametrize("which", ["power", "pre"])
+def test_lfilter_matches_difference_equation(which):
+    c = O.constants()
+    b, a = c[f"{which}_b"].numpy(), c[f"{which}_a"].numpy()
+    x = np.random.default_rng(0).standard_normal(300)
+    want = _recursion(x, b, a)
+    got = O.lfilter64(x[None], b, a)[0]
+    assert np.abs(got - want).max() <= 1e-9 * np.abs(want).max()
+    # second order sections of the same filter agree too
+    np.testing.assert_allclose(sosfilt(tf2sos(b, a), x), want, rtol=0, atol=1e-9 * np.abs(want).max())
+
+
+def test_lfilter_adjoint_is_time_reversed_filter():
+    c = O.constants()
+    rng = np.random.default_rng(1)
+    x, y = rng.standard_normal(4000), rng.standard_normal(4000)
+    b, a = c["power_b"].numpy(), c["power_a"].numpy()
+    lhs = float(np.dot(y, O.lfilter64(x[None], b, a)[0]))
+    rhs = float(np.dot(O.lfilter64(y[None], b, a, reverse=True)[0], x))
+    # the order 10 direct form itself carries ~1e-10 of float64 rounding
+    assert abs(lhs - rhs) <= 1e-8 * (abs(lhs) + 1e-30)
+    # and a wrong "adjoint" (the forward filter itself) does not pass
+    wrong = float(np.dot(O.lfilter64(y[None], b, a)[0], x))
+    assert abs(lhs - wrong) > 1e-3 * abs(lhs)
+
+
+def test_frame_count_known_answers():
+    # triton_ops/loss.py:142 pads by N % 256: 128000 -> 499 frames
+    assert O.n_frames(128000) == 499
+    assert O.n_frames(16000) == 62
+    assert O.n_frames(960000) == 3749
+    assert O.n_frames(64000) == 249
+    # 20000 samples pad by 32 -> 20032 -> 77 frames
+    assert O.n_frames(20000) == 77
+
+
+def test_stft_bark_matches_direct_dft():
+    c = O.constants()
+    rng = np.random.default_rng(2)
+    x = torch.from_numpy(rng.standard_normal((2, 1024)))
+    got = O.stft_bark(x, c)
+    w = c["window"].numpy()
+    k = np.arange(512)
+    frames = [x.numpy()[:, 256 * t : 256 * t + 512] * w for t in range(3)]
+    power = np.stack([np.abs(f @ np.exp(-2j * np.pi * np.outer(k, np.arange(257)) / 512)) ** 2 for f in frames], 1)
+    power[:, :, 0] = 0.0
+    want = power[:, :, :256] @ c["fbank"].numpy().T * c["corr"].numpy()
+    assert got.shape == (2, 3, 49)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-10, atol=1e-12 * np.abs(want).max())
+    # band 0 is the DC bin alone, which is dropped
+    assert torch.all(got[:, :, 0] == 0)
+
+
+def test_stft_bark_gradient_finite_difference():
+    c = O.constants()
+    x = torch.randn(1, 768, dtype=torch.float64, generator=torch.Generator().manual_seed(3))
+    w = torch.randn(1, 2, 49, dtype=torch.float64, generator=torch.Generator().manual_seed(4))
+    x.requires_grad_(True)
+    (O.stft_bark(x, c) * w).sum().backward()
+    for n in (5, 300, 511, 700):
+        e = torch.zeros_like(x)
+        e[0, n] = 1e-6
+        with torch.no_grad():
+            fd = ((O.stft_bark(x + e, c) - O.stft_bark(x - e, c)) * w).sum() / 2e-6
+        assert abs(float(fd) - float(x.grad[0, n])) <= 1e-6 * max(1.0, abs(float(fd)))
+
+
+def test_chain_identical_inputs_floor():
+    # test_triton_chain.py:365-383: ref == deg gives the 1e-20 floor divided by h
+    c = O.constants()
+    g = torch.Generator().manual_seed(5)
+    ref = c["threshs"] * 10 ** (torch.rand(1, 40, 1, generator=g, dtype=torch.float64) * 6) * (
+        0.2 + 2 * torch.rand(1, 40, 49, generator=g, dtype=torch.float64)
+    )
+    ds, da = O.chain(ref, ref.clone(), c)
+    assert float(ds) < 1e-19 and float(da) < 1e-19
+    symm, _ = O.frame_distances(ref, ref.clone(), c)
+    taer = (ref * (ref > c["threshs"])).sum(2)  # band ratio is 1 for identical inputs
+    h = ((taer + 1e5) / 1e7) ** 0.04
+    torch.testing.assert_close(symm, (1e-20 / h), rtol=1e-12, atol=0)
+
+
+def _chain_loops(ref, deg, c):
+    """The chain with explicit loops over frames and bands (tiny inputs only)."""
+
+    th, ex, wb = c["threshs"].tolist(), c["exp"].tolist(), c["width_bark"].tolist()
+    tw = float(c["total_width"])
+    T, K = len(ref), len(ref[0])
+    silent = [sum(v for k, v in enumerate(ref[t]) if v > 100 * th[k]) < 1e7 for t in range(T)]
+    mr = [sum(ref[t][k] for t in range(T) if not silent[t] and ref[t][k] > 100 * th[k]) / T for k in range(K)]
+    md = [sum(deg[t][k] for t in range(T) if not silent[t] and deg[t][k] > 100 * th[k]) / T for k in range(K)]
+    r = [min(max((md[k] + 1000) / (mr[k] + 1000), 0.01), 100.0) for k in range(K)]
+    er = [[r[k] * ref[t][k] for k in range(K)] for t in range(T)]
+    taer = [sum(v for k, v in enumerate(er[t]) if v > th[k]) for t in range(T)]
+    tad = [sum(v for k, v in enumerate(deg[t]) if v > th[k]) for t in range(T)]
+    f0 = [(taer[t] + 5e3) / (tad[t] + 5e3) for t in range(T)]
+    f1 = [f0[0]] + [0.8 * f0[t] + 0.2 * f0[t - 1] for t in range(1, T)]
+    fpr = [min(max(v, 3e-4), 5.0) for v in f1]
+
+    def loud(x, k):
+        return 0.0 if x <= th[k] else (2 * th[k]) ** ex[k] * ((0.5 + 0.5 * x / th[k]) ** ex[k] - 1) * O.SL
+
+    out_s, out_a = [], []
+    for t in range(T):
+        s2 = a1 = 0.0
+        for k in range(1, K):
+            ed = fpr[t] * deg[t][k]
+            ld, lr = loud(ed, k), loud(er[t][k], k)
+            u = ld - lr
+            dist = math.copysign(1.0, u) * max(abs(u) - 0.25 * min(ld, lr), 0.0) if u != 0 else 0.0
+            s2 += (wb[k] * dist) ** 2 / tw
+            asc = ((ed + 50) / (er[t][k] + 50)) ** 1.2
+            asc = 0.0 if asc < 3 else min(asc, 12.0)
+            a1 += abs(wb[k] * dist * asc / tw)
+        h = ((taer[t] + 1e5) / 1e7) ** 0.04
+        out_s.append(min(max(tw * math.sqrt(s2), 1e-20) / h, 45.0))
+        out_a.append(min(max(tw * a1, 1e-20) / h, 45.0))
+
+    def sums(v):
+        nwin = (T - 20) // 10 + 1
+        p = [(sum(v[10 * l + j] ** 6 for j in range(20)) / 20) ** (1 / 6) for l in range(nwin)]
+        return math.sqrt(sum(q * q for q in p) / nwin)
+
+    return sums(out_s), sums(out_a)
+
+
+def test_chain_matches_loop_evaluation():
+    c = O.constants()
+    g = torch.Generator().manual_seed(6)
+    level = 10 ** (torch.rand(1, 31, 1, generator=g, dtype=torch.float64) * 6)
+    ref = c["threshs"] * level * (0.2 + 2 * torch.rand(1, 31, 49, generator=g, dtype=torch.float64))
+    deg = ref * 10 ** ((torch.rand(1, 31, 49, generator=g, dtype=torch.float64) - 0.5))
+    ds, da = O.chain(ref, deg, c)
+    ws, wa = _chain_loops(ref[0].tolist(), deg[0].tolist(), c)
+    assert abs(float(ds) - ws) <= 1e-12 * ws and abs(float(da) - wa) <= 1e-12 * wa
+
+
+def test_chain_gradient_finite_difference():
+    c = O.constants()
+    g = torch.Generator().manual_seed(7)
+    level = 10 ** (torch.rand(1, 30, 1, generator=g, dtype=torch.float64) * 5 + 1)
+    ref = c["threshs"] * level * (0.5 + torch.rand(1, 30, 49, generator=g, dtype=torch.float64))
+    deg = (ref * 10 ** ((torch.rand(1, 30, 49, generator=g, dtype=torch.float64) - 0.5) * 0.6)).requires_grad_(True)
+    ds, da = O.chain(ref, deg, c)
+    (0.7 * ds + 0.3 * da).sum().backward()
+    flat = deg.grad.flatten()
+    for idx in torch.topk(flat.abs(), 4).indices.tolist():
+        e = torch.zeros_like(flat)
+        e[idx] = 1e-7 * abs(float(deg.detach().flatten()[idx]))
+        e = e.view_as(deg)
+        with torch.no_grad():
+            hi = O.chain(ref, deg + e, c)
+            lo = O.chain(ref, deg - e, c)
+        fd = (0.7 * (hi[0] - lo[0]) + 0.3 * (hi[1] - lo[1])).sum() / (2 * float(e.flatten()[idx]))
+        assert abs(float(fd) - float(flat[idx])) <= 1e-4 * abs(float(flat[idx]))
+
+
+def test_epilogue_closed_form():
+    ds = torch.tensor([0.0, 10.0, 40.0], dtype=torch.float64)
+    da = torch.tensor([0.0, 20.0, 45.0], dtype=torch.float64)
+    mos, loss = O.epilogue(ds, da, 0.5)
+    inner = 4.5 - 0.1 * ds - 0.0309 * da
+    torch.testing.assert_close(mos, 0.999 + 4 / (1 + torch.exp(-1.3669 * inner + 3.8224)))
+    torch.testing.assert_close(loss, 0.5 * (0.1 * ds + 0.0309 * da))
+    assert float(mos[0]) < 4.999 and float(mos[2]) > 1.0
+
+
+def _signals(batch, n, seed):
+    from bench import speech_like_pair
+
+    ref, deg = speech_like_pair(batch, n, seed=seed, noise=0.1)
+    return torch.from_numpy(ref).double(), torch.from_numpy(deg).double()
+
+
+def test_pipeline_scale_invariance_and_batch_independence():
+    ref, deg = _signals(3, 8000, 8)
+    ds, da = O.pipeline(ref, deg)
+    ds2, da2 = O.pipeline(ref * 7.5, deg * 1e-3)
+    torch.testing.assert_close(ds2, ds, rtol=1e-9, atol=0)
+    torch.testing.assert_close(da2, da, rtol=1e-9, atol=0)
+    one = O.pipeline(ref[1:2], deg[1:2])
+    assert abs(float(one[0]) - float(ds[1])) <= 1e-12 * float(ds[1])
+
+
+def test_pipeline_identical_signals_zero_loss():
+    # test_torch.py:18-27: loss(ref, ref) <= 1e-20 (here: the floor / h)
+    ref, _ = _signals(2, 8000, 9)
+    ds, da = O.pipeline(ref, ref.clone())
+    _, loss = O.epilogue(ds, da, 1.0)
+    assert torch.all(loss < 1e-19) and torch.all(loss > 0)
+
+
+@pytest.mark.parametrize(
+    "orig,new,width,total",
+    # width_total known answers of test_triton_resample.py:13,177-181,685-686
+    [(44100, 16000, 17, 475), (48000, 16000, 19, 41), (8000, 16000, 7, 15)],
+)
+def test_resample_kernel_shape_known_answers(orig, new, width, total):
+    kernel, w = O.sinc_resample_kernel(orig, new)
+    g = math.gcd(orig, new)
+    assert w == width and kernel.shape == (new // g, total)
+    assert kernel.dtype == torch.float32
+
+
+@pytest.mark.parametrize("orig,new", [(44100, 16000), (48000, 16000), (8000, 16000)])
+def test_resample_kernel_properties(orig, new):
+    kernel, width = O.sinc_resample_kernel(orig, new)
+    k = kernel.double()
+    # DC gain: every phase of a low pass interpolator sums to ~1 (rolloff 0.99 + window)
+    assert torch.all((k.sum(1) - 1).abs() < 2e-3)
+    # phase 0 is symmetric about the tap at offset `width`
+    phase0 = k[0]
+    g = math.gcd(orig, new)
+    centre = width
+    half = min(centre, phase0.shape[0] - 1 - centre)
+    torch.testing.assert_close(phase0[centre - half : centre], phase0[centre + 1 : centre + half + 1].flip(0), rtol=0, atol=1e-6)
+    assert float(phase0[centre]) == pytest.approx(min(orig, new) // g * 0.99 / (orig // g), rel=1e-6)
+
+
+def test_resample_lengths_and_identity():
+    # output length = float32 ceil of new * n / orig (test_triton_resample.py:620-647)
+    assert O.resample_length(176400, 44100, 16000) == 64000
+    assert O.resample_length(192000, 48000, 16000) == 64000
+    assert O.resample_length(1000, 48000, 16000) == 334
+    assert O.resample_length(0, 48000, 16000) == 0
+    x = torch.randn(2, 100, dtype=torch.float64)
+    assert O.resample(x, 16000) is x
+    # a pure tone below the cut-off survives 48 -> 16 kHz resampling
+    t = torch.arange(48000, dtype=torch.float64) / 48000
+    tone = torch.sin(2 * math.pi * 1000 * t)[None]
+    out = O.resample(tone, 48000)
+    want = torch.sin(2 * math.pi * 1000 * torch.arange(16000, dtype=torch.float64) / 16000)
+    assert (out[0, 200:-200] - want[200:-200]).abs().max() < 2e-3

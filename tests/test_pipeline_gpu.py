@@ -1,0 +1,261 @@
+"""GPU parity of the fused PESQ pipeline against the float64 oracle.
+
+Mirrors the reference's end to end suite (``tests/test_triton_loss.py``):
+distances/MOS/loss against a float64 evaluation of the same pipeline, the
+gradients, determinism, batch independence, HIP graph bit exactness, the
+identical-input and range invariants, strided / 1-d inputs and the error
+conventions.
+
+Tolerances (all relative):
+
+* distances, MOS, loss vs float64: ``F64_RTOL = 1e-5``;
+  measured ~5e-8 on every signal here.
+* gradients vs float64 on signals without digital silence: ``GRAD_RTOL =
+  2e-5`` of the largest gradient magnitude; measured ~1e-6.
+* the degraded-signal gradient on the BASELINE c2 generator: ``1e-4``;
+  measured ~4e-6.  The *reference* gradient of that generator is not compared
+  element wise: its references contain long runs of exact digital silence
+  where the loss has kinks and jumps within 1e-5 of the input (even the
+  float64 oracle's own finite differences disagree with its autograd there),
+  so element wise agreement is not a property of any float32 implementation.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from bench import speech_like_pair, synthetic_config
+from oracle import pesq_oracle as O
+from torch_pesq import PesqLossTriton
+from torch_pesq.hip_ops.pipeline import pipeline_forward, pipeline_region
+
+pytestmark = pytest.mark.gpu
+
+F64_RTOL = 1e-5
+GRAD_RTOL = 2e-5
+
+
+@pytest.fixture(scope="module")
+def model():
+    return PesqLossTriton(0.5, sample_rate=16000).cuda()
+
+
+def _rel(got, want):
+    got = torch.as_tensor(got).detach().double().cpu()
+    want = torch.as_tensor(want).detach().double().cpu()
+    return float(((got - want).abs() / want.abs().clamp(min=1e-30)).max())
+
+
+def _oracle(ref, deg, factor=0.5):
+    ds, da = O.pipeline(torch.from_numpy(ref), torch.from_numpy(deg))
+    mos, loss = O.epilogue(ds, da, factor)
+    return ds, da, mos, loss
+
+
+@pytest.mark.parametrize(
+    "batch,samples,seed",
+    [(1, 16000, 0), (3, 20000, 1), (2, 32000, 2), (4, 5376, 3), (2, 5400, 4)],
+)
+def test_matches_float64_speech_like(model, batch, samples, seed):
+    ref, deg = speech_like_pair(batch, samples, seed=seed, noise=0.1)
+    got = model._run(torch.from_numpy(ref).cuda(), torch.from_numpy(deg).cuda())
+    for name, g, w in zip(("d_symm", "d_asymm", "mos", "loss"), got, _oracle(ref, deg)):
+        assert _rel(g, w) < F64_RTOL, (name, _rel(g, w))
+
+
+@pytest.mark.parametrize("config,items", [(1, None), (2, None)])
+def test_matches_float64_baseline_configs(model, config, items):
+    ref, deg, fs = synthetic_config(config, items=items)
+    assert fs == 16000
+    got = model._run(torch.from_numpy(ref).cuda(), torch.from_numpy(deg).cuda())
+    for name, g, w in zip(("d_symm", "d_asymm", "mos", "loss"), got, _oracle(ref, deg)):
+        assert _rel(g, w) < F64_RTOL, (name, _rel(g, w))
+
+
+def test_long_signal_config4(model):
+    # 4 x 60 s, the level alignment scan spans 235 blocks per row
+    ref, deg, _ = synthetic_config(4)
+    got = model._run(torch.from_numpy(ref).cuda(), torch.from_numpy(deg).cuda())
+    for name, g, w in zip(("d_symm", "d_asymm", "mos", "loss"), got, _oracle(ref, deg)):
+        assert _rel(g, w) < F64_RTOL, (name, _rel(g, w))
+
+
+def _grads(model, ref, deg, weights, need_ref=True):
+    r = torch.from_numpy(ref).cuda().requires_grad_(need_ref)
+    d = torch.from_numpy(deg).cuda().requires_grad_(True)
+    loss = model(r, d)
+    inputs = [r, d] if need_ref else [d]
+    grads = torch.autograd.grad(loss, inputs, grad_outputs=weights.float().cuda())
+    return [g.double().cpu() for g in grads]
+
+
+def _oracle_grads(ref, deg, weights, factor=0.5):
+    r = torch.from_numpy(ref).double().requires_grad_(True)
+    d = torch.from_numpy(deg).double().requires_grad_(True)
+    ds, da = O.pipeline(r, d)
+    _, loss = O.epilogue(ds, da, factor)
+    (loss * weights).sum().backward()
+    return r.grad, d.grad
+
+
+def _grad_err(got, want):
+    return float((got - want).abs().max() / want.abs().max())
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_gradients_match_float64(model, seed):
+    ref, deg = speech_like_pair(2, 32000, seed=seed, noise=0.1)
+    weights = torch.tensor([0.7, -1.3], dtype=torch.float64)
+    g_ref, g_deg = _grads(model, ref, deg, weights)
+    w_ref, w_deg = _oracle_grads(ref, deg, weights)
+    assert _grad_err(g_ref, w_ref) < GRAD_RTOL
+    assert _grad_err(g_deg, w_deg) < GRAD_RTOL
+
+
+def test_degraded_gradient_config2(model):
+    ref, deg, _ = synthetic_config(2)
+    weights = torch.linspace(0.5, 1.5, ref.shape[0], dtype=torch.float64)
+    (g_deg,) = _grads(model, ref, deg, weights, need_ref=False)
+    _, w_deg = _oracle_grads(ref, deg, weights)
+    assert _grad_err(g_deg, w_deg) < 1e-4
+
+
+def test_gradient_masks_agree_bitwise(model):
+    ref, deg = speech_like_pair(2, 24000, seed=5, noise=0.1)
+    weights = torch.tensor([1.0, 2.0], dtype=torch.float64)
+    both = _grads(model, ref, deg, weights)
+    (deg_only,) = _grads(model, ref, deg, weights, need_ref=False)
+    assert torch.equal(both[1], deg_only)
+    r = torch.from_numpy(ref).cuda().requires_grad_(True)
+    (ref_only,) = torch.autograd.grad(
+        model(r, torch.from_numpy(deg).cuda()), r, grad_outputs=weights.float().cuda()
+    )
+    assert torch.equal(both[0], ref_only.double().cpu())
+
+
+def test_mos_and_distance_gradients(model):
+    ref, deg = speech_like_pair(2, 24000, seed=6, noise=0.1)
+    d = torch.from_numpy(deg).cuda().requires_grad_(True)
+    r = torch.from_numpy(ref).cuda()
+    (g_mos,) = torch.autograd.grad(model.mos(r, d).sum(), d)
+    ds, da = model.raw(r, d)
+    (g_raw,) = torch.autograd.grad((0.3 * ds + 0.2 * da).sum(), d)
+
+    dd = torch.from_numpy(deg).double().requires_grad_(True)
+    ods, oda = O.pipeline(torch.from_numpy(ref), dd)
+    omos, _ = O.epilogue(ods, oda, 0.5)
+    (want_mos,) = torch.autograd.grad(omos.sum(), dd, retain_graph=True)
+    (want_raw,) = torch.autograd.grad((0.3 * ods + 0.2 * oda).sum(), dd)
+    assert _grad_err(g_mos.double().cpu(), want_mos) < GRAD_RTOL
+    assert _grad_err(g_raw.double().cpu(), want_raw) < GRAD_RTOL
+
+
+def test_intermediates_match_oracle(model):
+    ref, deg = speech_like_pair(2, 20000, seed=7, noise=0.1)
+    r, d = torch.from_numpy(ref).cuda(), torch.from_numpy(deg).cuda()
+    _, ws = pipeline_forward(r, d, model.model_table, 0.5, 0)
+    batch, n = ref.shape
+
+    def region(name, dtype, shape):
+        off, size = pipeline_region(batch, n, 0, name)
+        count = int(np.prod(shape))
+        return ws[off : off + size].view(dtype)[:count].view(shape).double().cpu()
+
+    c = O.constants()
+    s = torch.cat([torch.from_numpy(ref), torch.from_numpy(deg)]).double()
+    peak = torch.max(s[:batch].abs().amax(1), s[batch:].abs().amax(1)).repeat(2)
+    x = s / peak[:, None]
+    fx = torch.from_numpy(O.lfilter64(x.numpy(), c["power_b"], c["power_a"]))
+    px = torch.from_numpy(O.lfilter64(O.edge_ramp(x).numpy(), c["pre_b"], c["pre_a"]))
+    energy = (fx**2).sum(1)
+    scale = (1e7 / (energy / (n + 5120) / 1.04684)).sqrt()
+
+    assert _grad_err(region("p", torch.float32, (2 * batch, n)), px) < 2e-7
+    rowconst = region("rowconst", torch.float64, (2 * batch, 4))
+    assert _rel(rowconst[:, 0], 1 / peak) < 1e-12
+    assert _rel(rowconst[:, 1], energy) < 1e-9
+    assert _rel(rowconst[:, 2], scale) < 1e-9
+    frames = O.n_frames(n)
+    bark = region("bark", torch.float32, (2 * batch, frames, 49))
+    want = O.stft_bark(px * scale[:, None], c)
+    frame_err = ((bark - want).abs().amax(2) / want.abs().amax(2).clamp(min=1e-30)).max()
+    assert float(frame_err) < 5e-7
+
+
+def test_deterministic(model):
+    ref, deg = speech_like_pair(3, 20000, seed=8, noise=0.1)
+    r = torch.from_numpy(ref).cuda().requires_grad_(True)
+    d = torch.from_numpy(deg).cuda()
+    first = model(r, d)
+    (g1,) = torch.autograd.grad(first.sum(), r)
+    second = model(r, d)
+    (g2,) = torch.autograd.grad(second.sum(), r)
+    assert torch.equal(first, second)
+    assert torch.equal(g1, g2)
+
+
+def test_batch_independence(model):
+    ref, deg = speech_like_pair(4, 16000, seed=9, noise=0.1)
+    r, d = torch.from_numpy(ref).cuda(), torch.from_numpy(deg).cuda()
+    batched = model(r, d)
+    single = torch.cat([model(r[i : i + 1], d[i : i + 1]) for i in range(4)])
+    assert torch.equal(batched, single)
+
+
+def test_graph_replay_is_bit_exact(model):
+    ref, deg = speech_like_pair(2, 16000, seed=10, noise=0.1)
+    r = torch.from_numpy(ref).cuda().requires_grad_(True)
+    d = torch.from_numpy(deg).cuda().requires_grad_(True)
+    eager = model(r, d)
+    eager_grads = torch.autograd.grad(eager.sum(), [r, d])
+    graphed = model.graphed(r, d)
+    for _ in range(3):
+        captured = graphed(r, d)
+        grads = torch.autograd.grad(captured.sum(), [r, d])
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager)
+        for want, got in zip(eager_grads, grads):
+            assert torch.equal(got, want)
+        # eager work between the replays
+        model(r.detach() * 2, d.detach())
+        torch.cuda.synchronize()
+
+
+def test_identical_signals_and_ranges(model):
+    ref, deg = speech_like_pair(3, 16000, seed=11, noise=0.1)
+    r = torch.from_numpy(ref).cuda()
+    same = model(r, r)
+    assert torch.all(same <= 1e-6) and torch.all(same >= 0.0)
+    loss = model(r, torch.from_numpy(deg).cuda())
+    assert torch.all(loss > 0.0)
+    mos = model.mos(r, torch.from_numpy(deg).cuda())
+    assert torch.all(mos > 1.0) and torch.all(mos < 5.0)
+
+
+def test_scale_invariance(model):
+    ref, deg = speech_like_pair(2, 16000, seed=12, noise=0.1)
+    r, d = torch.from_numpy(ref).cuda(), torch.from_numpy(deg).cuda()
+    base = model(r, d)
+    torch.testing.assert_close(model(r * 1e-3, d * 37.0), base, rtol=1e-6, atol=0)
+
+
+def test_one_dimensional_and_strided_inputs(model):
+    ref, deg = speech_like_pair(1, 32000, seed=13, noise=0.1)
+    r, d = torch.from_numpy(ref).cuda(), torch.from_numpy(deg).cuda()
+    assert torch.equal(model(r[0], d[0]), model(r, d))
+    strided_r, strided_d = r[:, ::2], d[:, ::2]
+    assert not strided_r.is_contiguous()
+    assert torch.equal(model(strided_r, strided_d), model(strided_r.contiguous(), strided_d.contiguous()))
+
+
+def test_error_conventions(model):
+    ref, deg = speech_like_pair(1, 16000, seed=14)
+    with pytest.raises(RuntimeError):
+        model(torch.from_numpy(ref), torch.from_numpy(deg))
+    with pytest.raises(RuntimeError):
+        model(torch.from_numpy(ref).cuda().double(), torch.from_numpy(deg).cuda().double())
+    with pytest.raises(ValueError):
+        model(torch.from_numpy(ref).cuda(), torch.from_numpy(deg[:, :8000]).cuda())
+    with pytest.raises(ValueError):
+        short = torch.from_numpy(ref[:, :5000]).cuda()
+        model(short, short)

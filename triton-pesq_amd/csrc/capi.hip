@@ -1,0 +1,154 @@
+// Host side of the C ABI: error reporting and constant table packing.
+#include <cmath>
+#include <cstdarg>
+#include <cstring>
+
+#include "tables.hpp"
+
+namespace pesq {
+
+static thread_local char g_error[512] = "";
+
+void set_error(const char *fmt, ...) {
+    va_list args;
+    va_start(args, fmt);
+    std::vsnprintf(g_error, sizeof(g_error), fmt, args);
+    va_end(args);
+}
+
+// A^n for the 2x2 companion block [[-a1, 1], [-a2, 0]], fp64
+static void mat_mul(const double *x, const double *y, double *out) {
+    const double r0 = x[0] * y[0] + x[1] * y[2];
+    const double r1 = x[0] * y[1] + x[1] * y[3];
+    const double r2 = x[2] * y[0] + x[3] * y[2];
+    const double r3 = x[2] * y[1] + x[3] * y[3];
+    out[0] = r0;
+    out[1] = r1;
+    out[2] = r2;
+    out[3] = r3;
+}
+
+static int fill_sections(IirTable &t, int first, const pesq_iir_sections &s) {
+    PESQ_CHECK_ARG(s.count >= 1 && first + s.count <= kMaxSections,
+                   "an IIR filter needs 1..%d sections in total, got %d", kMaxSections,
+                   first + s.count);
+    for (int k = 0; k < s.count; ++k) {
+        const int q = first + k;
+        t.b0[q] = s.b0[k];
+        t.b1[q] = s.b1[k];
+        t.b2[q] = s.b2[k];
+        t.a1[q] = s.a1[k];
+        t.a2[q] = s.a2[k];
+        PESQ_CHECK_ARG(std::isfinite(s.b0[k]) && std::isfinite(s.b1[k]) && std::isfinite(s.b2[k]) &&
+                           std::isfinite(s.a1[k]) && std::isfinite(s.a2[k]),
+                       "non finite IIR coefficient in section %d", k);
+        // chunk transfer powers: level 0 = A^kChunk, level j = A^(kChunk 2^j)
+        const double a[4] = {-s.a1[k], 1.0, -s.a2[k], 0.0};
+        double p[4] = {1.0, 0.0, 0.0, 1.0};
+        for (int i = 0; i < kChunk; ++i) mat_mul(a, p, p);
+        for (int level = 0; level < kLevels; ++level) {
+            std::memcpy(t.pw[level][q], p, sizeof(p));
+            mat_mul(p, p, p);
+        }
+    }
+    return PESQ_OK;
+}
+
+static int pack_iir(IirTable &t, const pesq_iir_sections *a, const pesq_iir_sections *b) {
+    std::memset(&t, 0, sizeof(t));
+    PESQ_CHECK_ARG(a != nullptr, "null filter");
+    t.na = a->count;
+    t.nb = b ? b->count : 0;
+    t.c0a = a->c0;
+    t.c0b = b ? b->c0 : 0.0;
+    if (int st = fill_sections(t, 0, *a)) return st;
+    if (b) {
+        if (int st = fill_sections(t, a->count, *b)) return st;
+    }
+    return PESQ_OK;
+}
+
+}  // namespace pesq
+
+using namespace pesq;
+
+extern "C" int pesq_abi_version(void) { return 1; }
+
+extern "C" const char *pesq_last_error(void) { return g_error; }
+
+extern "C" size_t pesq_iir_table_bytes(void) { return sizeof(IirTable); }
+
+extern "C" int pesq_iir_table_pack(const pesq_iir_sections *filter, void *out) {
+    PESQ_CHECK_ARG(out != nullptr, "null output buffer");
+    IirTable t;
+    if (int st = pack_iir(t, filter, nullptr)) return st;
+    std::memcpy(out, &t, sizeof(t));
+    return PESQ_OK;
+}
+
+extern "C" size_t pesq_model_table_bytes(void) { return sizeof(ModelTable); }
+
+extern "C" int pesq_model_table_pack(const pesq_model_constants *c, void *out) {
+    PESQ_CHECK_ARG(c != nullptr && out != nullptr, "null argument");
+    PESQ_CHECK_ARG(c->nbarks == kBands && c->n_fft == kNfft && c->hop == kHop,
+                   "the HIP pipeline supports nbarks=49, n_fft=512, hop_length=256 "
+                   "(got %d, %d, %d)",
+                   c->nbarks, c->n_fft, c->hop);
+    PESQ_CHECK_ARG(c->power_filter.count == 5 && c->pre_filter.count == 1,
+                   "the HIP pipeline is built for a 5 section level alignment filter and a "
+                   "1 section pre-emphasis filter (got %d and %d)",
+                   c->power_filter.count, c->pre_filter.count);
+
+    ModelTable *t = new ModelTable;
+    std::memset(t, 0, sizeof(*t));
+    int st = pack_iir(t->iir, &c->power_filter, &c->pre_filter);
+    if (st) {
+        delete t;
+        return st;
+    }
+
+    const double two_pi = 6.283185307179586476925286766559;
+    for (int m = 0; m < kHalf; ++m) {
+        t->tw256[m] = make_double2(std::cos(two_pi * m / 256.0), -std::sin(two_pi * m / 256.0));
+        t->tw512[m] = make_double2(std::cos(two_pi * m / 512.0), -std::sin(two_pi * m / 512.0));
+    }
+    std::memcpy(t->window, c->window, sizeof(t->window));
+
+    for (int f = 0; f < kHalf; ++f) t->bin_band[f] = -1;
+    int prev = 0;
+    for (int i = 0; i < kBands; ++i) {
+        const int lo = c->band_start[i], hi = c->band_end[i];
+        if (lo < prev || hi < lo || hi > kHalf) {
+            delete t;
+            set_error("Bark band %d covers [%d, %d): bands must be sorted, disjoint and "
+                      "inside [0, 256)",
+                      i, lo, hi);
+            return PESQ_ERR_ARGUMENT;
+        }
+        t->band_start[i] = lo;
+        t->band_end[i] = hi;
+        for (int f = lo; f < hi; ++f) t->bin_band[f] = i;
+        prev = hi;
+        if (!(c->threshs[i] > 0.0)) {
+            delete t;
+            set_error("Hearing thresholds have to be strictly positive.");
+            return PESQ_ERR_ARGUMENT;
+        }
+        t->corr[i] = c->corr[i];
+        t->threshs[i] = c->threshs[i];
+        t->exps[i] = c->exps[i];
+        t->width[i] = c->width[i];
+        t->loud_scale[i] = c->sl * std::pow(2.0 * c->threshs[i], c->exps[i]);
+    }
+    // the DC bin is dropped (the energy feature is unused)
+    t->bin_band[0] = -1;
+    t->total_width = c->total_width;
+    t->sl = c->sl;
+    t->nbarks = kBands;
+    t->n_fft = kNfft;
+    t->hop = kHop;
+
+    std::memcpy(out, t, sizeof(*t));
+    delete t;
+    return PESQ_OK;
+}

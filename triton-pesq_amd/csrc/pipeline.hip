@@ -1,0 +1,954 @@
+// Fused PESQ pipeline, forward and backward, for 16 kHz rows.
+//
+// Forward (5 kernels):
+//   1. iir_aggregate  <power, pre>   per block end states of both filters on the
+//                                    raw inputs, per block peak |s|
+//   2. iir_output     <power, pre>   p = pre(ramp(x)), f = power(x) (kept when a
+//                                    gradient is needed), per block sum f^2;
+//                                    x = s / peak, peak = max(|ref|, |deg|) per item
+//   3. stft_fwd       per (item, 16 frames): frames of scale * p, FFT, |X|^2,
+//                                    Bark sums, silent frames, band partials
+//   4. chain_fwd      per (item, 16 frames): band and frame equalisation,
+//                                    loudness, disturbance, per frame distances
+//   5. chain_final    per item: overlapping sums, distances, MOS, loss
+// Backward (4 kernels):
+//   6. chain_bwd      per (item, 16 frames): adjoint of 4 and of the PSQM/MOS
+//   7. stft_bwd       per (grad row, 7 hop blocks): band ratio adjoint, frame
+//                                    spectra recomputed, adjoint FFT, overlap-add
+//   8. iir_aggregate  <power^T, pre^T> on (f, dL/dp), time reversed
+//   9. iir_output     <power^T, pre^T> and the level alignment adjoint:
+//        dL/ds = (scale ramp(pre^T g_p) - scale S / E power^T f) / peak
+//
+// The level alignment (torch_pesq/loss.py:127-139) is folded in: with
+// E = sum f^2 the aligned, pre-emphasised signal is p_aligned = scale * p,
+// scale = sqrt(1e7 (len + 5120) 1.04684 / E), because the ramp and the
+// pre-emphasis filter are linear.  The peak normalisation
+// (torch_pesq/loss.py:179-183) is applied at the output of the scans, which
+// run on the raw inputs.
+#include <cmath>
+
+#include "pipeline_layout.hpp"
+#include "tables.hpp"
+
+namespace pesq {
+
+constexpr int kPowerSections = 5;  // order 10 band pass, parallel form
+constexpr int kPreSections = 1;    // pre-emphasis biquad
+
+// ---------------------------------------------------------------------------
+// IIR modes
+// ---------------------------------------------------------------------------
+
+struct PipeFwdMode {
+    static constexpr int kInputs = 1;
+    static constexpr bool kReverse = false;
+    static constexpr bool kAccumulates = true;
+
+    const float *ref, *deg;
+    float *p, *f;             // outputs; f may be null
+    float *peak;              // [rows, nblk] aggregate-pass output
+    const float *peak_in;     // same buffer, read by the output pass
+    double *energy;           // [rows, nblk]
+    int64_t len;
+    int batch, nblk, row0, nrg;
+
+    __device__ __forceinline__ void load(int row, int64_t n, float *in) const {
+        in[0] = row < batch ? ref[int64_t(row) * len + n] : deg[int64_t(row - batch) * len + n];
+    }
+    __device__ __forceinline__ void inputs(int64_t n, const float *in, double &xa,
+                                           double &xb) const {
+        xa = in[0];
+        xb = in[0] * edge_weight(n, len);
+    }
+    __device__ __forceinline__ float observe(float o, const float *in) const {
+        return fmaxf(o, fabsf(in[0]));
+    }
+    __device__ __forceinline__ float reduce_observed(float o) const { return wave_max(o); }
+    __device__ __forceinline__ float combine_observed(float a, float b) const { return fmaxf(a, b); }
+    __device__ __forceinline__ void observed(int row, int blk, float o) const {
+        peak[int64_t(row) * nblk + blk] = o;
+    }
+    __device__ __forceinline__ void setup(int row, int, double *sh, int lane) const {
+        const int item = row % batch;
+        float m = 0.0f;
+        for (int i = lane; i < nblk; i += kWave) {
+            m = fmaxf(m, peak_in[int64_t(item) * nblk + i]);
+            m = fmaxf(m, peak_in[int64_t(item + batch) * nblk + i]);
+        }
+        m = wave_max(m);
+        if (lane == 0) sh[0] = 1.0 / static_cast<double>(m);
+    }
+    __device__ __forceinline__ void emit(int row, int64_t n, double ya, double yb, double &acc,
+                                         const double *sh) const {
+        const double inv = sh[0];
+        const double fx = ya * inv;
+        p[int64_t(row) * len + n] = static_cast<float>(yb * inv);
+        if (f != nullptr && row >= row0 && row < row0 + nrg) {
+            f[int64_t(row - row0) * len + n] = static_cast<float>(fx);
+        }
+        acc = fma(fx, fx, acc);
+    }
+    __device__ __forceinline__ void finish(int row, int blk, double total) const {
+        energy[int64_t(row) * nblk + blk] = total;
+    }
+};
+
+struct PipeBwdMode {
+    static constexpr int kInputs = 2;
+    static constexpr bool kReverse = true;
+    static constexpr bool kAccumulates = false;
+
+    const float *f, *gp;      // [nrg, len] each
+    const double *rowconst;   // [rows, 4]: 1/peak, E, scale
+    const double *spart;      // [nrg, nhoptile]
+    float *g_ref, *g_deg;
+    int64_t len;
+    int batch, row0, nhoptile;
+
+    __device__ __forceinline__ void load(int row, int64_t n, float *in) const {
+        in[0] = f[int64_t(row) * len + n];
+        in[1] = gp[int64_t(row) * len + n];
+    }
+    __device__ __forceinline__ void inputs(int64_t, const float *in, double &xa, double &xb) const {
+        xa = in[0];
+        xb = in[1];
+    }
+    __device__ __forceinline__ float observe(float o, const float *) const { return o; }
+    __device__ __forceinline__ float reduce_observed(float o) const { return o; }
+    __device__ __forceinline__ float combine_observed(float a, float) const { return a; }
+    __device__ __forceinline__ void observed(int, int, float) const {}
+    __device__ __forceinline__ void setup(int row, int, double *sh, int lane) const {
+        double s = 0.0;
+        for (int i = lane; i < nhoptile; i += kWave) s += spart[int64_t(row) * nhoptile + i];
+        s = wave_sum(s);
+        if (lane == 0) {
+            const double *rc = rowconst + int64_t(row0 + row) * 4;
+            sh[0] = rc[0];                 // 1 / peak
+            sh[1] = rc[2];                 // scale
+            sh[2] = rc[2] * s / rc[1];     // scale S / E
+        }
+    }
+    __device__ __forceinline__ void emit(int row, int64_t n, double ya, double yb, double &,
+                                         const double *sh) const {
+        const double g = sh[0] * (sh[1] * edge_weight(n, len) * yb - sh[2] * ya);
+        const int stacked = row0 + row;
+        float *dst = stacked < batch ? g_ref + int64_t(stacked) * len
+                                     : g_deg + int64_t(stacked - batch) * len;
+        dst[n] = static_cast<float>(g);
+    }
+    __device__ __forceinline__ void finish(int, int, double) const {}
+};
+
+// ---------------------------------------------------------------------------
+// shared chain helpers
+// ---------------------------------------------------------------------------
+
+struct PipeArgs {
+    const ModelTable *tab;
+    const float *ref, *deg;
+    unsigned char *ws;  // forward workspace
+    unsigned char *bw;  // backward workspace
+    PipeLayout L;
+    double factor;
+    float *d_symm, *d_asymm, *mos, *loss;
+    const float *g_symm, *g_asymm, *g_mos, *g_loss;
+};
+
+template <typename T>
+__host__ __device__ __forceinline__ T *region(unsigned char *base, size_t off) {
+    return reinterpret_cast<T *>(base + off);
+}
+
+__device__ __forceinline__ double *frame_array(const PipeArgs &a, int which) {
+    return region<double>(a.ws, a.L.frame) + int64_t(which) * a.L.batch * a.L.frames;
+}
+
+__device__ __forceinline__ double *band_array(const PipeArgs &a, int which) {
+    return region<double>(a.ws, a.L.band) + int64_t(which) * a.L.batch * kBands;
+}
+
+// Zwicker loudness sl (2 th)^e ((0.5 + 0.5 x / th)^e - 1) above the threshold,
+// written as loud_scale expm1(e log1p((x - th) / (2 th))) so that bands just
+// above their threshold keep full precision.
+__device__ __forceinline__ double loudness(double x, double th, double e, double ls) {
+    if (!(x > th)) return 0.0;
+    return ls * expm1(e * log1p(0.5 * (x - th) / th));
+}
+
+// d loudness / dx above the threshold
+__device__ __forceinline__ double loudness_slope(double x, double th, double e, double ls) {
+    if (!(x > th)) return 0.0;
+    return ls * e * 0.5 / th * exp((e - 1.0) * log1p(0.5 * (x - th) / th));
+}
+
+__device__ __forceinline__ double sgn(double v) { return v > 0.0 ? 1.0 : (v < 0.0 ? -1.0 : 0.0); }
+
+// ---------------------------------------------------------------------------
+// 3. STFT forward + silent frames + band partials, per (item, 16 frames)
+// ---------------------------------------------------------------------------
+
+constexpr int kStftWaves = 8;
+
+template <typename real>
+__global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a) {
+    __shared__ cplx<real> fftbuf[kStftWaves][kHalf];
+    __shared__ float barks[2][kTile][kBands];
+    __shared__ float keepflag[kTile];
+
+    const ModelTable &t = *a.tab;
+    const PipeLayout &L = a.L;
+    const int item = blockIdx.x / L.ntile;
+    const int tile = blockIdx.x - item * L.ntile;
+    const int t0 = tile * kTile;
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int side = wave / 4;                   // 0 = reference, 1 = degraded
+    const int row = side * L.batch + item;
+
+    // row constants: 1 / peak, E, scale
+    const float *peak = region<float>(a.ws, L.peak);
+    const double *energy = region<double>(a.ws, L.energy);
+    float m = 0.0f;
+    double e = 0.0;
+    for (int i = lane; i < L.nblk; i += kWave) {
+        m = fmaxf(m, fmaxf(peak[int64_t(item) * L.nblk + i],
+                           peak[int64_t(item + L.batch) * L.nblk + i]));
+        e += energy[int64_t(row) * L.nblk + i];
+    }
+    m = wave_max(m);
+    e = wave_sum(e);
+    const double power = e / static_cast<double>(L.len + 5120) / 1.04684;
+    const double scale = sqrt(1e7 / power);
+    if (tile == 0 && (wave & 3) == 0 && lane == 0) {
+        double *rc = region<double>(a.ws, L.rowconst) + int64_t(row) * 4;
+        rc[0] = 1.0 / static_cast<double>(m);
+        rc[1] = e;
+        rc[2] = scale;
+        rc[3] = 0.0;
+    }
+    const real scale2 = static_cast<real>(scale * scale);
+
+    const float *p = region<float>(a.ws, L.p) + int64_t(row) * L.len;
+    float *bark = region<float>(a.ws, L.bark) + int64_t(row) * L.frames * kBands;
+    cplx<real> *buf = fftbuf[wave];
+    real *power_buf = reinterpret_cast<real *>(buf);
+
+    for (int q = 0; q < 4; ++q) {
+        const int local = (wave & 3) * 4 + q;
+        const int64_t frame = t0 + local;
+        if (frame >= L.frames) break;
+        const int64_t start = frame * kHop;
+        auto u = [&](int k) -> real {
+            const int64_t n = start + k;
+            return n < L.len ? static_cast<real>(p[n]) * static_cast<real>(t.window[k]) : real(0);
+        };
+        cplx<real> x[4];
+        frame_spectrum<real>(u, x, buf, t.tw256, t.tw512, lane);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int fbin = lane + 64 * r;
+            power_buf[fbin] = fbin == 0 ? real(0) : (x[r].re * x[r].re + x[r].im * x[r].im) * scale2;
+        }
+        wave_lds_fence();
+        double val = 0.0;
+        if (lane < kBands) {
+            double acc = 0.0;
+            for (int fbin = t.band_start[lane]; fbin < t.band_end[lane]; ++fbin) {
+                acc += static_cast<double>(power_buf[fbin]);
+            }
+            const float v = static_cast<float>(acc * t.corr[lane]);
+            bark[frame * kBands + lane] = v;
+            barks[side][local][lane] = v;
+            val = v;
+        }
+        wave_lds_fence();
+        if (side == 0) {
+            // silent frame: audible (> 100 th) energy of the reference below 1e7
+            const double aud = lane < kBands && val > 100.0 * t.threshs[lane] ? val : 0.0;
+            const double total = wave_sum(aud);
+            if (lane == 0) {
+                const float k = total >= 1e7 ? 1.0f : 0.0f;
+                keepflag[local] = k;
+                region<float>(a.ws, L.keep)[int64_t(item) * L.frames + frame] = k;
+            }
+        }
+    }
+    __syncthreads();
+
+    // band partial sums of the audible, non silent frames of this tile
+    if (wave < 2 && lane < kBands) {
+        const double th100 = 100.0 * t.threshs[lane];
+        double acc = 0.0;
+        for (int local = 0; local < kTile; ++local) {
+            if (t0 + local >= L.frames) break;
+            const double v = barks[wave][local][lane];
+            if (keepflag[local] != 0.0f && v > th100) acc += v;
+        }
+        double *dst = region<double>(a.ws, wave == 0 ? L.bandref : L.banddeg);
+        dst[(int64_t(item) * L.ntile + tile) * kBands + lane] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 4. chain forward per (item, 16 frames)
+// ---------------------------------------------------------------------------
+
+struct BandConsts {
+    double th, e, ls, w;
+};
+
+__device__ __forceinline__ BandConsts band_consts(const ModelTable &t, int lane) {
+    BandConsts c{1.0, 1.0, 0.0, 0.0};
+    if (lane < kBands) {
+        c.th = t.threshs[lane];
+        c.e = t.exps[lane];
+        c.ls = t.loud_scale[lane];
+        c.w = t.width[lane];
+    }
+    return c;
+}
+
+constexpr int kChainWaves = 4;
+
+__global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs a) {
+    __shared__ double rs[kBands];
+
+    const ModelTable &t = *a.tab;
+    const PipeLayout &L = a.L;
+    const int item = blockIdx.x / L.ntile;
+    const int tile = blockIdx.x - item * L.ntile;
+    const int t0 = tile * kTile;
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const double frames_f = static_cast<double>(L.frames);
+
+    if (wave == 0 && lane < kBands) {
+        const double *pr = region<double>(a.ws, L.bandref) + int64_t(item) * L.ntile * kBands;
+        const double *pd = region<double>(a.ws, L.banddeg) + int64_t(item) * L.ntile * kBands;
+        double sr = 0.0, sd = 0.0;
+        for (int i = 0; i < L.ntile; ++i) {
+            sr += pr[i * kBands + lane];
+            sd += pd[i * kBands + lane];
+        }
+        const double mref = sr / frames_f;
+        const double mdeg = sd / frames_f;
+        const double ratio = (mdeg + 1000.0) / (mref + 1000.0);
+        const double r = fmin(fmax(ratio, 0.01), 100.0);
+        rs[lane] = r;
+        if (tile == 0) {
+            band_array(a, kR)[item * kBands + lane] = r;
+            band_array(a, kRatio)[item * kBands + lane] = ratio;
+            band_array(a, kMref)[item * kBands + lane] = mref;
+        }
+    }
+    __syncthreads();
+
+    const BandConsts c = band_consts(t, lane);
+    const bool live = lane < kBands;
+    const double r = live ? rs[lane] : 0.0;
+    const float *bref = region<float>(a.ws, L.bark) + int64_t(item) * L.frames * kBands;
+    const float *bdeg = region<float>(a.ws, L.bark) + int64_t(item + L.batch) * L.frames * kBands;
+    const double sqrt_w = sqrt(t.total_width);
+    const double W = t.total_width;
+
+    auto totals = [&](int64_t frame, double &taer, double &tad) {
+        double vr = 0.0, vd = 0.0;
+        if (live) {
+            const double er = r * static_cast<double>(bref[frame * kBands + lane]);
+            const double g = bdeg[frame * kBands + lane];
+            vr = er > c.th ? er : 0.0;
+            vd = g > c.th ? g : 0.0;
+        }
+        taer = wave_sum(vr);
+        tad = wave_sum(vd);
+    };
+
+    for (int q = 0; q < kTile / kChainWaves; ++q) {
+        const int64_t frame = t0 + wave * (kTile / kChainWaves) + q;
+        if (frame >= L.frames) break;
+        double taer, tad;
+        totals(frame, taer, tad);
+        const double fpr0 = (taer + 5e3) / (tad + 5e3);
+        const double h = pow((taer + 1e5) / 1e7, 0.04);
+        double fpr1 = fpr0;
+        if (frame > 0) {
+            double taer_p, tad_p;
+            totals(frame - 1, taer_p, tad_p);
+            fpr1 = fpr0 * 0.8 + ((taer_p + 5e3) / (tad_p + 5e3)) * 0.2;
+        }
+        const double fpr = fmin(fmax(fpr1, 3e-4), 5.0);
+
+        double v2 = 0.0, ya = 0.0;
+        if (live) {
+            const double R = bref[frame * kBands + lane];
+            const double G = bdeg[frame * kBands + lane];
+            const double er = r * R;
+            const double ed = fpr * G;
+            const double lr = loudness(er, c.th, c.e, c.ls);
+            const double ld = loudness(ed, c.th, c.e, c.ls);
+            const double u = ld - lr;
+            const double z = fabs(u) - 0.25 * fmin(ld, lr);
+            const double dist = sgn(u) * fmax(z, 0.0);
+            const double asc_raw = pow((ed + 50.0) / (er + 50.0), 1.2);
+            const double asc = asc_raw < 3.0 ? 0.0 : fmin(asc_raw, 12.0);
+            if (lane >= 1) {
+                const double v = c.w * dist / sqrt_w;
+                v2 = v * v;
+                ya = fabs(c.w * (dist * asc) / W);
+            }
+        }
+        const double symm_raw = W * sqrt(wave_sum(v2));
+        const double asymm_raw = W * wave_sum(ya);
+        if (lane == 0) {
+            const int64_t o = int64_t(item) * L.frames + frame;
+            frame_array(a, kTaer)[o] = taer;
+            frame_array(a, kTad)[o] = tad;
+            frame_array(a, kFpr0)[o] = fpr0;
+            frame_array(a, kFpr1)[o] = fpr1;
+            frame_array(a, kH)[o] = h;
+            frame_array(a, kSymmRaw)[o] = symm_raw;
+            frame_array(a, kAsymmRaw)[o] = asymm_raw;
+            frame_array(a, kSymm)[o] = fmin(fmax(symm_raw, 1e-20) / h, 45.0);
+            frame_array(a, kAsymm)[o] = fmin(fmax(asymm_raw, 1e-20) / h, 45.0);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 5. overlapping sums, distances, MOS and loss, one workgroup per item
+// ---------------------------------------------------------------------------
+
+constexpr int kFinalThreads = 256;
+
+__device__ __forceinline__ double block_sum(double v, double *scratch) {
+    const int wave = threadIdx.x / kWave;
+    v = wave_sum(v);
+    if ((threadIdx.x % kWave) == 0) scratch[wave] = v;
+    __syncthreads();
+    double total = 0.0;
+    for (int i = 0; i < int(blockDim.x / kWave); ++i) total += scratch[i];
+    __syncthreads();
+    return total;
+}
+
+__global__ void __launch_bounds__(kFinalThreads) chain_final_kernel(PipeArgs a) {
+    __shared__ double scratch[kFinalThreads / kWave];
+    const PipeLayout &L = a.L;
+    const int item = blockIdx.x;
+    double d[2];
+    for (int which = 0; which < 2; ++which) {
+        const double *s = frame_array(a, which == 0 ? kSymm : kAsymm) + int64_t(item) * L.frames;
+        double *psqm = region<double>(a.ws, L.psqm) + (int64_t(which) * L.batch + item) * L.nwin;
+        double acc = 0.0;
+        for (int64_t l = threadIdx.x; l < L.nwin; l += blockDim.x) {
+            double m6 = 0.0;
+            for (int j = 0; j < kWin; ++j) {
+                const double v = s[l * kStride + j];
+                const double v2 = v * v;
+                m6 += v2 * v2 * v2;
+            }
+            const double pl = pow(m6 / kWin, 1.0 / 6.0);
+            psqm[l] = pl;
+            acc += pl * pl;
+        }
+        d[which] = sqrt(block_sum(acc, scratch) / static_cast<double>(L.nwin));
+    }
+    if (threadIdx.x == 0) {
+        double *dist = region<double>(a.ws, L.dist) + int64_t(item) * 2;
+        dist[0] = d[0];
+        dist[1] = d[1];
+        const double inner = 4.5 - 0.1 * d[0] - 0.0309 * d[1];
+        a.d_symm[item] = static_cast<float>(d[0]);
+        a.d_asymm[item] = static_cast<float>(d[1]);
+        a.mos[item] = static_cast<float>(0.999 + 4.0 / (1.0 + exp(-1.3669 * inner + 3.8224)));
+        a.loss[item] = static_cast<float>(a.factor * (0.1 * d[0] + 0.0309 * d[1]));
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 6. chain backward per (item, 16 frames)
+// ---------------------------------------------------------------------------
+
+// d d / d s_t of d = sqrt(mean_l psqm_l^2), psqm_l = (mean_{j<20} s_{10 l + j}^6)^(1/6)
+__device__ __forceinline__ double psqm_adjoint(const PipeLayout &L, const double *psqm,
+                                               double d, double s, int64_t frame) {
+    if (!(d > 0.0)) return 0.0;
+    double acc = 0.0;
+    const int64_t hi = frame / kStride;
+    for (int64_t l = hi - 1; l <= hi; ++l) {
+        if (l < 0 || l >= L.nwin || frame >= l * kStride + kWin) continue;
+        const double pl = psqm[l];
+        if (!(pl > 0.0)) continue;
+        const double ratio = s / pl;
+        const double r2 = ratio * ratio;
+        acc += pl / (static_cast<double>(L.nwin) * d) * (r2 * r2 * ratio) / kWin;
+    }
+    return acc;
+}
+
+__global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs a) {
+    constexpr int kPer = kTile / kChainWaves;
+    __shared__ double rs[kBands];
+    __shared__ double gfpr[kTile + 1], gh[kTile + 1];
+    __shared__ double part[kChainWaves][kBands];
+
+    const ModelTable &t = *a.tab;
+    const PipeLayout &L = a.L;
+    const int item = blockIdx.x / L.ntile;
+    const int tile = blockIdx.x - item * L.ntile;
+    const int t0 = tile * kTile;
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const bool live = lane < kBands;
+
+    if (wave == 0 && live) rs[lane] = band_array(a, kR)[item * kBands + lane];
+
+    // upstream gradients of the two distances, MOS and loss folded in
+    const double *dist = region<double>(a.ws, L.dist) + int64_t(item) * 2;
+    const double ds = dist[0], da = dist[1];
+    double gds = a.g_symm ? a.g_symm[item] : 0.0;
+    double gda = a.g_asymm ? a.g_asymm[item] : 0.0;
+    if (a.g_loss) {
+        gds += a.g_loss[item] * a.factor * 0.1;
+        gda += a.g_loss[item] * a.factor * 0.0309;
+    }
+    if (a.g_mos) {
+        const double inner = 4.5 - 0.1 * ds - 0.0309 * da;
+        const double ex = exp(-1.3669 * inner + 3.8224);
+        const double dmos = 4.0 * 1.3669 * ex / ((1.0 + ex) * (1.0 + ex));
+        gds += a.g_mos[item] * dmos * -0.1;
+        gda += a.g_mos[item] * dmos * -0.0309;
+    }
+    __syncthreads();
+
+    const BandConsts c = band_consts(t, lane);
+    const double r = live ? rs[lane] : 0.0;
+    const float *bref = region<float>(a.ws, L.bark) + int64_t(item) * L.frames * kBands;
+    const float *bdeg = region<float>(a.ws, L.bark) + int64_t(item + L.batch) * L.frames * kBands;
+    const double *psqm_s = region<double>(a.ws, L.psqm) + int64_t(item) * L.nwin;
+    const double *psqm_a = region<double>(a.ws, L.psqm) + (int64_t(L.batch) + item) * L.nwin;
+    const double W = t.total_width;
+    const int64_t fo = int64_t(item) * L.frames;
+
+    // phase 1: adjoint of the per frame distances down to equ_ref / equ_deg
+    double g_er[kPer + 1], g_ed[kPer + 1];
+    const int nmine = wave == kChainWaves - 1 ? kPer + 1 : kPer;
+    for (int q = 0; q < nmine; ++q) {
+        const int local = wave * kPer + q;
+        const int64_t frame = t0 + local;
+        g_er[q] = g_ed[q] = 0.0;
+        if (frame >= L.frames) continue;
+
+        const double s_sy = frame_array(a, kSymm)[fo + frame];
+        const double s_as = frame_array(a, kAsymm)[fo + frame];
+        const double g_sy = gds * psqm_adjoint(L, psqm_s, ds, s_sy, frame);
+        const double g_as = gda * psqm_adjoint(L, psqm_a, da, s_as, frame);
+        const double raw_s = frame_array(a, kSymmRaw)[fo + frame];
+        const double raw_a = frame_array(a, kAsymmRaw)[fo + frame];
+        const double h = frame_array(a, kH)[fo + frame];
+        const double pre_s = fmax(raw_s, 1e-20), pre_a = fmax(raw_a, 1e-20);
+        const double g_ps = pre_s / h <= 45.0 ? g_sy : 0.0;
+        const double g_pa = pre_a / h <= 45.0 ? g_as : 0.0;
+        const double g_hh = -(g_ps * pre_s + g_pa * pre_a) / (h * h);
+        const double g_rs = raw_s >= 1e-20 ? g_ps / h : 0.0;
+        const double g_ra = raw_a >= 1e-20 ? g_pa / h : 0.0;
+        const double fpr = fmin(fmax(frame_array(a, kFpr1)[fo + frame], 3e-4), 5.0);
+
+        double my_er = 0.0, my_ed = 0.0, gf = 0.0;
+        if (live) {
+            const double R = bref[frame * kBands + lane];
+            const double G = bdeg[frame * kBands + lane];
+            const double er = r * R, ed = fpr * G;
+            const double lr = loudness(er, c.th, c.e, c.ls);
+            const double ld = loudness(ed, c.th, c.e, c.ls);
+            const double u = ld - lr;
+            const double z = fabs(u) - 0.25 * fmin(ld, lr);
+            const double su = sgn(u);
+            const double dst = su * fmax(z, 0.0);
+            const double asc_raw = pow((ed + 50.0) / (er + 50.0), 1.2);
+            const double asc = asc_raw < 3.0 ? 0.0 : fmin(asc_raw, 12.0);
+
+            double g_dist = 0.0, g_asc = 0.0;
+            if (lane >= 1) {
+                if (raw_s > 0.0) g_dist = g_rs * W * c.w * c.w * dst / raw_s;
+                const double gy = g_ra * c.w * sgn(dst * asc);
+                g_dist += gy * asc;
+                g_asc = gy * dst;
+            }
+            const bool inzone = z >= 0.0;
+            const double g_u = inzone ? g_dist * su * su : 0.0;
+            const double g_min = inzone ? -0.25 * g_dist * su : 0.0;
+            const double wd = ld < lr ? 1.0 : (ld == lr ? 0.5 : 0.0);
+            const double wr = lr < ld ? 1.0 : (ld == lr ? 0.5 : 0.0);
+            const double g_ld = g_u + g_min * wd;
+            const double g_lr = -g_u + g_min * wr;
+            my_er = g_lr * loudness_slope(er, c.th, c.e, c.ls);
+            my_ed = g_ld * loudness_slope(ed, c.th, c.e, c.ls);
+            if (asc_raw >= 3.0 && asc_raw <= 12.0) {
+                my_ed += g_asc * 1.2 * asc_raw / (ed + 50.0);
+                my_er -= g_asc * 1.2 * asc_raw / (er + 50.0);
+            }
+            gf = my_ed * G;
+        }
+        gf = wave_sum(gf);
+        g_er[q] = my_er;
+        g_ed[q] = my_ed;
+        if (lane == 0) {
+            gfpr[local] = gf;
+            gh[local] = g_hh;
+        }
+    }
+    __syncthreads();
+
+    // phase 2: frame power ratio, h and the total audible energies
+    double acc = 0.0;
+    float *gb = region<float>(a.bw, L.gbark);
+    for (int q = 0; q < kPer; ++q) {
+        const int local = wave * kPer + q;
+        const int64_t frame = t0 + local;
+        if (frame >= L.frames) break;
+        const double f1 = frame_array(a, kFpr1)[fo + frame];
+        const double g1 = (f1 >= 3e-4 && f1 <= 5.0) ? gfpr[local] : 0.0;
+        double g1n = 0.0;
+        if (frame + 1 < L.frames) {
+            const double f1n = frame_array(a, kFpr1)[fo + frame + 1];
+            g1n = (f1n >= 3e-4 && f1n <= 5.0) ? gfpr[local + 1] : 0.0;
+        }
+        const double g0 = (frame == 0 ? g1 : 0.8 * g1) + 0.2 * g1n;
+        const double taer = frame_array(a, kTaer)[fo + frame];
+        const double tad = frame_array(a, kTad)[fo + frame];
+        const double fpr0 = frame_array(a, kFpr0)[fo + frame];
+        const double h = frame_array(a, kH)[fo + frame];
+        const double g_taer = g0 / (tad + 5e3) + gh[local] * 0.04 * h / (taer + 1e5);
+        const double g_tad = -g0 * fpr0 / (tad + 5e3);
+        const double fpr = fmin(fmax(f1, 3e-4), 5.0);
+        if (live) {
+            const double R = bref[frame * kBands + lane];
+            const double G = bdeg[frame * kBands + lane];
+            double ger = g_er[q];
+            if (r * R > c.th) ger += g_taer;
+            const double ged = g_ed[q] * fpr + (G > c.th ? g_tad : 0.0);
+            gb[(int64_t(item) * L.frames + frame) * kBands + lane] = static_cast<float>(ger * r);
+            gb[(int64_t(item + L.batch) * L.frames + frame) * kBands + lane] = static_cast<float>(ged);
+            acc += ger * R;
+        }
+    }
+    if (live) part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && live) {
+        double s = 0.0;
+        for (int w = 0; w < kChainWaves; ++w) s += part[w][lane];
+        region<double>(a.bw, L.grpart)[(int64_t(item) * L.ntile + tile) * kBands + lane] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// 7. STFT backward per (grad row, 7 hop blocks)
+// ---------------------------------------------------------------------------
+
+template <typename real>
+__global__ void __launch_bounds__(kWave *kBwdFrames) stft_bwd_kernel(PipeArgs a) {
+    __shared__ cplx<real> fftbuf[kBwdFrames][kHalf];
+    __shared__ float contrib[kBwdFrames][kNfft];
+    __shared__ double gm[kBands];
+    __shared__ float gband[kBwdFrames][kBands];
+    __shared__ double scratch[kBwdFrames];
+
+    const ModelTable &t = *a.tab;
+    const PipeLayout &L = a.L;
+    const int i = blockIdx.x / L.nhoptile;       // gradient row index
+    const int ht = blockIdx.x - i * L.nhoptile;
+    const int row = L.row0 + i;                  // stacked row
+    const int item = row % L.batch;
+    const bool is_ref = row < L.batch;
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int64_t j0 = int64_t(ht) * kBwdHops;   // first output hop block
+
+    // adjoint of the band power ratio and its clamp, then of the mean band powers
+    if (wave == 0 && lane < kBands) {
+        const double *gp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
+        double g = 0.0;
+        for (int k = 0; k < L.ntile; ++k) g += gp[k * kBands + lane];
+        const double ratio = band_array(a, kRatio)[item * kBands + lane];
+        const double mref = band_array(a, kMref)[item * kBands + lane];
+        const double gr = (ratio >= 0.01 && ratio <= 100.0) ? g : 0.0;
+        const double inv = 1.0 / (mref + 1000.0);
+        gm[lane] = (is_ref ? -gr * ratio * inv : gr * inv) / static_cast<double>(L.frames);
+    }
+    __syncthreads();
+
+    const double scale = region<double>(a.ws, L.rowconst)[int64_t(row) * 4 + 2];
+    const float *p = region<float>(a.ws, L.p) + int64_t(row) * L.len;
+    const int64_t frame = j0 - 1 + wave;
+    cplx<real> *buf = fftbuf[wave];
+    if (frame >= 0 && frame < L.frames) {
+        const int64_t fo = frame * kBands;
+        if (lane < kBands) {
+            const float *bk = region<float>(a.ws, L.bark) + int64_t(row) * L.frames * kBands;
+            const float *gbk = region<float>(a.bw, L.gbark) + int64_t(row) * L.frames * kBands;
+            const float keep = region<float>(a.ws, L.keep)[int64_t(item) * L.frames + frame];
+            double g = gbk[fo + lane];
+            if (keep != 0.0f && static_cast<double>(bk[fo + lane]) > 100.0 * t.threshs[lane]) {
+                g += gm[lane];
+            }
+            gband[wave][lane] = static_cast<float>(g * t.corr[lane]);
+        }
+        wave_lds_fence();
+        const int64_t start = frame * kHop;
+        auto u = [&](int k) -> real {
+            const int64_t n = start + k;
+            return n < L.len ? static_cast<real>(p[n]) * static_cast<real>(t.window[k]) : real(0);
+        };
+        cplx<real> x[4];
+        frame_spectrum<real>(u, x, buf, t.tw256, t.tw512, lane);
+        cplx<real> v[4];
+        const real s = static_cast<real>(scale);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int fbin = lane + 64 * r;
+            const int band = t.bin_band[fbin];
+            const real gpw = band >= 0 ? static_cast<real>(gband[wave][band]) * s : real(0);
+            v[r] = {gpw * x[r].re, gpw * x[r].im};
+        }
+        real ev[4], od[4];
+        frame_adjoint<real>(v, ev, od, buf, t.tw256, t.tw512, lane);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int n = lane + 64 * r;
+            contrib[wave][2 * n] = static_cast<float>(ev[r] * static_cast<real>(t.window[2 * n]));
+            contrib[wave][2 * n + 1] =
+                static_cast<float>(od[r] * static_cast<real>(t.window[2 * n + 1]));
+        }
+    } else {
+        for (int k = lane; k < kNfft; k += kWave) contrib[wave][k] = 0.0f;
+    }
+    __syncthreads();
+
+    // overlap-add: hop block j0 + q receives frames j0 + q - 1 (second half) and j0 + q
+    float *gp_out = region<float>(a.bw, L.gp) + int64_t(i) * L.len;
+    double acc = 0.0;
+    for (int k = threadIdx.x; k < kBwdHops * kHop; k += blockDim.x) {
+        const int q = k / kHop, m = k % kHop;
+        const int64_t n = (j0 + q) * kHop + m;
+        if (n >= L.len) continue;
+        const double g = static_cast<double>(contrib[q][kHop + m]) + static_cast<double>(contrib[q + 1][m]);
+        gp_out[n] = static_cast<float>(g);
+        acc += g * static_cast<double>(p[n]);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) scratch[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double s = 0.0;
+        for (int w = 0; w < kBwdFrames; ++w) s += scratch[w];
+        region<double>(a.bw, L.spart)[int64_t(i) * L.nhoptile + ht] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host entry points
+// ---------------------------------------------------------------------------
+
+// FFT arithmetic of the STFT kernels.  float64 costs no measurable time on
+// gfx950 (both kernels are latency bound, float64 FMA issues at the float32
+// rate with packed float32 disabled) and cuts the spectral rounding error.
+#ifndef PESQ_STFT_REAL
+#define PESQ_STFT_REAL double
+#endif
+using StftReal = PESQ_STFT_REAL;
+
+static int check_sizes(int64_t batch, int64_t len, const PipeLayout &L) {
+    PESQ_CHECK_ARG(batch > 0, "batch must be positive, got %lld", (long long)batch);
+    PESQ_CHECK_ARG(len >= 15, "the edge ramp needs at least 15 samples, got %lld", (long long)len);
+    PESQ_CHECK_ARG(L.frames >= kWin,
+                   "The PESQ chain needs at least 20 frames for the overlapping sums, got %lld",
+                   (long long)L.frames);
+    PESQ_CHECK_ARG(2 * batch * L.nblk < (int64_t(1) << 31) && 2 * batch * L.ntile < (int64_t(1) << 31),
+                   "problem too large for one launch");
+    return PESQ_OK;
+}
+
+}  // namespace pesq
+
+using namespace pesq;
+
+extern "C" int pesq_pipeline_forward_workspace(int64_t batch, int64_t len, int grad_mask,
+                                               size_t *bytes) {
+    PipeLayout L;
+    L.build(batch, len, grad_mask);
+    if (int st = check_sizes(batch, len, L)) return st;
+    *bytes = L.fwd_bytes;
+    return PESQ_OK;
+}
+
+extern "C" int pesq_pipeline_backward_workspace(int64_t batch, int64_t len, int grad_mask,
+                                                size_t *bytes) {
+    PipeLayout L;
+    L.build(batch, len, grad_mask);
+    if (int st = check_sizes(batch, len, L)) return st;
+    *bytes = L.bwd_bytes;
+    return PESQ_OK;
+}
+
+extern "C" int pesq_pipeline_region(int64_t batch, int64_t len, int grad_mask, const char *name,
+                                    size_t *offset, size_t *bytes) {
+    PipeLayout L;
+    L.build(batch, len, grad_mask);
+    PESQ_CHECK_ARG(name != nullptr && L.region(name, offset, bytes), "unknown region %s",
+                   name ? name : "(null)");
+    return PESQ_OK;
+}
+
+extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, int64_t batch,
+                                            int64_t len, const void *model_table, double factor,
+                                            int grad_mask, float *d_symm, float *d_asymm,
+                                            float *mos, float *loss, void *fwd_workspace,
+                                            unsigned stages, hipStream_t stream) {
+    PipeArgs a{};
+    a.L.build(batch, len, grad_mask);
+    if (int st = check_sizes(batch, len, a.L)) return st;
+    PESQ_CHECK_ARG(ref && deg && model_table && fwd_workspace && d_symm && d_asymm && mos && loss,
+                   "null pointer argument");
+    PESQ_CHECK_ARG((grad_mask & ~3) == 0, "invalid grad_mask %d", grad_mask);
+    a.tab = static_cast<const ModelTable *>(model_table);
+    a.ref = ref;
+    a.deg = deg;
+    a.ws = static_cast<unsigned char *>(fwd_workspace);
+    a.factor = factor;
+    a.d_symm = d_symm;
+    a.d_asymm = d_asymm;
+    a.mos = mos;
+    a.loss = loss;
+    const PipeLayout &L = a.L;
+    const IirTable *iir = &a.tab->iir;
+
+    PipeFwdMode m{};
+    m.ref = ref;
+    m.deg = deg;
+    m.p = region<float>(a.ws, L.p);
+    m.f = grad_mask ? region<float>(a.ws, L.f) : nullptr;
+    m.peak = region<float>(a.ws, L.peak);
+    m.peak_in = m.peak;
+    m.energy = region<double>(a.ws, L.energy);
+    m.len = len;
+    m.batch = static_cast<int>(batch);
+    m.nblk = static_cast<int>(L.nblk);
+    m.row0 = static_cast<int>(L.row0);
+    m.nrg = static_cast<int>(L.nrg);
+    double *aggr = region<double>(a.ws, L.aggr);
+    const unsigned grid_iir = static_cast<unsigned>(L.rows * L.nblk);
+
+    if (stages & 1u) {
+        hipLaunchKernelGGL((iir_aggregate_kernel<kPowerSections, kPreSections, PipeFwdMode>),
+                           dim3(grid_iir), dim3(kWave * kWaves), 0, stream, m, iir, aggr, len,
+                           static_cast<int>(L.nblk));
+        PESQ_CHECK_LAUNCH("pipeline iir aggregate");
+    }
+    if (stages & 2u) {
+        hipLaunchKernelGGL((iir_output_kernel<kPowerSections, kPreSections, PipeFwdMode>),
+                           dim3(grid_iir), dim3(kWave * kWaves), 0, stream, m, iir,
+                           static_cast<const double *>(aggr), len, static_cast<int>(L.nblk));
+        PESQ_CHECK_LAUNCH("pipeline iir output");
+    }
+    if (stages & 4u) {
+        hipLaunchKernelGGL(stft_fwd_kernel<StftReal>, dim3(static_cast<unsigned>(batch * L.ntile)),
+                           dim3(kWave * kStftWaves), 0, stream, a);
+        PESQ_CHECK_LAUNCH("pipeline stft");
+    }
+    if (stages & 8u) {
+        hipLaunchKernelGGL(chain_fwd_kernel, dim3(static_cast<unsigned>(batch * L.ntile)),
+                           dim3(kWave * kChainWaves), 0, stream, a);
+        PESQ_CHECK_LAUNCH("pipeline chain");
+    }
+    if (stages & 16u) {
+        hipLaunchKernelGGL(chain_final_kernel, dim3(static_cast<unsigned>(batch)),
+                           dim3(kFinalThreads), 0, stream, a);
+        PESQ_CHECK_LAUNCH("pipeline chain final");
+    }
+    return PESQ_OK;
+}
+
+extern "C" int pesq_pipeline_forward(const float *ref, const float *deg, int64_t batch,
+                                     int64_t len, const void *model_table, double factor,
+                                     int grad_mask, float *d_symm, float *d_asymm, float *mos,
+                                     float *loss, void *fwd_workspace, hipStream_t stream) {
+    return pesq_pipeline_forward_stages(ref, deg, batch, len, model_table, factor, grad_mask,
+                                        d_symm, d_asymm, mos, loss, fwd_workspace, 0x1Fu, stream);
+}
+
+extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g_asymm,
+                                             const float *g_mos, const float *g_loss,
+                                             int64_t batch, int64_t len, const void *model_table,
+                                             double factor, int grad_mask, float *g_ref,
+                                             float *g_deg, const void *fwd_workspace,
+                                             void *bwd_workspace, unsigned stages,
+                                             hipStream_t stream) {
+    PipeArgs a{};
+    a.L.build(batch, len, grad_mask);
+    if (int st = check_sizes(batch, len, a.L)) return st;
+    PESQ_CHECK_ARG(grad_mask >= 1 && grad_mask <= 3, "backward needs a non-empty grad_mask");
+    PESQ_CHECK_ARG(!(grad_mask & PESQ_GRAD_REF) || g_ref, "g_ref is required by grad_mask");
+    PESQ_CHECK_ARG(!(grad_mask & PESQ_GRAD_DEG) || g_deg, "g_deg is required by grad_mask");
+    PESQ_CHECK_ARG(model_table && fwd_workspace && bwd_workspace, "null pointer argument");
+    a.tab = static_cast<const ModelTable *>(model_table);
+    a.ws = static_cast<unsigned char *>(const_cast<void *>(fwd_workspace));
+    a.bw = static_cast<unsigned char *>(bwd_workspace);
+    a.factor = factor;
+    a.g_symm = g_symm;
+    a.g_asymm = g_asymm;
+    a.g_mos = g_mos;
+    a.g_loss = g_loss;
+    const PipeLayout &L = a.L;
+    const IirTable *iir = &a.tab->iir;
+
+    if (stages & 1u) {
+        hipLaunchKernelGGL(chain_bwd_kernel, dim3(static_cast<unsigned>(batch * L.ntile)),
+                           dim3(kWave * kChainWaves), 0, stream, a);
+        PESQ_CHECK_LAUNCH("pipeline chain backward");
+    }
+    if (stages & 2u) {
+        hipLaunchKernelGGL(stft_bwd_kernel<StftReal>,
+                           dim3(static_cast<unsigned>(L.nrg * L.nhoptile)),
+                           dim3(kWave * kBwdFrames), 0, stream, a);
+        PESQ_CHECK_LAUNCH("pipeline stft backward");
+    }
+
+    PipeBwdMode m{};
+    m.f = region<float>(a.ws, L.f);
+    m.gp = region<float>(a.bw, L.gp);
+    m.rowconst = region<double>(a.ws, L.rowconst);
+    m.spart = region<double>(a.bw, L.spart);
+    m.g_ref = g_ref;
+    m.g_deg = g_deg;
+    m.len = len;
+    m.batch = static_cast<int>(batch);
+    m.row0 = static_cast<int>(L.row0);
+    m.nhoptile = static_cast<int>(L.nhoptile);
+    double *aggr = region<double>(a.bw, L.aggr_b);
+    const unsigned grid_iir = static_cast<unsigned>(L.nrg * L.nblk);
+    if (stages & 4u) {
+        hipLaunchKernelGGL((iir_aggregate_kernel<kPowerSections, kPreSections, PipeBwdMode>),
+                           dim3(grid_iir), dim3(kWave * kWaves), 0, stream, m, iir, aggr, len,
+                           static_cast<int>(L.nblk));
+        PESQ_CHECK_LAUNCH("pipeline iir aggregate (adjoint)");
+    }
+    if (stages & 8u) {
+        hipLaunchKernelGGL((iir_output_kernel<kPowerSections, kPreSections, PipeBwdMode>),
+                           dim3(grid_iir), dim3(kWave * kWaves), 0, stream, m, iir,
+                           static_cast<const double *>(aggr), len, static_cast<int>(L.nblk));
+        PESQ_CHECK_LAUNCH("pipeline iir output (adjoint)");
+    }
+    return PESQ_OK;
+}
+
+extern "C" int pesq_pipeline_backward(const float *g_symm, const float *g_asymm,
+                                      const float *g_mos, const float *g_loss, int64_t batch,
+                                      int64_t len, const void *model_table, double factor,
+                                      int grad_mask, float *g_ref, float *g_deg,
+                                      const void *fwd_workspace, void *bwd_workspace,
+                                      hipStream_t stream) {
+    return pesq_pipeline_backward_stages(g_symm, g_asymm, g_mos, g_loss, batch, len, model_table,
+                                         factor, grad_mask, g_ref, g_deg, fwd_workspace,
+                                         bwd_workspace, 0xFu, stream);
+}

@@ -1,0 +1,109 @@
+// Workspace layout of the fused pipeline (host and device agree on it).
+#pragma once
+
+#include <cstring>
+
+#include "common.hpp"
+#include "iir.hpp"
+#include "spectral.hpp"
+
+namespace pesq {
+
+constexpr int kTile = 16;          // frames per workgroup of the STFT / chain kernels
+constexpr int kBwdFrames = 8;      // frames per workgroup of the STFT backward
+constexpr int kBwdHops = kBwdFrames - 1;  // output hop blocks per such workgroup
+constexpr int kWin = 20;           // PSQM window (frames)
+constexpr int kStride = 10;        // PSQM stride (frames)
+
+// per frame chain arrays, [batch, frames] each
+enum FrameArray { kTaer, kTad, kFpr0, kFpr1, kH, kSymmRaw, kAsymmRaw, kSymm, kAsymm, kFrameArrays };
+// per band chain arrays, [batch, bands] each
+enum BandArray { kR, kRatio, kMref, kBandArrays };
+
+struct PipeLayout {
+    int64_t batch = 0, len = 0, rows = 0, frames = 0;
+    int64_t nblk = 0, ntile = 0, nhoptile = 0, nwin = 0;
+    int64_t row0 = 0, nrg = 0;  // stacked rows that receive gradients
+    int grad_mask = 0;
+
+    // forward workspace
+    size_t aggr = 0, peak = 0, energy = 0, p = 0, f = 0, rowconst = 0, bark = 0, keep = 0;
+    size_t bandref = 0, banddeg = 0, frame = 0, band = 0, psqm = 0, dist = 0, fwd_bytes = 0;
+    // backward workspace
+    size_t gbark = 0, grpart = 0, gp = 0, spart = 0, aggr_b = 0, bwd_bytes = 0;
+
+    static size_t align(size_t v) { return (v + 255) & ~size_t(255); }
+
+    static int64_t frames_for(int64_t len) {
+        const int64_t padded = len + len % 256;
+        return padded < kNfft ? 0 : 1 + (padded - kNfft) / kHop;
+    }
+
+    void build(int64_t b, int64_t n, int mask) {
+        batch = b;
+        len = n;
+        rows = 2 * b;
+        grad_mask = mask;
+        frames = frames_for(n);
+        nblk = cdiv(n, kBlockSpan);
+        ntile = cdiv(frames, kTile);
+        nhoptile = cdiv(cdiv(n, kHop), kBwdHops);
+        nwin = frames >= kWin ? (frames - kWin) / kStride + 1 : 0;
+        row0 = (mask & PESQ_GRAD_REF) ? 0 : b;
+        nrg = mask == (PESQ_GRAD_REF | PESQ_GRAD_DEG) ? 2 * b : (mask ? b : 0);
+
+        constexpr int nstate = 2 * (kMaxSections);  // generous: 2 states x 8 sections
+        size_t off = 0;
+        auto take = [&](size_t &field, size_t bytes) {
+            field = off;
+            off = align(off + bytes);
+        };
+        take(aggr, size_t(rows) * nblk * nstate * sizeof(double));
+        take(peak, size_t(rows) * nblk * sizeof(float));
+        take(energy, size_t(rows) * nblk * sizeof(double));
+        take(p, size_t(rows) * len * sizeof(float));
+        take(f, size_t(nrg) * len * sizeof(float));
+        take(rowconst, size_t(rows) * 4 * sizeof(double));
+        take(bark, size_t(rows) * frames * kBands * sizeof(float));
+        take(keep, size_t(batch) * frames * sizeof(float));
+        take(bandref, size_t(batch) * ntile * kBands * sizeof(double));
+        take(banddeg, size_t(batch) * ntile * kBands * sizeof(double));
+        take(frame, size_t(kFrameArrays) * batch * frames * sizeof(double));
+        take(band, size_t(kBandArrays) * batch * kBands * sizeof(double));
+        take(psqm, size_t(2) * batch * nwin * sizeof(double));
+        take(dist, size_t(batch) * 2 * sizeof(double));
+        fwd_bytes = off;
+
+        off = 0;
+        take(gbark, size_t(rows) * frames * kBands * sizeof(float));
+        take(grpart, size_t(batch) * ntile * kBands * sizeof(double));
+        take(gp, size_t(nrg) * len * sizeof(float));
+        take(spart, size_t(nrg) * nhoptile * sizeof(double));
+        take(aggr_b, size_t(nrg) * nblk * nstate * sizeof(double));
+        bwd_bytes = off;
+    }
+
+    bool region(const char *name, size_t *offset, size_t *bytes) const {
+        struct Entry {
+            const char *name;
+            size_t off, end;
+        };
+        const Entry table[] = {
+            {"aggr", aggr, peak},       {"peak", peak, energy},     {"energy", energy, p},
+            {"p", p, f},                {"f", f, rowconst},         {"rowconst", rowconst, bark},
+            {"bark", bark, keep},       {"keep", keep, bandref},    {"bandref", bandref, banddeg},
+            {"banddeg", banddeg, frame}, {"frame", frame, band},    {"band", band, psqm},
+            {"psqm", psqm, dist},       {"dist", dist, fwd_bytes},
+        };
+        for (const Entry &e : table) {
+            if (std::strcmp(e.name, name) == 0) {
+                *offset = e.off;
+                *bytes = e.end - e.off;
+                return true;
+            }
+        }
+        return false;
+    }
+};
+
+}  // namespace pesq

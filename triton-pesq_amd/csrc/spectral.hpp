@@ -1,0 +1,153 @@
+// Framed 512 point real FFT for the STFT / Bark stage, one wavefront per frame.
+//
+// A 512 point real frame u is folded into the 256 point complex sequence
+// z_n = u_{2n} + i u_{2n+1}; Z = FFT256(z) is computed by a radix-4 Stockham
+// autosort FFT (4 passes) whose 64 butterflies per pass are the 64 lanes of
+// the wavefront, with the sequence held in a wave-private LDS buffer.  The
+// half spectrum follows from
+//     X_f = (Z_f + conj Z_{256-f}) / 2 - i e^{-2 pi i f / 512} (Z_f - conj Z_{256-f}) / 2.
+// The backward pass needs the adjoint g_u_k = sum_f V_f e^{+2 pi i f k / 512}
+// of a Hermitian V (V_f = gP_f X_f for f = 1..255, zero at DC and Nyquist),
+// obtained from the inverse of the same fold:
+//     Z'_f = (V_f + conj V_{256-f}) + i e^{+2 pi i f / 512} (V_f - conj V_{256-f}),
+//     z = IFFT256(Z') (unnormalised),  g_u_{2n} = Re z_n,  g_u_{2n+1} = Im z_n.
+#pragma once
+
+#include "common.hpp"
+
+namespace pesq {
+
+constexpr int kNfft = 512;
+constexpr int kHop = 256;
+constexpr int kHalf = 256;
+constexpr int kBands = 49;
+
+template <typename real>
+struct cplx {
+    real re, im;
+};
+
+template <typename real>
+__device__ __forceinline__ cplx<real> cmul(cplx<real> a, cplx<real> b) {
+    return {a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re};
+}
+
+// radix-4 DFT of v[0..3]; forward uses e^{-2 pi i / 4} = -i
+template <typename real, bool kInverse>
+__device__ __forceinline__ void dft4(cplx<real> (&v)[4]) {
+    const cplx<real> a0 = {v[0].re + v[2].re, v[0].im + v[2].im};
+    const cplx<real> a1 = {v[0].re - v[2].re, v[0].im - v[2].im};
+    const cplx<real> a2 = {v[1].re + v[3].re, v[1].im + v[3].im};
+    const cplx<real> d = {v[1].re - v[3].re, v[1].im - v[3].im};
+    // forward: a3 = -i d, inverse: a3 = +i d
+    const cplx<real> a3 = kInverse ? cplx<real>{-d.im, d.re} : cplx<real>{d.im, -d.re};
+    v[0] = {a0.re + a2.re, a0.im + a2.im};
+    v[2] = {a0.re - a2.re, a0.im - a2.im};
+    v[1] = {a1.re + a3.re, a1.im + a3.im};
+    v[3] = {a1.re - a3.re, a1.im - a3.im};
+}
+
+// The wavefront's lanes only touch their own LDS buffer; LDS accesses of one
+// wavefront complete in program order, so a compiler level barrier between
+// the read and the write phases of a pass is all the ordering needed.
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// In: v[r] = z_{lane + 64 r}.  Out: buf[n] = Z_n (natural order), unnormalised.
+// tw[m] = e^{-2 pi i m / 256}.
+template <typename real, bool kInverse>
+__device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, const double2 *tw,
+                                       int lane) {
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        const int ns = 1 << (2 * pass);
+        if (pass > 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[r] = buf[lane + 64 * r];
+            wave_lds_fence();
+        }
+        const int k = lane & (ns - 1);
+#pragma unroll
+        for (int r = 1; r < 4; ++r) {
+            const double2 w = tw[(k * r * (64 / ns)) & 255];
+            const cplx<real> c = {static_cast<real>(w.x),
+                                  static_cast<real>(kInverse ? -w.y : w.y)};
+            v[r] = cmul(v[r], c);
+        }
+        dft4<real, kInverse>(v);
+        const int base = (lane / ns) * ns * 4 + k;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) buf[base + r * ns] = v[r];
+        wave_lds_fence();
+    }
+}
+
+// Spectrum of one frame: X_f for f = lane + 64 r (r = 0..3), given the frame
+// samples u (already windowed) through the load functor u(k), k < 512.
+// tw512[f] = e^{-2 pi i f / 512}.
+template <typename real, class Load>
+__device__ __forceinline__ void frame_spectrum(Load u, cplx<real> (&x)[4], cplx<real> *buf,
+                                               const double2 *tw256, const double2 *tw512,
+                                               int lane) {
+    cplx<real> v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int n = lane + 64 * r;
+        v[r] = {u(2 * n), u(2 * n + 1)};
+    }
+    fft256<real, false>(v, buf, tw256, lane);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int f = lane + 64 * r;
+        const cplx<real> zf = buf[f];
+        const cplx<real> zm = buf[(kHalf - f) & (kHalf - 1)];
+        // E = (Zf + conj Zm) / 2,  O = -i (Zf - conj Zm) / 2
+        const cplx<real> e = {(zf.re + zm.re) * real(0.5), (zf.im - zm.im) * real(0.5)};
+        const cplx<real> o = {(zf.im + zm.im) * real(0.5), -(zf.re - zm.re) * real(0.5)};
+        const double2 w = tw512[f];
+        const cplx<real> c = {static_cast<real>(w.x), static_cast<real>(w.y)};
+        const cplx<real> t = cmul(c, o);
+        x[r] = {e.re + t.re, e.im + t.im};
+    }
+    wave_lds_fence();
+}
+
+// Adjoint: given V_f for f = lane + 64 r (zero at f = 0), returns g_u_{2n} and
+// g_u_{2n+1} for n = lane + 64 r in (even[r], odd[r]).  V_256 is zero.
+template <typename real>
+__device__ __forceinline__ void frame_adjoint(const cplx<real> (&vf)[4], real (&even)[4],
+                                              real (&odd)[4], cplx<real> *buf,
+                                              const double2 *tw256, const double2 *tw512,
+                                              int lane) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) buf[lane + 64 * r] = vf[r];
+    wave_lds_fence();
+    cplx<real> v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int f = lane + 64 * r;
+        const cplx<real> a = vf[r];
+        // V_{256 - f}; f = 0 pairs with the Nyquist bin, which is zero
+        const cplx<real> b = f == 0 ? cplx<real>{real(0), real(0)} : buf[kHalf - f];
+        const cplx<real> s = {a.re + b.re, a.im - b.im};   // V_f + conj V_{256-f}
+        const cplx<real> d = {a.re - b.re, a.im + b.im};   // V_f - conj V_{256-f}
+        const double2 w = tw512[f];
+        const cplx<real> c = {static_cast<real>(w.x), static_cast<real>(-w.y)};  // e^{+...}
+        const cplx<real> t = cmul(c, d);
+        // Z' = s + i t
+        v[r] = {s.re - t.im, s.im + t.re};
+    }
+    wave_lds_fence();
+    fft256<real, true>(v, buf, tw256, lane);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const cplx<real> z = buf[lane + 64 * r];
+        even[r] = z.re;
+        odd[r] = z.im;
+    }
+    wave_lds_fence();
+}
+
+}  // namespace pesq

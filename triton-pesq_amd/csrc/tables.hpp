@@ -1,0 +1,32 @@
+// Device layout of the constant tables.  Built on the host by
+// pesq_model_table_pack / pesq_iir_table_pack (capi.cpp) from the plain C
+// structs of pesq_hip.h, copied to device memory by the caller.
+#pragma once
+
+#include "iir.hpp"
+#include "spectral.hpp"
+
+namespace pesq {
+
+struct ModelTable {
+    IirTable iir;                 // A = level alignment band pass, B = pre-emphasis
+    double2 tw256[kHalf];         // e^{-2 pi i m / 256}
+    double2 tw512[kHalf];         // e^{-2 pi i f / 512}
+    float window[kNfft];          // analysis window, centred in n_fft taps
+    int32_t band_start[kBands];   // first bin of band i
+    int32_t band_end[kBands];     // one past the last bin of band i
+    int32_t bin_band[kHalf];      // band owning bin f, -1 if none (bin 0 is -1)
+    double corr[kBands];          // power density correction per band
+    double threshs[kBands];       // hearing thresholds
+    double exps[kBands];          // Zwicker exponents
+    double loud_scale[kBands];    // sl (2 th)^e
+    double width[kBands];         // band widths in Bark
+    double total_width;           // sum of widths of bands 1..
+    double sl;                    // loudness calibration constant
+    int32_t nbarks;
+    int32_t n_fft;
+    int32_t hop;
+    int32_t pad;
+};
+
+}  // namespace pesq

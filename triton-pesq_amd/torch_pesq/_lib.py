@@ -1,0 +1,165 @@
+"""ctypes binding of the HIP library's C ABI (``include/pesq_hip.h``).
+
+The shared object is ``torch_pesq/_lib/libpesq_hip.so``, built in-tree by
+``triton-pesq_amd/build.py``.  There is no fallback: every GPU operator of the
+package calls through this library and fails with a descriptive error when it
+is missing.
+"""
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+__all__ = [
+    "IirSections",
+    "ModelConstants",
+    "library",
+    "check",
+    "stream_handle",
+    "MAX_SECTIONS",
+    "GRAD_REF",
+    "GRAD_DEG",
+]
+
+MAX_SECTIONS = 8
+NBARKS = 49
+NFFT = 512
+GRAD_REF = 1
+GRAD_DEG = 2
+
+LIB_PATH = Path(os.environ.get("PESQ_HIP_LIB", Path(__file__).with_name("_lib") / "libpesq_hip.so"))
+
+c_double8 = ctypes.c_double * MAX_SECTIONS
+
+
+class IirSections(ctypes.Structure):
+    """``pesq_iir_sections``: a filter in parallel biquad form."""
+
+    _fields_ = [
+        ("count", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("c0", ctypes.c_double),
+        ("b0", c_double8),
+        ("b1", c_double8),
+        ("b2", c_double8),
+        ("a1", c_double8),
+        ("a2", c_double8),
+    ]
+
+
+class ModelConstants(ctypes.Structure):
+    """``pesq_model_constants``: every constant of the PESQ model."""
+
+    _fields_ = [
+        ("power_filter", IirSections),
+        ("pre_filter", IirSections),
+        ("window", ctypes.c_float * NFFT),
+        ("band_start", ctypes.c_int32 * NBARKS),
+        ("band_end", ctypes.c_int32 * NBARKS),
+        ("corr", ctypes.c_double * NBARKS),
+        ("threshs", ctypes.c_double * NBARKS),
+        ("exps", ctypes.c_double * NBARKS),
+        ("width", ctypes.c_double * NBARKS),
+        ("total_width", ctypes.c_double),
+        ("sl", ctypes.c_double),
+        ("nbarks", ctypes.c_int32),
+        ("n_fft", ctypes.c_int32),
+        ("hop", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+_SIZE_P = ctypes.POINTER(ctypes.c_size_t)
+
+#: name -> (restype, argtypes) of every exported entry point
+SIGNATURES = {
+    "pesq_abi_version": (_INT, []),
+    "pesq_last_error": (ctypes.c_char_p, []),
+    "pesq_iir_table_bytes": (ctypes.c_size_t, []),
+    "pesq_iir_table_pack": (_INT, [ctypes.POINTER(IirSections), _P]),
+    "pesq_model_table_bytes": (ctypes.c_size_t, []),
+    "pesq_model_table_pack": (_INT, [ctypes.POINTER(ModelConstants), _P]),
+    "pesq_pipeline_forward_workspace": (_INT, [_I64, _I64, _INT, _SIZE_P]),
+    "pesq_pipeline_backward_workspace": (_INT, [_I64, _I64, _INT, _SIZE_P]),
+    "pesq_pipeline_region": (_INT, [_I64, _I64, _INT, ctypes.c_char_p, _SIZE_P, _SIZE_P]),
+    "pesq_pipeline_forward": (
+        _INT,
+        [_P, _P, _I64, _I64, _P, ctypes.c_double, _INT, _P, _P, _P, _P, _P, _P],
+    ),
+    "pesq_pipeline_backward": (
+        _INT,
+        [_P, _P, _P, _P, _I64, _I64, _P, ctypes.c_double, _INT, _P, _P, _P, _P, _P],
+    ),
+    "pesq_pipeline_forward_stages": (
+        _INT,
+        [_P, _P, _I64, _I64, _P, ctypes.c_double, _INT, _P, _P, _P, _P, _P, ctypes.c_uint, _P],
+    ),
+    "pesq_pipeline_backward_stages": (
+        _INT,
+        [_P, _P, _P, _P, _I64, _I64, _P, ctypes.c_double, _INT, _P, _P, _P, _P, ctypes.c_uint, _P],
+    ),
+    "pesq_iir_workspace": (_INT, [_I64, _I64, _SIZE_P]),
+    "pesq_iir_apply": (_INT, [_P, _P, _I64, _I64, _P, _INT, _INT, _P, _P]),
+    "pesq_resample_forward": (
+        _INT,
+        [_P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    ),
+    "pesq_resample_backward": (
+        _INT,
+        [_P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    ),
+}
+
+_LIB = None
+
+
+def library():
+    """The loaded library; raises ``RuntimeError`` when it is not built."""
+
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"The PESQ HIP library is not built ({LIB_PATH} is missing). Run "
+                "`python triton-pesq_amd/build.py` (or `__graft_entry__.build()`)."
+            )
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _LIB = lib
+    return _LIB
+
+
+def check(status: int, what: str = "") -> None:
+    """Turn a non-zero status into a ``RuntimeError`` with the library's message."""
+
+    if status == 0:
+        return
+    message = library().pesq_last_error().decode(errors="replace")
+    prefix = f"{what}: " if what else ""
+    raise RuntimeError(f"{prefix}{message} (status {status})")
+
+
+def stream_handle(device: torch.device) -> ctypes.c_void_p:
+    """Raw ``hipStream_t`` of the current PyTorch stream on ``device``."""
+
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(tensor) -> ctypes.c_void_p:
+    """Device pointer of a tensor, or NULL for ``None``."""
+
+    return ctypes.c_void_p(0 if tensor is None else tensor.data_ptr())
+
+
+def size_query(fn, *args) -> int:
+    out = ctypes.c_size_t(0)
+    check(fn(*args, ctypes.byref(out)), fn.__name__)
+    return int(out.value)

@@ -1,0 +1,57 @@
+"""``PesqLossHip``: the drop-in for ``PesqLossTriton`` (``torch_pesq/triton_ops/loss.py:18-215``).
+
+Same module as :class:`torch_pesq.loss.PesqLoss` plus :meth:`graphed`, which
+captures forward and backward into HIP graphs for one input shape.
+"""
+
+import torch
+
+from ..loss import PesqLoss
+
+__all__ = ["PesqLossHip", "PesqLossTriton"]
+
+
+class PesqLossHip(PesqLoss):
+    """PESQ loss on HIP kernels with HIP graph capture."""
+
+    def graphed(self, ref: torch.Tensor, deg: torch.Tensor):
+        """Capture the loss in a HIP graph, specialised to one input shape.
+
+        Mirrors ``triton_ops/loss.py:149-201``: detached sample copies with the
+        same ``requires_grad`` flags, one warm-up on a side stream (nothing is
+        tuned at run time here, the warm-up only settles the allocator), then
+        ``torch.cuda.make_graphed_callables``.  The returned callable replaces
+        ``self.__call__`` for this shape and these flags, and is bit exact with
+        the eager path.  Unlike the reference, ``self`` is left untouched (the
+        graph is captured through a thin wrapper), so the module keeps working
+        for other shapes.
+        """
+
+        sample = tuple(t.detach().clone().requires_grad_(t.requires_grad) for t in (ref, deg))
+        target = _LossCall(self)
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            output = target(*sample)
+            if output.requires_grad:
+                torch.autograd.grad(output.sum(), [t for t in sample if t.requires_grad])
+        torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+        return torch.cuda.make_graphed_callables(target, sample)
+
+
+class _LossCall(torch.nn.Module):
+    """``loss(ref, deg)`` of a :class:`PesqLossHip` as a capturable module."""
+
+    def __init__(self, loss: PesqLossHip):
+        super().__init__()
+        # a plain attribute, not a submodule: the capture must not see (and
+        # re-register) the loss module's constant parameters
+        object.__setattr__(self, "loss", loss)
+
+    def forward(self, ref: torch.Tensor, deg: torch.Tensor) -> torch.Tensor:
+        return self.loss(ref, deg)
+
+
+#: the reference's name for the GPU backend class
+PesqLossTriton = PesqLossHip

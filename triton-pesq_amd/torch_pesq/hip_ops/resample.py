@@ -1,0 +1,168 @@
+"""HIP polyphase resampler, the ``TritonResample`` operator (``resample.py:442-574``).
+
+Same constructor and attributes as the reference (``kernel``, ``kernel_t``
+is not needed, ``width``, ``orig_step``, ``new_step``).  Forward and adjoint
+are HIP kernels (``csrc/resample.hip``) that evaluate only the non-zero taps
+of each phase; the adjoint is itself differentiable (its derivative is the
+forward), which gives a working double backward like the reference's
+``_ResampleAdjoint`` (``resample.py:381-410``).
+"""
+
+import math
+from typing import Optional
+
+import torch
+
+from .. import _lib
+from ._common import check_input
+from .sinc import resample_length, sinc_resample_kernel
+
+__all__ = ["HipResample"]
+
+_INDEX_LIMIT = 2**31 - 1
+
+
+def _launch(fn_name, src, n_out_or_in, module, forward: bool):
+    lib = _lib.library()
+    rows = src.shape[0]
+    if forward:
+        n_in, n_out = src.shape[1], n_out_or_in
+        out = torch.empty((rows, n_out), dtype=torch.float32, device=src.device)
+        lo, hi = module.tap_lo, module.tap_hi
+    else:
+        n_out, n_in = src.shape[1], n_out_or_in
+        out = torch.empty((rows, n_in), dtype=torch.float32, device=src.device)
+        lo, hi = module.phase_lo, module.phase_hi
+    with torch.cuda.device(src.device):
+        _lib.check(
+            getattr(lib, fn_name)(
+                _lib.ptr(src),
+                _lib.ptr(out),
+                rows,
+                n_in,
+                n_out,
+                _lib.ptr(module.kernel),
+                _lib.ptr(lo),
+                _lib.ptr(hi),
+                module.orig_step,
+                module.new_step,
+                module.width,
+                module.kernel.shape[1],
+                _lib.stream_handle(src.device),
+            ),
+            fn_name,
+        )
+    return out
+
+
+class _ResampleAdjoint(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, grad_out, module, n_in):
+        ctx.module, ctx.n_out = module, grad_out.shape[1]
+        return _launch("pesq_resample_backward", grad_out.contiguous(), n_in, module, False)
+
+    @staticmethod
+    def backward(ctx, grad_grad):
+        if not ctx.needs_input_grad[0]:
+            return None, None, None
+        out = _launch("pesq_resample_forward", grad_grad.contiguous(), ctx.n_out, ctx.module, True)
+        return out, None, None
+
+
+class _ResampleFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, waveform, module, n_out):
+        ctx.module, ctx.n_in = module, waveform.shape[1]
+        return _launch("pesq_resample_forward", waveform, n_out, module, True)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        if not ctx.needs_input_grad[0]:
+            return None, None, None
+        return _ResampleAdjoint.apply(grad_out, ctx.module, ctx.n_in), None, None
+
+
+class HipResample(torch.nn.Module):
+    """Resample a signal from one rate to another with HIP kernels.
+
+    Numerically ``torchaudio.transforms.Resample`` with the same arguments,
+    with float64 accumulation of the taps.  Identity (no kernel launch, any
+    device) when both rates are equal.
+    """
+
+    def __init__(
+        self,
+        orig_freq: int = 16000,
+        new_freq: int = 16000,
+        lowpass_filter_width: int = 6,
+        rolloff: float = 0.99,
+        resampling_method: str = "sinc_interp_hann",
+        beta: Optional[float] = None,
+    ):
+        super().__init__()
+        if orig_freq <= 0 or new_freq <= 0:
+            raise ValueError("Original and desired frequency have to be positive.")
+        self.orig_freq, self.new_freq = int(orig_freq), int(new_freq)
+        self.gcd = math.gcd(self.orig_freq, self.new_freq)
+        self.orig_step = self.orig_freq // self.gcd
+        self.new_step = self.new_freq // self.gcd
+        self.lowpass_filter_width = lowpass_filter_width
+        self.rolloff = rolloff
+        self.resampling_method = resampling_method
+        self.beta = beta
+
+        if self.orig_freq == self.new_freq:
+            self.width = 0
+            return
+
+        kernel, self.width = sinc_resample_kernel(
+            self.orig_freq, self.new_freq, lowpass_filter_width, rolloff, resampling_method, beta
+        )
+        nonzero = kernel != 0
+        ntaps = kernel.shape[1]
+        tap_lo = torch.zeros(self.new_step, dtype=torch.int32)
+        tap_hi = torch.zeros(self.new_step, dtype=torch.int32)
+        for j in range(self.new_step):
+            idx = torch.nonzero(nonzero[j]).flatten()
+            if idx.numel():
+                tap_lo[j], tap_hi[j] = int(idx[0]), int(idx[-1]) + 1
+        phase_lo = torch.zeros(ntaps, dtype=torch.int32)
+        phase_hi = torch.zeros(ntaps, dtype=torch.int32)
+        for k in range(ntaps):
+            # phases whose non-zero band [tap_lo, tap_hi) contains k
+            inside = torch.nonzero((tap_lo <= k) & (k < tap_hi)).flatten()
+            if inside.numel():
+                phase_lo[k], phase_hi[k] = int(inside[0]), int(inside[-1]) + 1
+                span = torch.arange(int(phase_lo[k]), int(phase_hi[k]))
+                assert bool(((tap_lo[span] <= k) & (k < tap_hi[span])).all()), "bands not monotone"
+        self.register_buffer("kernel", kernel.contiguous())
+        self.register_buffer("tap_lo", tap_lo)
+        self.register_buffer("tap_hi", tap_hi)
+        self.register_buffer("phase_lo", phase_lo)
+        self.register_buffer("phase_hi", phase_hi)
+
+    def output_length(self, n_samples: int) -> int:
+        return resample_length(n_samples, self.orig_step, self.new_step)
+
+    def forward(self, waveform: torch.Tensor) -> torch.Tensor:
+        """Resample ``[..., sample]`` signals along the last axis."""
+
+        if self.orig_freq == self.new_freq:
+            return waveform
+        if self.kernel.device != waveform.device:
+            raise RuntimeError(
+                f"The resampling kernel lives on {self.kernel.device} but the waveform on "
+                f"{waveform.device}, move the module with `.to(...)`."
+            )
+        shape = waveform.shape
+        batch = math.prod(shape[:-1])
+        packed = check_input(waveform.reshape(batch, shape[-1]), "waveform")
+        n_out = self.output_length(shape[-1])
+        slack = 128 * max(self.orig_step, self.new_step) + self.kernel.shape[1]
+        if max(shape[-1], n_out) > _INDEX_LIMIT - slack:
+            raise RuntimeError("The signal is too long for the resampler's 32 bit launch grid.")
+        out = _ResampleFunction.apply(packed, self, n_out)
+        return out.reshape(shape[:-1] + out.shape[-1:])
+
+    def extra_repr(self) -> str:
+        return f"orig_freq={self.orig_freq}, new_freq={self.new_freq}"

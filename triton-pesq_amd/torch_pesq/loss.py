@@ -1,0 +1,199 @@
+"""PESQ loss evaluated by HIP kernels on an AMD Instinct GPU.
+
+:class:`PesqLoss` keeps the constructor, attributes and methods of the
+reference ``torch_pesq/loss.py:20-322`` (``raw``, ``mos``, ``forward``,
+``align_level``, ``preemphasize``; ``resampler``, ``to_spec``, ``fbank``,
+``loudness``, ``power_filter``, ``pre_filter``).  Every computation runs on
+the GPU through ``libpesq_hip.so``; CPU tensors are rejected with a
+``RuntimeError``.
+
+``raw``/``mos``/``forward`` go through the fused pipeline (five kernels
+forward, four backward, see ``csrc/pipeline.hip``); ``align_level`` and
+``preemphasize`` are the stand-alone per stage operators.
+"""
+
+import numpy as np
+import torch
+from scipy.signal import butter
+from torch.nn import Parameter
+
+from .bark import BarkScale
+from .loudness import Loudness, Sl_16k
+
+__all__ = ["PesqLoss", "SpectrogramSpec"]
+
+#: loudness calibration constant used by the perceptual chain
+#: (``torch_pesq/triton_ops/reference.py:322``; ``loudness.py:Sl_16k``)
+SL = 0.1866055
+
+
+class SpectrogramSpec(torch.nn.Module):
+    """Parameters of the framed power spectrogram (``loss.py:79-87``).
+
+    ``torch.hann_window(win_length)`` (periodic, float32), centred into
+    ``n_fft`` taps, power 2, no centring of the frames, no normalisation.
+    """
+
+    def __init__(self, win_length: int = 512, n_fft: int = 512, hop_length: int = 256):
+        super().__init__()
+        self.n_fft = int(n_fft)
+        self.win_length = int(win_length)
+        self.hop_length = int(hop_length)
+        if self.win_length > self.n_fft:
+            raise ValueError(f"win_length {win_length} exceeds n_fft {n_fft}.")
+        window = torch.zeros(self.n_fft, dtype=torch.float32)
+        left = (self.n_fft - self.win_length) // 2
+        window[left : left + self.win_length] = torch.hann_window(self.win_length)
+        self.register_buffer("window", window)
+
+
+class PesqLoss(torch.nn.Module):
+    """Perceptual Evaluation of Speech Quality as a differentiable loss.
+
+    Parameters
+    ----------
+    factor : float
+        Scaling of the loss function
+    sample_rate : int
+        Sampling rate of the inputs; other rates than 16 kHz are resampled
+    nbarks, win_length, n_fft, hop_length : int
+        Bark bands and STFT geometry; the HIP pipeline supports the PESQ
+        defaults 49 / 512 / 512 / 256
+    """
+
+    factor: float
+
+    def __init__(
+        self,
+        factor: float,
+        sample_rate: int = 48000,
+        nbarks: int = 49,
+        win_length: int = 512,
+        n_fft: int = 512,
+        hop_length: int = 256,
+    ):
+        super().__init__()
+
+        if (nbarks, win_length, n_fft, hop_length) != (49, 512, 512, 256):
+            raise NotImplementedError(
+                "The HIP PESQ pipeline supports nbarks=49, win_length=n_fft=512 and "
+                f"hop_length=256, got {(nbarks, win_length, n_fft, hop_length)}."
+            )
+
+        from .hip_ops.iir import HipIIR
+        from .hip_ops.pipeline import pack_model_table
+        from .hip_ops.resample import HipResample
+
+        self.factor = factor
+        self.source_sample_rate = int(sample_rate)
+
+        self.resampler = HipResample(self.source_sample_rate, 16000)
+        self.to_spec = SpectrogramSpec(win_length, n_fft, hop_length)
+        self.fbank = BarkScale(n_fft // 2, nbarks)
+        self.loudness = Loudness(nbarks)
+
+        coeffs = np.asarray(butter(5, [325, 3250], fs=16000, btype="band"))
+        self.power_filter = Parameter(torch.as_tensor(coeffs, dtype=torch.float32), requires_grad=False)
+        self.pre_filter = Parameter(
+            torch.tensor(
+                [[2.740826, -5.4816519, 2.740826], [1.0, -1.9444777, 0.94597794]],
+                dtype=torch.float32,
+            ),
+            requires_grad=False,
+        )
+
+        # stand-alone per stage operators (align_level / preemphasize)
+        self.power_iir = HipIIR(self.power_filter[0], self.power_filter[1])
+        self.pre_iir = HipIIR(self.pre_filter[0], self.pre_filter[1])
+
+        table = pack_model_table(
+            self.power_filter[0],
+            self.power_filter[1],
+            self.pre_filter[0],
+            self.pre_filter[1],
+            self.to_spec.window,
+            self.fbank.fbank,
+            self.fbank.pow_dens_correction,
+            self.loudness.threshs,
+            self.loudness.exp,
+            self.fbank.width_bark,
+            self.fbank.total_width,
+            SL,
+        )
+        self.register_buffer("model_table", table, persistent=False)
+
+    # -- stages -------------------------------------------------------------
+
+    def align_level(self, signal: torch.Tensor) -> torch.Tensor:
+        """Align the 325 Hz - 3.25 kHz band power of ``signal`` to 1e7 (``loss.py:111-141``)."""
+
+        from .hip_ops.elementwise import align_scale
+
+        return align_scale(signal, self.power_iir(signal))
+
+    def preemphasize(self, signal: torch.Tensor) -> torch.Tensor:
+        """Edge ramp and pre-emphasis filter (``loss.py:144-169``)."""
+
+        from .hip_ops.elementwise import edge_ramp
+
+        return self.pre_iir(edge_ramp(signal))
+
+    # -- pipeline -----------------------------------------------------------
+
+    def _run(self, ref: torch.Tensor, deg: torch.Tensor):
+        from .hip_ops._common import check_input
+        from .hip_ops.pipeline import PipelineFunction
+
+        deg, ref = torch.atleast_2d(deg), torch.atleast_2d(ref)
+        if ref.shape != deg.shape:
+            raise ValueError(
+                "Reference and degraded signal must have the same shape, "
+                f"got {tuple(ref.shape)} and {tuple(deg.shape)}."
+            )
+        if ref.dim() != 2:
+            raise ValueError(f"Expected [batch, sample] signals, got {tuple(ref.shape)}.")
+        ref = check_input(ref, "ref")
+        deg = check_input(deg, "deg")
+        if self.model_table.device != ref.device:
+            raise RuntimeError(
+                f"The module lives on {self.model_table.device} but the signals on "
+                f"{ref.device}; move it with `.to(...)` first."
+            )
+
+        if self.source_sample_rate != 16000:
+            ref, deg = self.resampler(ref), self.resampler(deg)
+
+        length = ref.shape[1]
+        padded = length + length % 256
+        frames = 1 + (padded - 512) // 256 if padded >= 512 else 0
+        if length < 15:
+            raise RuntimeError(
+                f"The edge ramp needs at least 15 samples at 16 kHz, got {length}."
+            )
+        if frames < 20:
+            raise ValueError(
+                "The PESQ chain needs at least 20 frames for the overlapping sums, "
+                f"got {frames}."
+            )
+        if isinstance(self.factor, torch.Tensor) and self.factor.requires_grad:
+            raise RuntimeError(
+                "The loss treats `factor` as a constant, pass a Python float. A tensor "
+                "that requires a gradient would receive none."
+            )
+        return PipelineFunction.apply(ref, deg, self.model_table, float(self.factor))
+
+    def raw(self, ref: torch.Tensor, deg: torch.Tensor):
+        """Symmetric and asymmetric distances, both ``[batch]``."""
+
+        d_symm, d_asymm, _, _ = self._run(ref, deg)
+        return d_symm, d_asymm
+
+    def mos(self, ref: torch.Tensor, deg: torch.Tensor) -> torch.Tensor:
+        """Mean opinion score in ``(1.08, 4.999)`` (``loss.py:271-297``)."""
+
+        return self._run(ref, deg)[2]
+
+    def forward(self, ref: torch.Tensor, deg: torch.Tensor) -> torch.Tensor:
+        """Loss ``factor * (0.1 d_symm + 0.0309 d_asymm)`` (``loss.py:300-322``)."""
+
+        return self._run(ref, deg)[3]
