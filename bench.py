@@ -331,6 +331,24 @@ def cpu_baseline(ref_np, deg_np, gpu_outputs, budget_s: float = 12.0):
     return baseline, errors
 
 
+def _profiled_traffic(stage: str):
+    """HBM bytes per launch of a stage from the committed rocprofv3 PMC summary.
+
+    ``profiles/pipeline_c2_hbm_traffic.txt`` holds FETCH_SIZE and WRITE_SIZE per
+    dispatch, calibrated against a plain device copy of known size; ``None``
+    when it is missing.
+    """
+
+    path = ROOT / "profiles" / "pipeline_c2_hbm_traffic.txt"
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("# traffic_json:"):
+                return json.loads(line.split(":", 1)[1])["stage_bytes"].get(stage)
+    except (OSError, ValueError, KeyError):
+        return None
+    return None
+
+
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -338,6 +356,12 @@ def main(argv=None):
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    parser.add_argument(
+        "--copy-calibration",
+        action="store_true",
+        help="first run a plain 64 MiB device copy (5 launches), the known-size reference "
+        "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters",
+    )
     args = parser.parse_args(argv)
 
     if args.gpus != 1:
@@ -357,6 +381,12 @@ def main(argv=None):
     ref_np, deg_np, fs = synthetic_config(2)
     batch, samples = ref_np.shape
     device = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.ones(16 * 1024 * 1024, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     model = PesqLossTriton(1.0, sample_rate=fs).to(device)
     ref = torch.from_numpy(ref_np).to(device)
     deg = torch.from_numpy(deg_np).to(device).requires_grad_(True)
@@ -417,7 +447,7 @@ def main(argv=None):
         "peak": HBM_PEAK / 1e9,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK, 4),
-        "traffic": None,
+        "traffic": _profiled_traffic(dominant),
         "kernel": " + ".join(STAGES[dominant][2]),
         "stage": dominant,
         "model_bytes_per_launch": per_stage[dominant],
