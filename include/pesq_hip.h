@@ -196,6 +196,96 @@ int pesq_resample_backward(const float *grad_y, float *grad_x, int64_t rows, int
                            const int32_t *phase_hi, int64_t orig_step, int64_t new_step,
                            int64_t width, int64_t width_total, hipStream_t stream);
 
+/* ----------------------------------------------------------------------- */
+/* STFT / Bark (TritonStftBark, torch_pesq/triton_ops/spectral.py:584-774)  */
+/* ----------------------------------------------------------------------- */
+
+/* bark[r, t, i] = corr_i sum_{f in band i} |DFT(window . x[r, 256 t : 256 t + 512])_f|^2
+ * for t < 1 + (n_padded - 512) / 256, samples at or beyond len read as zero,
+ * DC dropped.  model_table from pesq_model_table_pack (filters may be absent).
+ * Replaces _fwd_kernel (spectral.py:229-332). */
+int pesq_stft_bark_forward(const float *x, int64_t rows, int64_t len, int64_t n_padded,
+                           const void *model_table, float *bark, hipStream_t stream);
+
+/* Vector-Jacobian product of pesq_stft_bark_forward: g_x [rows, len].
+ * Replaces _bwd_frame_kernel + _bwd_gather_kernel (spectral.py:334-440). */
+int pesq_stft_bark_backward(const float *g_bark, const float *x, int64_t rows, int64_t len,
+                            int64_t n_padded, const void *model_table, float *g_x,
+                            hipStream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* perceptual chain (TritonPesqChain, torch_pesq/triton_ops/chain.py:1024-1126) */
+/* ----------------------------------------------------------------------- */
+
+int pesq_chain_forward_workspace(int64_t batch, int64_t frames, size_t *bytes);
+int pesq_chain_backward_workspace(int64_t batch, int64_t frames, size_t *bytes);
+
+/* (d_symm, d_asymm)[batch] of two Bark spectrograms [batch, frames, 49];
+ * needs at least 20 frames.  Replaces the 7 forward kernels of
+ * _ChainFunction.forward (chain.py:768-940). */
+int pesq_chain_forward(const float *ref_bark, const float *deg_bark, int64_t batch,
+                       int64_t frames, const void *model_table, float *d_symm, float *d_asymm,
+                       void *fwd_workspace, hipStream_t stream);
+
+/* Gradients w.r.t. both spectrograms given those of the distances (NULL =
+ * zero).  Replaces _ChainFunction.backward (chain.py:942-1021). */
+int pesq_chain_backward(const float *g_symm, const float *g_asymm, const float *ref_bark,
+                        const float *deg_bark, int64_t batch, int64_t frames,
+                        const void *model_table, float *g_ref_bark, float *g_deg_bark,
+                        const void *fwd_workspace, void *bwd_workspace, hipStream_t stream);
+
+/* ----------------------------------------------------------------------- */
+/* element-wise stages (torch_pesq/triton_ops/elementwise.py)               */
+/* ----------------------------------------------------------------------- */
+
+/* Scratch of the element-wise reductions for `rows` rows. */
+int pesq_elementwise_workspace(int64_t rows, size_t *bytes);
+
+/* peak[b] = max(max|ref[b]|, max|deg[b]|); out = x / peak (IEEE division).
+ * out_ref / out_deg may point into one stacked [2 batch, len] buffer.
+ * Replaces _peak_partial_kernel + _peak_apply_kernel (elementwise.py:74-133). */
+int pesq_peak_normalize_forward(const float *ref, const float *deg, int64_t batch, int64_t len,
+                                float *out_ref, float *out_deg, float *peak, void *workspace,
+                                hipStream_t stream);
+
+/* g / peak for the requested halves (NULL skips one); the peak is a constant.
+ * Replaces _div_pair_kernel (elementwise.py:136-162). */
+int pesq_peak_normalize_backward(const float *g_ref, const float *g_deg, const float *peak,
+                                 int64_t batch, int64_t len, float *out_ref, float *out_deg,
+                                 hipStream_t stream);
+
+/* y = (x head) tail with head_k = (k+1)/16 (k < 15), tail_k = (len-k)/16 (last
+ * 15); its own adjoint.  Replaces _edge_ramp_kernel (elementwise.py:308-331). */
+int pesq_edge_ramp(const float *x, float *y, int64_t rows, int64_t len, hipStream_t stream);
+
+/* power = sum filtered^2 / (n_flt + 5120) / 1.04684, scale = sqrt(1e7 / power),
+ * out = signal * scale; state[rows, 2] (float64) = {power, scale} for the
+ * backward.  Replaces _dot_partial_kernel + _align_apply_kernel
+ * (elementwise.py:416-481). */
+int pesq_align_scale_forward(const float *signal, const float *filtered, int64_t rows,
+                             int64_t n_sig, int64_t n_flt, float *out, double *state,
+                             void *workspace, hipStream_t stream);
+
+/* g_signal = grad scale; g_filtered = 2 filtered (-0.5 S scale / power) / D
+ * with S = sum grad signal (either output may be NULL).  Replaces
+ * _mul_bcast_kernel + _align_grad_filtered_kernel (elementwise.py:484-536). */
+int pesq_align_scale_backward(const float *grad, const float *signal, const float *filtered,
+                              const double *state, int64_t rows, int64_t n_sig, int64_t n_flt,
+                              float *g_signal, float *g_filtered, void *workspace,
+                              hipStream_t stream);
+
+/* mos = 0.999 + 4 / (1 + exp(-1.3669 (4.5 - 0.1 ds - 0.0309 da) + 3.8224)),
+ * loss = factor (0.1 ds + 0.0309 da).  Replaces _epilogue_kernel
+ * (elementwise.py:683-700). */
+int pesq_epilogue_forward(const float *d_symm, const float *d_asymm, int64_t batch, double factor,
+                          float *mos, float *loss, hipStream_t stream);
+
+/* Gradients of both distances from those of MOS and/or loss (NULL = zero).
+ * Replaces _epilogue_bwd_kernel (elementwise.py:703-747). */
+int pesq_epilogue_backward(const float *d_symm, const float *d_asymm, const float *g_mos,
+                           const float *g_loss, int64_t batch, double factor, float *g_symm,
+                           float *g_asymm, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

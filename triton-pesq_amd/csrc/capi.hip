@@ -94,17 +94,20 @@ extern "C" int pesq_model_table_pack(const pesq_model_constants *c, void *out) {
                    "the HIP pipeline supports nbarks=49, n_fft=512, hop_length=256 "
                    "(got %d, %d, %d)",
                    c->nbarks, c->n_fft, c->hop);
-    PESQ_CHECK_ARG(c->power_filter.count == 5 && c->pre_filter.count == 1,
+    const bool no_filters = c->power_filter.count == 0 && c->pre_filter.count == 0;
+    PESQ_CHECK_ARG(no_filters || (c->power_filter.count == 5 && c->pre_filter.count == 1),
                    "the HIP pipeline is built for a 5 section level alignment filter and a "
                    "1 section pre-emphasis filter (got %d and %d)",
                    c->power_filter.count, c->pre_filter.count);
 
     ModelTable *t = new ModelTable;
     std::memset(t, 0, sizeof(*t));
-    int st = pack_iir(t->iir, &c->power_filter, &c->pre_filter);
-    if (st) {
-        delete t;
-        return st;
+    if (!no_filters) {
+        const int st = pack_iir(t->iir, &c->power_filter, &c->pre_filter);
+        if (st) {
+            delete t;
+            return st;
+        }
     }
 
     const double two_pi = 6.283185307179586476925286766559;

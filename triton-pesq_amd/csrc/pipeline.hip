@@ -150,8 +150,12 @@ struct PipeArgs {
     unsigned char *bw;  // backward workspace
     PipeLayout L;
     double factor;
-    float *d_symm, *d_asymm, *mos, *loss;
+    float *d_symm, *d_asymm, *mos, *loss;  // mos / loss may be null
     const float *g_symm, *g_asymm, *g_mos, *g_loss;
+    // Bark spectra read by the chain kernels and the gradients they write,
+    // [batch, frames, 49] each (inside the workspaces for the pipeline)
+    const float *bark_ref, *bark_deg;
+    float *gbark_ref, *gbark_deg;
 };
 
 template <typename T>
@@ -346,8 +350,8 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs 
     const BandConsts c = band_consts(t, lane);
     const bool live = lane < kBands;
     const double r = live ? rs[lane] : 0.0;
-    const float *bref = region<float>(a.ws, L.bark) + int64_t(item) * L.frames * kBands;
-    const float *bdeg = region<float>(a.ws, L.bark) + int64_t(item + L.batch) * L.frames * kBands;
+    const float *bref = a.bark_ref + int64_t(item) * L.frames * kBands;
+    const float *bdeg = a.bark_deg + int64_t(item) * L.frames * kBands;
     const double sqrt_w = sqrt(t.total_width);
     const double W = t.total_width;
 
@@ -460,8 +464,8 @@ __global__ void __launch_bounds__(kFinalThreads) chain_final_kernel(PipeArgs a) 
         const double inner = 4.5 - 0.1 * d[0] - 0.0309 * d[1];
         a.d_symm[item] = static_cast<float>(d[0]);
         a.d_asymm[item] = static_cast<float>(d[1]);
-        a.mos[item] = static_cast<float>(0.999 + 4.0 / (1.0 + exp(-1.3669 * inner + 3.8224)));
-        a.loss[item] = static_cast<float>(a.factor * (0.1 * d[0] + 0.0309 * d[1]));
+        if (a.mos) a.mos[item] = static_cast<float>(0.999 + 4.0 / (1.0 + exp(-1.3669 * inner + 3.8224)));
+        if (a.loss) a.loss[item] = static_cast<float>(a.factor * (0.1 * d[0] + 0.0309 * d[1]));
     }
 }
 
@@ -523,8 +527,8 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
 
     const BandConsts c = band_consts(t, lane);
     const double r = live ? rs[lane] : 0.0;
-    const float *bref = region<float>(a.ws, L.bark) + int64_t(item) * L.frames * kBands;
-    const float *bdeg = region<float>(a.ws, L.bark) + int64_t(item + L.batch) * L.frames * kBands;
+    const float *bref = a.bark_ref + int64_t(item) * L.frames * kBands;
+    const float *bdeg = a.bark_deg + int64_t(item) * L.frames * kBands;
     const double *psqm_s = region<double>(a.ws, L.psqm) + int64_t(item) * L.nwin;
     const double *psqm_a = region<double>(a.ws, L.psqm) + (int64_t(L.batch) + item) * L.nwin;
     const double W = t.total_width;
@@ -602,7 +606,6 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
 
     // phase 2: frame power ratio, h and the total audible energies
     double acc = 0.0;
-    float *gb = region<float>(a.bw, L.gbark);
     for (int q = 0; q < kPer; ++q) {
         const int local = wave * kPer + q;
         const int64_t frame = t0 + local;
@@ -628,8 +631,8 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
             double ger = g_er[q];
             if (r * R > c.th) ger += g_taer;
             const double ged = g_ed[q] * fpr + (G > c.th ? g_tad : 0.0);
-            gb[(int64_t(item) * L.frames + frame) * kBands + lane] = static_cast<float>(ger * r);
-            gb[(int64_t(item + L.batch) * L.frames + frame) * kBands + lane] = static_cast<float>(ged);
+            a.gbark_ref[(int64_t(item) * L.frames + frame) * kBands + lane] = static_cast<float>(ger * r);
+            a.gbark_deg[(int64_t(item) * L.frames + frame) * kBands + lane] = static_cast<float>(ged);
             acc += ger * R;
         }
     }
@@ -747,6 +750,177 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_bwd_kernel(PipeArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// stand-alone perceptual chain: silent frames + band partials from given
+// spectra, and the mean band power scatter of the backward
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(kWave) chain_partials_kernel(PipeArgs a) {
+    const ModelTable &t = *a.tab;
+    const PipeLayout &L = a.L;
+    const int item = blockIdx.x / L.ntile;
+    const int tile = blockIdx.x - item * L.ntile;
+    const int t0 = tile * kTile;
+    const int lane = threadIdx.x;
+    const bool live = lane < kBands;
+    const double th100 = live ? 100.0 * t.threshs[lane] : 0.0;
+    const float *bref = a.bark_ref + int64_t(item) * L.frames * kBands;
+    const float *bdeg = a.bark_deg + int64_t(item) * L.frames * kBands;
+    double pr = 0.0, pd = 0.0;
+    for (int local = 0; local < kTile; ++local) {
+        const int64_t frame = t0 + local;
+        if (frame >= L.frames) break;
+        const double r = live ? static_cast<double>(bref[frame * kBands + lane]) : 0.0;
+        const double d = live ? static_cast<double>(bdeg[frame * kBands + lane]) : 0.0;
+        const double total = wave_sum(live && r > th100 ? r : 0.0);
+        const bool keep = total >= 1e7;
+        if (lane == 0) region<float>(a.ws, L.keep)[int64_t(item) * L.frames + frame] = keep ? 1.0f : 0.0f;
+        if (keep && r > th100) pr += r;
+        if (keep && d > th100) pd += d;
+    }
+    if (live) {
+        region<double>(a.ws, L.bandref)[(int64_t(item) * L.ntile + tile) * kBands + lane] = pr;
+        region<double>(a.ws, L.banddeg)[(int64_t(item) * L.ntile + tile) * kBands + lane] = pd;
+    }
+}
+
+__global__ void __launch_bounds__(kWave) chain_meanpow_kernel(PipeArgs a) {
+    const ModelTable &t = *a.tab;
+    const PipeLayout &L = a.L;
+    const int item = blockIdx.x / L.ntile;
+    const int tile = blockIdx.x - item * L.ntile;
+    const int t0 = tile * kTile;
+    const int lane = threadIdx.x;
+    if (lane >= kBands) return;
+    const double *gp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
+    double g = 0.0;
+    for (int k = 0; k < L.ntile; ++k) g += gp[k * kBands + lane];
+    const double ratio = band_array(a, kRatio)[item * kBands + lane];
+    const double mref = band_array(a, kMref)[item * kBands + lane];
+    const double gr = (ratio >= 0.01 && ratio <= 100.0) ? g : 0.0;
+    const double inv = 1.0 / (mref + 1000.0);
+    const double frames_f = static_cast<double>(L.frames);
+    const double gm_ref = -gr * ratio * inv / frames_f;
+    const double gm_deg = gr * inv / frames_f;
+    const double th100 = 100.0 * t.threshs[lane];
+    const float *keep = region<float>(a.ws, L.keep) + int64_t(item) * L.frames;
+    for (int local = 0; local < kTile; ++local) {
+        const int64_t frame = t0 + local;
+        if (frame >= L.frames) break;
+        if (keep[frame] == 0.0f) continue;
+        const int64_t o = (int64_t(item) * L.frames + frame) * kBands + lane;
+        if (static_cast<double>(a.bark_ref[o]) > th100) {
+            a.gbark_ref[o] = static_cast<float>(static_cast<double>(a.gbark_ref[o]) + gm_ref);
+        }
+        if (static_cast<double>(a.bark_deg[o]) > th100) {
+            a.gbark_deg[o] = static_cast<float>(static_cast<double>(a.gbark_deg[o]) + gm_deg);
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// stand-alone STFT / Bark (the TritonStftBark operator): independent rows,
+// no level scale, frames laid over n_padded samples (zero beyond len)
+// ---------------------------------------------------------------------------
+
+struct StftArgs {
+    const ModelTable *tab;
+    const float *x;       // [rows, len]
+    float *bark;          // [rows, frames, 49]
+    const float *gbark;   // [rows, frames, 49]
+    float *gx;            // [rows, len]
+    int64_t rows, len, frames, nhoptile, ftiles;
+};
+
+constexpr int kPlainWaves = 8;
+
+template <typename real>
+__global__ void __launch_bounds__(kWave *kPlainWaves) stft_plain_fwd_kernel(StftArgs a) {
+    __shared__ cplx<real> fftbuf[kPlainWaves][kHalf];
+    const ModelTable &t = *a.tab;
+    const int64_t row = blockIdx.x / a.ftiles;
+    const int64_t ft = blockIdx.x - row * a.ftiles;
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int64_t frame = ft * kPlainWaves + wave;
+    if (frame >= a.frames) return;
+    const float *x = a.x + row * a.len;
+    const int64_t start = frame * kHop;
+    auto u = [&](int k) -> real {
+        const int64_t n = start + k;
+        return n < a.len ? static_cast<real>(x[n]) * static_cast<real>(t.window[k]) : real(0);
+    };
+    cplx<real> *buf = fftbuf[wave];
+    cplx<real> spec[4];
+    frame_spectrum<real>(u, spec, buf, t.tw256, t.tw512, lane);
+    real *power = reinterpret_cast<real *>(buf);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int f = lane + 64 * r;
+        power[f] = f == 0 ? real(0) : spec[r].re * spec[r].re + spec[r].im * spec[r].im;
+    }
+    wave_lds_fence();
+    if (lane < kBands) {
+        double acc = 0.0;
+        for (int f = t.band_start[lane]; f < t.band_end[lane]; ++f) acc += static_cast<double>(power[f]);
+        a.bark[(row * a.frames + frame) * kBands + lane] = static_cast<float>(acc * t.corr[lane]);
+    }
+}
+
+template <typename real>
+__global__ void __launch_bounds__(kWave *kBwdFrames) stft_plain_bwd_kernel(StftArgs a) {
+    __shared__ cplx<real> fftbuf[kBwdFrames][kHalf];
+    __shared__ float contrib[kBwdFrames][kNfft];
+    __shared__ float gband[kBwdFrames][kBands];
+    const ModelTable &t = *a.tab;
+    const int64_t row = blockIdx.x / a.nhoptile;
+    const int64_t ht = blockIdx.x - row * a.nhoptile;
+    const int wave = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    const int64_t j0 = ht * kBwdHops;
+    const int64_t frame = j0 - 1 + wave;
+    const float *x = a.x + row * a.len;
+    if (frame >= 0 && frame < a.frames) {
+        if (lane < kBands) {
+            gband[wave][lane] = static_cast<float>(
+                static_cast<double>(a.gbark[(row * a.frames + frame) * kBands + lane]) * t.corr[lane]);
+        }
+        wave_lds_fence();
+        const int64_t start = frame * kHop;
+        auto u = [&](int k) -> real {
+            const int64_t n = start + k;
+            return n < a.len ? static_cast<real>(x[n]) * static_cast<real>(t.window[k]) : real(0);
+        };
+        cplx<real> spec[4], v[4];
+        frame_spectrum<real>(u, spec, fftbuf[wave], t.tw256, t.tw512, lane);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int band = t.bin_band[lane + 64 * r];
+            const real g = band >= 0 ? static_cast<real>(gband[wave][band]) : real(0);
+            v[r] = {g * spec[r].re, g * spec[r].im};
+        }
+        real ev[4], od[4];
+        frame_adjoint<real>(v, ev, od, fftbuf[wave], t.tw256, t.tw512, lane);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int n = lane + 64 * r;
+            contrib[wave][2 * n] = static_cast<float>(ev[r] * static_cast<real>(t.window[2 * n]));
+            contrib[wave][2 * n + 1] = static_cast<float>(od[r] * static_cast<real>(t.window[2 * n + 1]));
+        }
+    } else {
+        for (int k = lane; k < kNfft; k += kWave) contrib[wave][k] = 0.0f;
+    }
+    __syncthreads();
+    float *gx = a.gx + row * a.len;
+    for (int k = threadIdx.x; k < kBwdHops * kHop; k += blockDim.x) {
+        const int q = k / kHop, m = k % kHop;
+        const int64_t n = (j0 + q) * kHop + m;
+        if (n >= a.len) continue;
+        gx[n] = static_cast<float>(static_cast<double>(contrib[q][kHop + m]) +
+                                   static_cast<double>(contrib[q + 1][m]));
+    }
+}
+
+// ---------------------------------------------------------------------------
 // host entry points
 // ---------------------------------------------------------------------------
 
@@ -822,6 +996,8 @@ extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, 
     a.loss = loss;
     const PipeLayout &L = a.L;
     const IirTable *iir = &a.tab->iir;
+    a.bark_ref = region<float>(a.ws, L.bark);
+    a.bark_deg = a.bark_ref + batch * L.frames * kBands;
 
     PipeFwdMode m{};
     m.ref = ref;
@@ -901,6 +1077,10 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
     a.g_loss = g_loss;
     const PipeLayout &L = a.L;
     const IirTable *iir = &a.tab->iir;
+    a.bark_ref = region<float>(a.ws, L.bark);
+    a.bark_deg = a.bark_ref + batch * L.frames * kBands;
+    a.gbark_ref = region<float>(a.bw, L.gbark);
+    a.gbark_deg = a.gbark_ref + batch * L.frames * kBands;
 
     if (stages & 1u) {
         hipLaunchKernelGGL(chain_bwd_kernel, dim3(static_cast<unsigned>(batch * L.ntile)),
@@ -951,4 +1131,129 @@ extern "C" int pesq_pipeline_backward(const float *g_symm, const float *g_asymm,
     return pesq_pipeline_backward_stages(g_symm, g_asymm, g_mos, g_loss, batch, len, model_table,
                                          factor, grad_mask, g_ref, g_deg, fwd_workspace,
                                          bwd_workspace, 0xFu, stream);
+}
+
+// ---------------------------------------------------------------------------
+// stand-alone chain and STFT entry points
+// ---------------------------------------------------------------------------
+
+static int chain_args(PipeArgs &a, int64_t batch, int64_t frames, const void *model_table) {
+    PESQ_CHECK_ARG(batch > 0, "batch must be positive, got %lld", (long long)batch);
+    PESQ_CHECK_ARG(frames >= kWin,
+                   "The PESQ chain needs at least 20 frames for the overlapping sums, got %lld",
+                   (long long)frames);
+    PESQ_CHECK_ARG(batch * cdiv(frames, kTile) < (int64_t(1) << 31), "problem too large for one launch");
+    PESQ_CHECK_ARG(model_table != nullptr, "null model table");
+    a.L.build_chain(batch, frames);
+    a.tab = static_cast<const ModelTable *>(model_table);
+    return PESQ_OK;
+}
+
+extern "C" int pesq_chain_forward_workspace(int64_t batch, int64_t frames, size_t *bytes) {
+    PipeArgs a{};
+    if (int st = chain_args(a, batch, frames, reinterpret_cast<const void *>(1))) return st;
+    *bytes = a.L.fwd_bytes;
+    return PESQ_OK;
+}
+
+extern "C" int pesq_chain_backward_workspace(int64_t batch, int64_t frames, size_t *bytes) {
+    PipeArgs a{};
+    if (int st = chain_args(a, batch, frames, reinterpret_cast<const void *>(1))) return st;
+    *bytes = a.L.bwd_bytes;
+    return PESQ_OK;
+}
+
+extern "C" int pesq_chain_forward(const float *ref_bark, const float *deg_bark, int64_t batch,
+                                  int64_t frames, const void *model_table, float *d_symm,
+                                  float *d_asymm, void *fwd_workspace, hipStream_t stream) {
+    PipeArgs a{};
+    if (int st = chain_args(a, batch, frames, model_table)) return st;
+    PESQ_CHECK_ARG(ref_bark && deg_bark && d_symm && d_asymm && fwd_workspace, "null pointer argument");
+    a.ws = static_cast<unsigned char *>(fwd_workspace);
+    a.bark_ref = ref_bark;
+    a.bark_deg = deg_bark;
+    a.d_symm = d_symm;
+    a.d_asymm = d_asymm;
+    const unsigned grid = static_cast<unsigned>(batch * a.L.ntile);
+    hipLaunchKernelGGL(chain_partials_kernel, dim3(grid), dim3(kWave), 0, stream, a);
+    PESQ_CHECK_LAUNCH("chain partials");
+    hipLaunchKernelGGL(chain_fwd_kernel, dim3(grid), dim3(kWave * kChainWaves), 0, stream, a);
+    PESQ_CHECK_LAUNCH("chain");
+    hipLaunchKernelGGL(chain_final_kernel, dim3(static_cast<unsigned>(batch)), dim3(kFinalThreads),
+                       0, stream, a);
+    PESQ_CHECK_LAUNCH("chain final");
+    return PESQ_OK;
+}
+
+extern "C" int pesq_chain_backward(const float *g_symm, const float *g_asymm, const float *ref_bark,
+                                   const float *deg_bark, int64_t batch, int64_t frames,
+                                   const void *model_table, float *g_ref_bark, float *g_deg_bark,
+                                   const void *fwd_workspace, void *bwd_workspace,
+                                   hipStream_t stream) {
+    PipeArgs a{};
+    if (int st = chain_args(a, batch, frames, model_table)) return st;
+    PESQ_CHECK_ARG(ref_bark && deg_bark && g_ref_bark && g_deg_bark && fwd_workspace && bwd_workspace,
+                   "null pointer argument");
+    a.ws = static_cast<unsigned char *>(const_cast<void *>(fwd_workspace));
+    a.bw = static_cast<unsigned char *>(bwd_workspace);
+    a.bark_ref = ref_bark;
+    a.bark_deg = deg_bark;
+    a.gbark_ref = g_ref_bark;
+    a.gbark_deg = g_deg_bark;
+    a.g_symm = g_symm;
+    a.g_asymm = g_asymm;
+    const unsigned grid = static_cast<unsigned>(batch * a.L.ntile);
+    hipLaunchKernelGGL(chain_bwd_kernel, dim3(grid), dim3(kWave * kChainWaves), 0, stream, a);
+    PESQ_CHECK_LAUNCH("chain backward");
+    hipLaunchKernelGGL(chain_meanpow_kernel, dim3(grid), dim3(kWave), 0, stream, a);
+    PESQ_CHECK_LAUNCH("chain mean power backward");
+    return PESQ_OK;
+}
+
+static int stft_args(StftArgs &a, int64_t rows, int64_t len, int64_t n_padded, const void *table) {
+    PESQ_CHECK_ARG(rows >= 0 && len >= 0, "invalid sizes");
+    PESQ_CHECK_ARG(n_padded >= len, "n_padded (%lld) is smaller than the signal length (%lld)",
+                   (long long)n_padded, (long long)len);
+    PESQ_CHECK_ARG(n_padded >= kNfft, "n_padded (%lld) is shorter than one frame (512)",
+                   (long long)n_padded);
+    PESQ_CHECK_ARG(table != nullptr, "null model table");
+    a.tab = static_cast<const ModelTable *>(table);
+    a.rows = rows;
+    a.len = len;
+    a.frames = 1 + (n_padded - kNfft) / kHop;
+    a.ftiles = cdiv(a.frames, kPlainWaves);
+    a.nhoptile = cdiv(cdiv(len, kHop), kBwdHops);
+    PESQ_CHECK_ARG(rows * a.ftiles < (int64_t(1) << 31) && rows * a.nhoptile < (int64_t(1) << 31),
+                   "problem too large for one launch");
+    return PESQ_OK;
+}
+
+extern "C" int pesq_stft_bark_forward(const float *x, int64_t rows, int64_t len, int64_t n_padded,
+                                      const void *model_table, float *bark, hipStream_t stream) {
+    StftArgs a{};
+    if (int st = stft_args(a, rows, len, n_padded, model_table)) return st;
+    if (rows == 0) return PESQ_OK;
+    PESQ_CHECK_ARG(x && bark, "null pointer argument");
+    a.x = x;
+    a.bark = bark;
+    hipLaunchKernelGGL(stft_plain_fwd_kernel<StftReal>, dim3(static_cast<unsigned>(rows * a.ftiles)),
+                       dim3(kWave * kPlainWaves), 0, stream, a);
+    PESQ_CHECK_LAUNCH("stft bark forward");
+    return PESQ_OK;
+}
+
+extern "C" int pesq_stft_bark_backward(const float *g_bark, const float *x, int64_t rows,
+                                       int64_t len, int64_t n_padded, const void *model_table,
+                                       float *g_x, hipStream_t stream) {
+    StftArgs a{};
+    if (int st = stft_args(a, rows, len, n_padded, model_table)) return st;
+    if (rows == 0 || len == 0) return PESQ_OK;
+    PESQ_CHECK_ARG(x && g_bark && g_x, "null pointer argument");
+    a.x = x;
+    a.gbark = g_bark;
+    a.gx = g_x;
+    hipLaunchKernelGGL(stft_plain_bwd_kernel<StftReal>, dim3(static_cast<unsigned>(rows * a.nhoptile)),
+                       dim3(kWave * kBwdFrames), 0, stream, a);
+    PESQ_CHECK_LAUNCH("stft bark backward");
+    return PESQ_OK;
 }

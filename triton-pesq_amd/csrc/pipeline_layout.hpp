@@ -83,6 +83,33 @@ struct PipeLayout {
         bwd_bytes = off;
     }
 
+    // Regions of the stand-alone perceptual chain over given Bark spectra:
+    // only the chain state (forward) and the band partials (backward).
+    void build_chain(int64_t b, int64_t nframes) {
+        *this = PipeLayout();
+        batch = b;
+        rows = 2 * b;
+        frames = nframes;
+        ntile = cdiv(frames, kTile);
+        nwin = frames >= kWin ? (frames - kWin) / kStride + 1 : 0;
+        size_t off = 0;
+        auto take = [&](size_t &field, size_t bytes) {
+            field = off;
+            off = align(off + bytes);
+        };
+        take(keep, size_t(batch) * frames * sizeof(float));
+        take(bandref, size_t(batch) * ntile * kBands * sizeof(double));
+        take(banddeg, size_t(batch) * ntile * kBands * sizeof(double));
+        take(frame, size_t(kFrameArrays) * batch * frames * sizeof(double));
+        take(band, size_t(kBandArrays) * batch * kBands * sizeof(double));
+        take(psqm, size_t(2) * batch * nwin * sizeof(double));
+        take(dist, size_t(batch) * 2 * sizeof(double));
+        fwd_bytes = off;
+        off = 0;
+        take(grpart, size_t(batch) * ntile * kBands * sizeof(double));
+        bwd_bytes = off;
+    }
+
     bool region(const char *name, size_t *offset, size_t *bytes) const {
         struct Entry {
             const char *name;

@@ -105,6 +105,20 @@ SIGNATURES = {
     ),
     "pesq_iir_workspace": (_INT, [_I64, _I64, _SIZE_P]),
     "pesq_iir_apply": (_INT, [_P, _P, _I64, _I64, _P, _INT, _INT, _P, _P]),
+    "pesq_stft_bark_forward": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P]),
+    "pesq_stft_bark_backward": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P, _P]),
+    "pesq_chain_forward_workspace": (_INT, [_I64, _I64, _SIZE_P]),
+    "pesq_chain_backward_workspace": (_INT, [_I64, _I64, _SIZE_P]),
+    "pesq_chain_forward": (_INT, [_P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
+    "pesq_chain_backward": (_INT, [_P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P]),
+    "pesq_elementwise_workspace": (_INT, [_I64, _SIZE_P]),
+    "pesq_peak_normalize_forward": (_INT, [_P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
+    "pesq_peak_normalize_backward": (_INT, [_P, _P, _P, _I64, _I64, _P, _P, _P]),
+    "pesq_edge_ramp": (_INT, [_P, _P, _I64, _I64, _P]),
+    "pesq_align_scale_forward": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
+    "pesq_align_scale_backward": (_INT, [_P, _P, _P, _P, _I64, _I64, _I64, _P, _P, _P, _P]),
+    "pesq_epilogue_forward": (_INT, [_P, _P, _I64, ctypes.c_double, _P, _P, _P]),
+    "pesq_epilogue_backward": (_INT, [_P, _P, _P, _P, _I64, ctypes.c_double, _P, _P, _P]),
     "pesq_resample_forward": (
         _INT,
         [_P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P],

@@ -31,13 +31,18 @@ __all__ = [
 def pack_model_table(
     power_b, power_a, pre_b, pre_a, window, fbank, corr, threshs, exps, width, total_width, sl
 ) -> torch.Tensor:
-    """Pack the model constants into the library's device table (host bytes)."""
+    """Pack the model constants into the library's device table (host bytes).
+
+    ``power_b`` / ``pre_b`` may be ``None`` (both), giving a table for the
+    stand-alone STFT and chain operators only.
+    """
 
     constants = _lib.ModelConstants()
-    c0, secs = parallel_sections(power_b, power_a)
-    constants.power_filter = sections_struct(c0, secs)
-    c0, secs = parallel_sections(pre_b, pre_a)
-    constants.pre_filter = sections_struct(c0, secs)
+    if power_b is not None:
+        c0, secs = parallel_sections(power_b, power_a)
+        constants.power_filter = sections_struct(c0, secs)
+        c0, secs = parallel_sections(pre_b, pre_a)
+        constants.pre_filter = sections_struct(c0, secs)
 
     window = torch.as_tensor(window).detach().cpu().float().numpy()
     if window.shape != (_lib.NFFT,):
