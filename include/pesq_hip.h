@@ -55,7 +55,10 @@ const char *pesq_last_error(void);
 
 /* A causal IIR filter in parallel form: y = c0 x + sum_k s_k(x), section k a
  * direct form II transposed biquad (b0[k] + b1[k] z^-1 + b2[k] z^-2) /
- * (1 + a1[k] z^-1 + a2[k] z^-2) with zero initial state. */
+ * (1 + a1[k] z^-1 + a2[k] z^-2) with zero initial state.  Packing rewrites a
+ * section with b2[k] != 0 as the direct term b2[k] / a2[k] plus a section
+ * without z^-2 in the numerator (the same transfer function); b2[k] != 0
+ * with a2[k] == 0 is rejected. */
 typedef struct pesq_iir_sections {
     int32_t count; /* 1 .. PESQ_IIR_MAX_SECTIONS */
     int32_t reserved;
@@ -121,7 +124,10 @@ int pesq_pipeline_backward_workspace(int64_t batch, int64_t len, int grad_mask, 
  * Replaces PesqLossTriton.raw / mos / forward
  * (torch_pesq/triton_ops/loss.py:104-147,203-215): peak normalisation,
  * level alignment, pre-emphasis, STFT, Bark, perceptual chain and the MOS
- * epilogue, in five kernels.  grad_mask (PESQ_GRAD_*) selects which inputs
+ * epilogue, in five kernels (six for rows longer than 131072 samples).  The
+ * peak normalisation cancels in the level alignment and is not formed; the
+ * workspace's "p" and "f" hold the pre-emphasised and band-passed signals in
+ * the units of the input.  grad_mask (PESQ_GRAD_*) selects which inputs
  * the backward will need; it must match the backward call.  Requires
  * len >= 15 and at least 20 frames (1 + (len + len % 256 - 512) / 256). */
 int pesq_pipeline_forward(const float *ref, const float *deg, int64_t batch, int64_t len,

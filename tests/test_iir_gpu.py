@@ -38,7 +38,8 @@ def _peak_rel(got, want):
 
 
 @pytest.mark.parametrize("name", sorted(FILTERS))
-@pytest.mark.parametrize("length", [1, 17, 4095, 4096, 4097, 20000])
+# 1024 samples per scan block: block edges, a partial last block, several blocks
+@pytest.mark.parametrize("length", [1, 17, 1023, 1024, 1025, 4097, 20000])
 def test_forward_and_adjoint(name, length):
     b, a = FILTERS[name]
     mod = HipIIR(b, a).cuda()
@@ -53,7 +54,9 @@ def test_forward_and_adjoint(name, length):
     assert _peak_rel(gx, O.lfilter64(g.numpy(), b, a, reverse=True)) < TOL
 
 
-@pytest.mark.parametrize("length", [128000, 960000])
+# up to 128 blocks the output kernel scans the preceding block aggregates
+# itself (in groups of 64 blocks); longer rows go through the prefix kernel
+@pytest.mark.parametrize("length", [65537, 128000, 131072, 132097, 960000])
 def test_long_signals(length):
     b, a = FILTERS["power"]
     mod = HipIIR(b, a).cuda()

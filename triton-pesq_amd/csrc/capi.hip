@@ -28,20 +28,28 @@ static void mat_mul(const double *x, const double *y, double *out) {
     out[3] = r3;
 }
 
-static int fill_sections(IirTable &t, int first, const pesq_iir_sections &s) {
+// Sections are stored with b2 = 0: a section with b2 != 0 and a2 != 0 is
+// rewritten as the direct term b2 / a2 plus the section
+// (b0 - b2 / a2) + (b1 - a1 b2 / a2) z^-1 over the same denominator, which is
+// the same transfer function.  `direct` accumulates the direct terms.
+static int fill_sections(IirTable &t, int first, const pesq_iir_sections &s, double &direct) {
     PESQ_CHECK_ARG(s.count >= 1 && first + s.count <= kMaxSections,
                    "an IIR filter needs 1..%d sections in total, got %d", kMaxSections,
                    first + s.count);
     for (int k = 0; k < s.count; ++k) {
         const int q = first + k;
-        t.b0[q] = s.b0[k];
-        t.b1[q] = s.b1[k];
-        t.b2[q] = s.b2[k];
-        t.a1[q] = s.a1[k];
-        t.a2[q] = s.a2[k];
         PESQ_CHECK_ARG(std::isfinite(s.b0[k]) && std::isfinite(s.b1[k]) && std::isfinite(s.b2[k]) &&
                            std::isfinite(s.a1[k]) && std::isfinite(s.a2[k]),
                        "non finite IIR coefficient in section %d", k);
+        PESQ_CHECK_ARG(s.b2[k] == 0.0 || s.a2[k] != 0.0,
+                       "section %d has b2 != 0 over a first order denominator (an FIR tail)", k);
+        const double d = s.b2[k] == 0.0 ? 0.0 : s.b2[k] / s.a2[k];
+        direct += d;
+        t.b0[q] = s.b0[k] - d;
+        t.b1[q] = s.b1[k] - s.a1[k] * d;
+        t.b2[q] = 0.0;
+        t.a1[q] = s.a1[k];
+        t.a2[q] = s.a2[k];
         // chunk transfer powers: level 0 = A^kChunk, level j = A^(kChunk 2^j)
         const double a[4] = {-s.a1[k], 1.0, -s.a2[k], 0.0};
         double p[4] = {1.0, 0.0, 0.0, 1.0};
@@ -61,9 +69,9 @@ static int pack_iir(IirTable &t, const pesq_iir_sections *a, const pesq_iir_sect
     t.nb = b ? b->count : 0;
     t.c0a = a->c0;
     t.c0b = b ? b->c0 : 0.0;
-    if (int st = fill_sections(t, 0, *a)) return st;
+    if (int st = fill_sections(t, 0, *a, t.c0a)) return st;
     if (b) {
-        if (int st = fill_sections(t, a->count, *b)) return st;
+        if (int st = fill_sections(t, a->count, *b, t.c0b)) return st;
     }
     return PESQ_OK;
 }

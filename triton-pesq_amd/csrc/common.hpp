@@ -77,18 +77,47 @@ __device__ __forceinline__ double wave_max(double v) {
     return v;
 }
 
+// x[n] for n < len, else 0, without a branch around the load (len >= 1): the
+// index is clamped and the value selected, so that consecutive calls issue
+// their loads back to back instead of waiting on each one.
+__device__ __forceinline__ float load_or_zero(const float *x, int64_t n, int64_t len) {
+    const float v = x[n < len ? n : len - 1];
+    return n < len ? v : 0.0f;
+}
+
+// sum_{i < n} p[i * stride] accumulated in the order i = 0, 1, ..., n - 1
+// (the same value as the plain loop), n >= 1.  The loads are issued in
+// batches of 8 (indices past the end are clamped and their values dropped)
+// so that a batch costs one memory latency instead of eight.
+__device__ __forceinline__ double strided_sum(const double *p, int n, int64_t stride) {
+    double s = 0.0;
+    for (int i0 = 0; i0 < n; i0 += 8) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p[int64_t(i0 + u < n ? i0 + u : n - 1) * stride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (i0 + u < n) s += v[u];
+        }
+    }
+    return s;
+}
+
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) {
     return (a + b - 1) / b;
 }
 
 // Edge ramp of the pre-emphasis stage: samples 0..14 are weighted (k+1)/16,
 // the last 15 samples (n-k)/16, both weights for rows shorter than 30, in the
-// order head then tail.
+// order head then tail.  Every factor is a small integer times 2^-4, so the
+// products are exact; samples at least kEdge from both ends have weight 1.
+constexpr int kEdge = 15;
+
 __device__ __forceinline__ double edge_weight(int64_t n, int64_t len) {
-    double w = 1.0;
-    if (n < 15) w = static_cast<double>(n + 1) * 0.0625;
-    if (n >= len - 15) w *= static_cast<double>(len - n) * 0.0625;
-    return w;
+    const int64_t head = n + 1 < 16 ? n + 1 : 16;
+    const int64_t tail = len - n < 16 ? len - n : 16;
+    return static_cast<double>(static_cast<int>(head)) * 0.0625 *
+           (static_cast<double>(static_cast<int>(tail)) * 0.0625);
 }
 
 }  // namespace pesq

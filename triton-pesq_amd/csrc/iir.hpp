@@ -1,24 +1,32 @@
 // Chunked parallel scan of a bank of parallel second order sections, fp64 state.
 //
 // A filter is realised in parallel form, y = c0 x + sum_k y_k, where section k
-// is a direct form II transposed biquad
+// is a direct form II transposed biquad with b2 = 0 (the form partial
+// fractions give; the table packing folds any b2 into the direct term)
 //     y_k  = b0 x + z1
 //     z1'  = b1 x - a1 y_k + z2
-//     z2'  = b2 x - a2 y_k
+//     z2'  = - a2 y_k
 // i.e. the state z = (z1, z2) evolves as z' = A_k z + beta_k x with
 // A_k = [[-a1, 1], [-a2, 0]].  Because every A_k is 2x2 and the sections are
 // independent, the chunk transfer matrices are block diagonal (4 numbers per
 // section) and the scan combine costs 4 FMAs per section.
 //
-// Geometry: one lane runs the recursion over a chunk of kChunk samples; a
-// wavefront covers 64 consecutive chunks, a workgroup kWaves wavefronts (one
-// "block" of kBlockSpan samples).  Two kernels per pass:
-//   aggregate: zero state run per chunk, in-wave Kogge-Stone scan, block end
-//              state written to `aggr` (the block's contribution to the state
-//              after it, given a zero state before it);
-//   output:    zero state run, in-wave scan, block start state from a scan of
-//              the preceding blocks' aggregates, lane start state, re-run of
-//              the recursion from it, outputs.
+// Geometry.  A lane runs the recursion of all sections over a chunk of kChunk
+// consecutive samples (the sections are independent chains, so the lane has
+// that much instruction level parallelism); a workgroup is one wavefront and
+// covers one block of kBlockSpan = 64 kChunk samples of one row.  Nothing is
+// shared between wavefronts, so the kernels have no LDS and no barriers.
+//   aggregate: zero state run per chunk, in-wave Kogge-Stone scan; the block's
+//              end state per section (given a zero state before the block) is
+//              written to `aggr`, laid out [row][section][block][2];
+//   prefix:    rows of more than kLookbackBlocks blocks only: per (row,
+//              section) an exclusive scan of the block aggregates, written over
+//              them (aggr[b] becomes the state at the start of block b);
+//   output:    zero state run, in-wave scan, block start state (scanned from
+//              the preceding blocks' aggregates, or read after the prefix
+//              kernel) injected at lane 0 of the in-wave scan, so that the
+//              scan gives the true state at the start of every chunk, second
+//              run from it; per sample y = c0 x + y_0 + y_1 + ... in this order.
 // The time axis can be reversed (adjoint filter) by the Mode policy.
 //
 // Two filters (A and B) can be scanned in the same pass on different inputs;
@@ -30,24 +38,31 @@
 
 namespace pesq {
 
-constexpr int kChunk = 16;                      // samples per lane
-constexpr int kWaves = 4;                       // wavefronts per workgroup
-constexpr int kBlockChunks = kWave * kWaves;    // chunks per workgroup
-constexpr int64_t kBlockSpan = int64_t(kBlockChunks) * kChunk;  // samples per workgroup
+#ifndef PESQ_CHUNK
+#define PESQ_CHUNK 16
+#endif
+constexpr int kChunk = PESQ_CHUNK;                         // samples per lane
+constexpr int kSpan = kWave * kChunk;                      // samples per block
+constexpr int64_t kBlockSpan = kSpan;
 constexpr int kMaxSections = PESQ_IIR_MAX_SECTIONS;
-// power levels: A^(kChunk * 2^j); j = 0..5 in-wave, 6 = one wave, 8 = one
-// block (kBlockChunks = 2^8 chunks), 8..13 = the block level scan
-constexpr int kLevelWave = 6;
-constexpr int kLevelBlock = 8;
+// power levels: A^(kChunk 2^j); j = 0..5 in-wave, 6 = one block, 6..11 the
+// block level scan over 64 blocks
+constexpr int kLevelBlock = 6;
 constexpr int kLevels = 14;
-static_assert(kBlockChunks == (1 << kLevelBlock), "block must be 2^8 chunks");
+static_assert(kSpan == kChunk << kLevelBlock, "a block is 2^6 chunks");
+// rows of at most this many blocks scan their preceding block aggregates in
+// the output kernel; longer rows run the prefix kernel first
+#ifndef PESQ_LOOKBACK_BLOCKS
+#define PESQ_LOOKBACK_BLOCKS 128
+#endif
+constexpr int kLookbackBlocks = PESQ_LOOKBACK_BLOCKS;
 
 struct IirTable {
     int32_t na, nb;      // sections of filter A, then of filter B
     double c0a, c0b;     // direct feed through of A and B
-    double b0[kMaxSections], b1[kMaxSections], b2[kMaxSections];
+    double b0[kMaxSections], b1[kMaxSections], b2[kMaxSections];  // b2 = 0 (packing)
     double a1[kMaxSections], a2[kMaxSections];
-    double pw[kLevels][kMaxSections][4];  // A_k^(kChunk 2^j), row major 2x2
+    double pw[kLevels][kMaxSections][4];     // A_k^(kChunk 2^j), row major 2x2
 };
 
 // --------------------------------------------------------------------------
@@ -56,17 +71,31 @@ struct IirTable {
 
 template <int NS>
 struct Bank {
-    double z[NS > 0 ? NS : 1][2];
+    double u[NS > 0 ? NS : 1], v[NS > 0 ? NS : 1];  // z1, z2 per section
 
     __device__ __forceinline__ void zero() {
 #pragma unroll
-        for (int k = 0; k < NS; ++k) z[k][0] = z[k][1] = 0.0;
+        for (int k = 0; k < NS; ++k) u[k] = v[k] = 0.0;
     }
 };
 
+// The table pointer through an empty asm statement: loads through the result
+// are issued again instead of being kept live in registers from earlier ones
+// (the coefficients are re-read from the scalar cache for each run).
+// (p must be wave-uniform)
+template <typename T>
+__device__ __forceinline__ const T *reload(const T *p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    asm volatile("" : "+s"(lo), "+s"(hi));
+    return reinterpret_cast<const T *>((uint64_t(hi) << 32) | lo);
+}
+
+// Coefficients of NS sections starting at section S0 (b2 = 0 in the table).
 template <int S0, int NS>
 struct Coeffs {
-    double b0[NS > 0 ? NS : 1], b1[NS > 0 ? NS : 1], b2[NS > 0 ? NS : 1];
+    double b0[NS > 0 ? NS : 1], b1[NS > 0 ? NS : 1];
     double a1[NS > 0 ? NS : 1], a2[NS > 0 ? NS : 1];
     double c0;
 
@@ -75,37 +104,36 @@ struct Coeffs {
         for (int k = 0; k < NS; ++k) {
             b0[k] = t.b0[S0 + k];
             b1[k] = t.b1[S0 + k];
-            b2[k] = t.b2[S0 + k];
             a1[k] = t.a1[S0 + k];
             a2[k] = t.a2[S0 + k];
         }
         c0 = direct;
     }
 
-    // one time step: consumes x, advances the state, returns the output
+    // one time step: consumes x, advances the state, returns c0 x + sum_k y_k
     __device__ __forceinline__ double step(Bank<NS> &s, double x) const {
         double y = c0 * x;
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
-            const double yk = fma(b0[k], x, s.z[k][0]);
-            s.z[k][0] = fma(-a1[k], yk, fma(b1[k], x, s.z[k][1]));
-            s.z[k][1] = fma(-a2[k], yk, b2[k] * x);
+            const double yk = fma(b0[k], x, s.u[k]);
+            s.u[k] = fma(-a1[k], yk, fma(b1[k], x, s.v[k]));
+            s.v[k] = -a2[k] * yk;
             y += yk;
         }
         return y;
     }
 };
 
-// z <- P z + add, P = A^(kChunk 2^level) per section
+// z <- P z + add, P = A_k^(kChunk 2^level) per section
 template <int S0, int NS>
 __device__ __forceinline__ void apply_power(const IirTable &t, int level, Bank<NS> &z,
                                             const Bank<NS> &add) {
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
         const double *p = t.pw[level][S0 + k];
-        const double u = z.z[k][0], v = z.z[k][1];
-        z.z[k][0] = fma(p[0], u, fma(p[1], v, add.z[k][0]));
-        z.z[k][1] = fma(p[2], u, fma(p[3], v, add.z[k][1]));
+        const double u = z.u[k], v = z.v[k];
+        z.u[k] = fma(p[0], u, fma(p[1], v, add.u[k]));
+        z.v[k] = fma(p[2], u, fma(p[3], v, add.v[k]));
     }
 }
 
@@ -120,315 +148,410 @@ __device__ __forceinline__ void scan_wave(const IirTable &t, int level0, Bank<NS
         Bank<NS> o;
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
-            o.z[k][0] = shfl_up(z.z[k][0], d);
-            o.z[k][1] = shfl_up(z.z[k][1], d);
+            o.u[k] = shfl_up(z.u[k], d);
+            o.v[k] = shfl_up(z.v[k], d);
         }
         if (lane >= d) {
-            // z <- z + P o, written as o <- P o + z then copy
-            apply_power<S0, NS>(t, level0 + j, o, z);
-#pragma unroll
-            for (int k = 0; k < NS; ++k) {
-                z.z[k][0] = o.z[k][0];
-                z.z[k][1] = o.z[k][1];
-            }
+            apply_power<S0, NS>(t, level0 + j, o, z);  // o <- P o + z
+            z = o;
         }
     }
 }
-
-template <int NS>
-__device__ __forceinline__ void shift_up_one(Bank<NS> &z, int lane) {
-#pragma unroll
-    for (int k = 0; k < NS; ++k) {
-        const double u = shfl_up(z.z[k][0], 1), v = shfl_up(z.z[k][1], 1);
-        z.z[k][0] = lane == 0 ? 0.0 : u;
-        z.z[k][1] = lane == 0 ? 0.0 : v;
-    }
-}
-
-// --------------------------------------------------------------------------
-// the two kernels, parametrised by a Mode policy:
-//   Mode::kInputs                 number of float inputs per sample (1 or 2)
-//   Mode::kReverse                process the time axis back to front
-//   Mode::kAccumulates            the output pass reduces a per block sum
-//   m.load(row, n, in[])          raw inputs at physical sample n
-//   m.inputs(n, in[], xa, xb)     filter inputs from the raw ones
-//   m.observe(o, in[]) / reduce_observed / combine_observed / observed(row, blk, o)
-//                                 aggregate-pass reduction over the raw inputs
-//   m.setup(row, blk, sh, lane)   output pass, wavefront 0 before the block
-//                                 barrier: per row constants into sh[0..3]
-//   m.emit(row, n, ya, yb, acc, sh) consume the outputs of sample n
-//   m.finish(row, blk, total)     block total of the accumulator
-// The scan itself is linear, so it runs in the units of the raw inputs and a
-// per row normalisation is applied by emit.
-// --------------------------------------------------------------------------
 
 template <int NA, int NB>
 struct BankPair {
     Bank<NA> a;
     Bank<NB> b;
+
+    __device__ __forceinline__ void zero() {
+        a.zero();
+        b.zero();
+    }
+    __device__ __forceinline__ void scan(const IirTable &t, int level0, int lane) {
+        if constexpr (NA > 0) scan_wave<0, NA>(t, level0, a, lane);
+        if constexpr (NB > 0) scan_wave<NA, NB>(t, level0, b, lane);
+    }
+    __device__ __forceinline__ void power(const IirTable &t, int level, const BankPair &add) {
+        if constexpr (NA > 0) apply_power<0, NA>(t, level, a, add.a);
+        if constexpr (NB > 0) apply_power<NA, NB>(t, level, b, add.b);
+    }
+    // section k (0 .. NA + NB - 1) as (u, v) references
+    __device__ __forceinline__ double &u(int k) { return k < NA ? a.u[k] : b.u[k - NA]; }
+    __device__ __forceinline__ double &v(int k) { return k < NA ? a.v[k] : b.v[k - NA]; }
 };
 
+// The aggregates of blocks base + lane (zero past blk) of one row.
 template <int NA, int NB>
-__device__ __forceinline__ void store_state(double *dst, const BankPair<NA, NB> &s) {
+__device__ __forceinline__ BankPair<NA, NB> load_group(const double *row_aggr, int nblk, int base,
+                                                       int blk, int lane) {
+    BankPair<NA, NB> v;
+    const int jb = base + lane;
+    const int jc = jb < blk ? jb : (blk > 0 ? blk - 1 : 0);
 #pragma unroll
-    for (int k = 0; k < NA; ++k) {
-        dst[2 * k] = s.a.z[k][0];
-        dst[2 * k + 1] = s.a.z[k][1];
+    for (int k = 0; k < NA + NB; ++k) {
+        const double *src = row_aggr + (int64_t(k) * nblk + jc) * 2;
+        const double u = src[0], w = src[1];
+        v.u(k) = jb < blk ? u : 0.0;
+        v.v(k) = jb < blk ? w : 0.0;
     }
-#pragma unroll
-    for (int k = 0; k < NB; ++k) {
-        dst[2 * (NA + k)] = s.b.z[k][0];
-        dst[2 * (NA + k) + 1] = s.b.z[k][1];
-    }
+    return v;
 }
 
-template <int NA, int NB>
-__device__ __forceinline__ void load_state(BankPair<NA, NB> &s, const double *src, double scale) {
+// --------------------------------------------------------------------------
+// the kernels, parametrised by a Mode policy:
+//   Mode::kInputs                 raw inputs per sample (1 or 2)
+//   Mode::kOutputs                outputs per sample (1 or 2)
+//   Mode::kReverse                process the time axis back to front
+//   Mode::kAccumulates            the output pass reduces a per block sum
+//   Mode::kRamp                   the Mode uses the edge ramp weight w of the
+//                                 sample (edge_weight(n, len)); otherwise the
+//                                 kernels pass w = 1
+//   m.src(row, q)                 row base of raw input q (physical order)
+//   m.dst(row, q)                 row base of output q, or null when the row
+//                                 does not write that output
+//   m.inputs(w, in[], xa, xb)     filter inputs of a sample from its raw inputs
+//   m.setup(row, sh, lane)        output pass: per row constants into sh[0..3]
+//                                 (wave-uniform values)
+//   m.compute(w, ya, yb, acc, sh, out[]) the outputs of a sample from the
+//                                 outputs ya, yb of the two filters
+//   m.finish(row, blk, total)     block total of the accumulator
+// The scan is linear, so it runs in the units of the raw inputs; per row
+// constants are applied by compute.
+//
+// Memory access: a lane reads and writes its kChunk consecutive samples as
+// 16-byte vectors when the row's alignment allows it (the whole wavefront
+// then covers kSpan contiguous samples per instruction group), else element
+// by element; the last chunk of a row is handled element by element.
+// --------------------------------------------------------------------------
+
+// physical index of the first sample of a full chunk starting at time j0
+template <bool kRev>
+__device__ __forceinline__ int64_t chunk_lo(int64_t j0, int64_t len) {
+    return kRev ? len - j0 - kChunk : j0;
+}
+
+template <class Mode>
+__device__ __forceinline__ void load_chunk(const Mode &m, int row, int64_t j0, int64_t len,
+                                           float (&in)[kChunk][Mode::kInputs]) {
+    const bool full = j0 + kChunk <= len;
+    const int64_t lo = chunk_lo<Mode::kReverse>(j0, len);
 #pragma unroll
-    for (int k = 0; k < NA; ++k) {
-        s.a.z[k][0] = src[2 * k] * scale;
-        s.a.z[k][1] = src[2 * k + 1] * scale;
-    }
+    for (int q = 0; q < Mode::kInputs; ++q) {
+        const float *base = m.src(row, q);
+        float buf[kChunk];
+        if (full && (reinterpret_cast<uintptr_t>(base + lo) & 15) == 0) {
+            const float4 *p4 = reinterpret_cast<const float4 *>(base + lo);
 #pragma unroll
-    for (int k = 0; k < NB; ++k) {
-        s.b.z[k][0] = src[2 * (NA + k)] * scale;
-        s.b.z[k][1] = src[2 * (NA + k) + 1] * scale;
-    }
-}
-
-template <int NA, int NB>
-__device__ __forceinline__ void scan_pair(const IirTable &t, int level0, BankPair<NA, NB> &s,
-                                          int lane) {
-    if constexpr (NA > 0) scan_wave<0, NA>(t, level0, s.a, lane);
-    if constexpr (NB > 0) scan_wave<NA, NB>(t, level0, s.b, lane);
-}
-
-template <int NA, int NB>
-__device__ __forceinline__ void power_pair(const IirTable &t, int level, BankPair<NA, NB> &s,
-                                           const BankPair<NA, NB> &add) {
-    if constexpr (NA > 0) apply_power<0, NA>(t, level, s.a, add.a);
-    if constexpr (NB > 0) apply_power<NA, NB>(t, level, s.b, add.b);
-}
-
-template <int NA, int NB>
-__device__ __forceinline__ void zero_pair(BankPair<NA, NB> &s) {
-    s.a.zero();
-    s.b.zero();
-}
-
-template <int NA, int NB, class Mode>
-__global__ void __launch_bounds__(kWave *kWaves)
-    iir_aggregate_kernel(Mode m, const IirTable *__restrict__ table, double *__restrict__ aggr,
-                         int64_t len, int nblk) {
-    constexpr int NSTATE = 2 * (NA + NB);
-    __shared__ double totals[kWaves][NSTATE];
-    __shared__ float observed[kWaves];
-
-    const IirTable &t = *table;
-    const int row = blockIdx.x / nblk;
-    const int blk = blockIdx.x - row * nblk;
-    const int wave = threadIdx.x / kWave;
-    const int lane = threadIdx.x % kWave;
-    const int64_t j0 = (int64_t(blk) * kBlockChunks + wave * kWave + lane) * kChunk;
-
-    Coeffs<0, NA> ca;
-    Coeffs<NA, NB> cb;
-    ca.load(t, t.c0a);
-    cb.load(t, t.c0b);
-
-    BankPair<NA, NB> s;
-    zero_pair(s);
-    float obs = 0.0f;
-
+            for (int r = 0; r < kChunk / 4; ++r) {
+                const float4 w = p4[r];
+                buf[4 * r] = w.x;
+                buf[4 * r + 1] = w.y;
+                buf[4 * r + 2] = w.z;
+                buf[4 * r + 3] = w.w;
+            }
 #pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-        const int64_t j = j0 + i;
-        float in[Mode::kInputs];
-        double xa = 0.0, xb = 0.0;
-        if (j < len) {
-            const int64_t n = Mode::kReverse ? len - 1 - j : j;
-            m.load(row, n, in);
-            m.inputs(n, in, xa, xb);
-            obs = m.observe(obs, in);
-        }
-        if constexpr (NA > 0) ca.step(s.a, xa);
-        if constexpr (NB > 0) cb.step(s.b, xb);
-    }
-
-    scan_pair(t, 0, s, lane);
-    if (lane == kWave - 1) store_state(totals[wave], s);
-    obs = m.reduce_observed(obs);
-    if (lane == 0) observed[wave] = obs;
-    __syncthreads();
-
-    if (threadIdx.x == 0) {
-        BankPair<NA, NB> acc, w;
-        load_state(acc, totals[0], 1.0);
-        for (int i = 1; i < kWaves; ++i) {
-            load_state(w, totals[i], 1.0);
-            power_pair(t, kLevelWave, acc, w);
-        }
-        store_state(aggr + (int64_t(row) * nblk + blk) * NSTATE, acc);
-        float o = observed[0];
-        for (int i = 1; i < kWaves; ++i) o = m.combine_observed(o, observed[i]);
-        m.observed(row, blk, o);
-    }
-}
-
-template <int NA, int NB, class Mode>
-__global__ void __launch_bounds__(kWave *kWaves)
-    iir_output_kernel(Mode m, const IirTable *__restrict__ table,
-                      const double *__restrict__ aggr, int64_t len, int nblk) {
-    constexpr int NSTATE = 2 * (NA + NB);
-    __shared__ double totals[kWaves][NSTATE];
-    __shared__ double prefix[NSTATE];
-    __shared__ double accum[kWaves];
-    __shared__ double consts[4];
-
-    const IirTable &t = *table;
-    const int row = blockIdx.x / nblk;
-    const int blk = blockIdx.x - row * nblk;
-    const int wave = threadIdx.x / kWave;
-    const int lane = threadIdx.x % kWave;
-    const int64_t j0 = (int64_t(blk) * kBlockChunks + wave * kWave + lane) * kChunk;
-
-    Coeffs<0, NA> ca;
-    Coeffs<NA, NB> cb;
-    ca.load(t, t.c0a);
-    cb.load(t, t.c0b);
-
-    // raw inputs of the chunk stay in registers for the second run
-    float in[kChunk][Mode::kInputs];
-#pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-        const int64_t j = j0 + i;
-        if (j < len) {
-            m.load(row, Mode::kReverse ? len - 1 - j : j, in[i]);
+            for (int i = 0; i < kChunk; ++i) in[i][q] = buf[Mode::kReverse ? kChunk - 1 - i : i];
         } else {
 #pragma unroll
-            for (int q = 0; q < Mode::kInputs; ++q) in[i][q] = 0.0f;
+            for (int i = 0; i < kChunk; ++i) {
+                const int64_t j = j0 + i;
+                const int64_t jc = j < len ? j : len - 1;
+                const float v = base[Mode::kReverse ? len - 1 - jc : jc];
+                in[i][q] = j < len ? v : 0.0f;
+            }
         }
     }
+}
 
-    // zero state run -> chunk end state
+// out[i] is stored at time index j0 + i
+__device__ __forceinline__ void store_chunk(float *base, const float (&out)[kChunk], bool kRev,
+                                            int64_t j0, int64_t len) {
+    const bool full = j0 + kChunk <= len;
+    const int64_t lo = kRev ? len - j0 - kChunk : j0;
+    if (full && (reinterpret_cast<uintptr_t>(base + lo) & 15) == 0) {
+        float4 *p4 = reinterpret_cast<float4 *>(base + lo);
+#pragma unroll
+        for (int r = 0; r < kChunk / 4; ++r) {
+            float e[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int i = 4 * r + c;
+                e[c] = out[kRev ? kChunk - 1 - i : i];
+            }
+            p4[r] = make_float4(e[0], e[1], e[2], e[3]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) {
+            const int64_t j = j0 + i;
+            if (j < len) base[kRev ? len - 1 - j : j] = out[i];
+        }
+    }
+}
+
+// edge ramp weight at time index j; 1 in chunks at least kEdge from both ends
+template <class Mode>
+__device__ __forceinline__ double ramp_weight(bool edge, int64_t j, int64_t len) {
+    if constexpr (!Mode::kRamp) return 1.0;
+    return edge ? edge_weight(Mode::kReverse ? len - 1 - j : j, len) : 1.0;
+}
+
+// filter inputs of time index j (zero past the end of the row)
+template <class Mode>
+__device__ __forceinline__ void chunk_inputs(const Mode &m, const float (&in)[Mode::kInputs],
+                                             double w, int64_t j, int64_t len, double &xa,
+                                             double &xb) {
+    m.inputs(w, in, xa, xb);
+    if (j >= len) xa = xb = 0.0;
+}
+
+template <int NA, int NB, class Mode>
+__global__ void __launch_bounds__(kWave)
+    iir_aggregate_kernel(Mode m, const IirTable *__restrict__ table, double *__restrict__ aggr,
+                         int64_t len, int nblk) {
+    constexpr int NS = NA + NB;
+    const IirTable &t = *table;
+    const int row = blockIdx.x / nblk;
+    const int blk = blockIdx.x - row * nblk;
+    const int lane = threadIdx.x;
+    const int64_t j0 = int64_t(blk) * kSpan + int64_t(lane) * kChunk;
+    // with len >= 2 kEdge + kChunk only the first and last chunks are edges;
+    // shorter rows take the general path everywhere
+    const bool edge = j0 < kEdge || j0 + kChunk + kEdge > len;
+
+    Coeffs<0, NA> ca;
+    Coeffs<NA, NB> cb;
+    ca.load(t, t.c0a);
+    cb.load(t, t.c0b);
+
+    float in[kChunk][Mode::kInputs];
+    load_chunk(m, row, j0, len, in);
+
     BankPair<NA, NB> s;
-    zero_pair(s);
+    s.zero();
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) {
-        const int64_t j = j0 + i;
-        double xa = 0.0, xb = 0.0;
-        if (j < len) m.inputs(Mode::kReverse ? len - 1 - j : j, in[i], xa, xb);
+        double xa, xb;
+        chunk_inputs(m, in[i], ramp_weight<Mode>(edge, j0 + i, len), j0 + i, len, xa, xb);
         if constexpr (NA > 0) ca.step(s.a, xa);
         if constexpr (NB > 0) cb.step(s.b, xb);
     }
-
-    scan_pair(t, 0, s, lane);  // s = inclusive end state of the wave's chunks
-    if (lane == kWave - 1) store_state(totals[wave], s);
-
-    // state at the start of this block: scan of the preceding blocks' aggregates
-    if (wave == 0) {
-        BankPair<NA, NB> carry;
-        zero_pair(carry);
-        for (int base = 0; base < blk; base += kWave) {
-            BankPair<NA, NB> v, zero;
-            zero_pair(zero);
-            const int jb = base + lane;
-            if (jb < blk) {
-                load_state(v, aggr + (int64_t(row) * nblk + jb) * NSTATE, 1.0);
-            } else {
-                zero_pair(v);
-            }
-            // element 0 also carries the state entering the tile
-            BankPair<NA, NB> injected = carry;
-            power_pair(t, kLevelBlock, injected, zero);
-            if (lane == 0) {
-                if constexpr (NA > 0) {
+    s.scan(t, 0, lane);
+    if (lane == kWave - 1) {
 #pragma unroll
-                    for (int k = 0; k < NA; ++k) {
-                        v.a.z[k][0] += injected.a.z[k][0];
-                        v.a.z[k][1] += injected.a.z[k][1];
-                    }
-                }
-                if constexpr (NB > 0) {
-#pragma unroll
-                    for (int k = 0; k < NB; ++k) {
-                        v.b.z[k][0] += injected.b.z[k][0];
-                        v.b.z[k][1] += injected.b.z[k][1];
-                    }
-                }
-            }
-            scan_pair(t, kLevelBlock, v, lane);
-            // state at the end of block min(blk, base + 64) - 1
-            const int src = (blk - base < kWave ? blk - base : kWave) - 1;
-            double flat[NSTATE];
-            store_state(flat, v);
-#pragma unroll
-            for (int q = 0; q < NSTATE; ++q) flat[q] = shfl(flat[q], src);
-            load_state(carry, flat, 1.0);
+        for (int k = 0; k < NS; ++k) {
+            double *dst = aggr + ((int64_t(row) * NS + k) * nblk + blk) * 2;
+            dst[0] = s.u(k);
+            dst[1] = s.v(k);
         }
-        if (lane == 0) store_state(prefix, carry);
-        m.setup(row, blk, consts, lane);
     }
-    __syncthreads();
+}
 
-    // state entering this wave: the block prefix advanced over earlier waves
+// Exclusive scan of the block aggregates, one (row, section) sequence per
+// wavefront; aggr[b] is replaced by the state at the start of block b.
+constexpr int kPrefixWaves = 4;
+
+template <int NS>
+__global__ void __launch_bounds__(kWave *kPrefixWaves)
+    iir_prefix_kernel(const IirTable *__restrict__ table, double *__restrict__ aggr, int nblk,
+                      int64_t nseq) {
+    const IirTable &t = *table;
+    const int64_t seq = int64_t(blockIdx.x) * kPrefixWaves +
+                        __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+    if (seq >= nseq) return;  // whole wavefronts only
+    const int k = static_cast<int>(seq % NS);
+    const int lane = threadIdx.x % kWave;
+    double *agg = aggr + seq * nblk * 2;
+    double cu = 0.0, cv = 0.0;  // carry: state at the end of block base - 1
+    for (int base = 0; base < nblk; base += kWave) {
+        const int jb = base + lane;
+        const int jc = jb < nblk ? jb : nblk - 1;
+        double u = agg[2 * jc], v = agg[2 * jc + 1];
+        if (jb >= nblk) u = v = 0.0;
+        if (lane == 0) {
+            const double *p = t.pw[kLevelBlock][k];
+            u = fma(p[0], cu, fma(p[1], cv, u));
+            v = fma(p[2], cu, fma(p[3], cv, v));
+        }
+#pragma unroll
+        for (int j = 0; j < 6; ++j) {
+            const int d = 1 << j;
+            const double ou = shfl_up(u, d), ov = shfl_up(v, d);
+            if (lane >= d) {
+                const double *p = t.pw[kLevelBlock + j][k];
+                u = fma(p[0], ou, fma(p[1], ov, u));
+                v = fma(p[2], ou, fma(p[3], ov, v));
+            }
+        }
+        double eu = shfl_up(u, 1), ev = shfl_up(v, 1);
+        if (lane == 0) {
+            eu = cu;
+            ev = cv;
+        }
+        if (jb < nblk) {
+            agg[2 * jb] = eu;
+            agg[2 * jb + 1] = ev;
+        }
+        const int src = (nblk - base < kWave ? nblk - base : kWave) - 1;
+        cu = shfl(u, src);
+        cv = shfl(v, src);
+    }
+}
+
+template <int NA, int NB, class Mode>
+__global__ void __launch_bounds__(kWave)
+    iir_output_kernel(Mode m, const IirTable *__restrict__ table,
+                      const double *__restrict__ aggr, int64_t len, int nblk, int prefixed) {
+    constexpr int NS = NA + NB;
+    const IirTable &t = *table;
+    const int row = blockIdx.x / nblk;
+    const int blk = blockIdx.x - row * nblk;
+    const int lane = threadIdx.x;
+    const int64_t j0 = int64_t(blk) * kSpan + int64_t(lane) * kChunk;
+    const bool edge = j0 < kEdge || j0 + kChunk + kEdge > len;
+
+    // the block start states (or the first group of aggregates), the row
+    // constants and the raw inputs are all requested before any of them is used
+    const double *row_aggr = aggr + int64_t(row) * NS * nblk * 2;
     BankPair<NA, NB> p;
-    load_state(p, prefix, 1.0);
-    for (int i = 0; i < wave; ++i) {
-        BankPair<NA, NB> tot;
-        load_state(tot, totals[i], 1.0);
-        power_pair(t, kLevelWave, p, tot);
-    }
-
-    // lane start state = A^(lane L) p + (inclusive end state of lane - 1)
-    BankPair<NA, NB> e;
-    if (lane == 0) {
-        e = p;
+    if (prefixed) {
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+            const double *src = row_aggr + (int64_t(k) * nblk + blk) * 2;
+            p.u(k) = src[0];
+            p.v(k) = src[1];
+        }
     } else {
-        zero_pair(e);
+        p = load_group<NA, NB>(row_aggr, nblk, 0, blk, lane);
     }
-    scan_pair(t, 0, e, lane);
-    if constexpr (NA > 0) shift_up_one(s.a, lane);
-    if constexpr (NB > 0) shift_up_one(s.b, lane);
-    if constexpr (NA > 0) {
+    double sh[4];
+    m.setup(row, sh, lane);
+    float in[kChunk][Mode::kInputs];
+    load_chunk(m, row, j0, len, in);
+
+    // state at the start of the block, scanned from the preceding blocks'
+    // aggregates while the inputs are in flight (wave-uniform afterwards)
+    if (!prefixed) {
+        BankPair<NA, NB> carry;
+        carry.zero();
+        for (int base = 0; base < blk; base += kWave) {
+            BankPair<NA, NB> v = base == 0 ? p : load_group<NA, NB>(row_aggr, nblk, base, blk, lane);
+            // the state entering the group is carried into its first element
+            if (lane == 0) {
+                BankPair<NA, NB> c = carry;
+                c.power(t, kLevelBlock, v);
+                v = c;
+            }
+            v.scan(t, kLevelBlock, lane);
+            const int src = (blk - base < kWave ? blk - base : kWave) - 1;
 #pragma unroll
-        for (int k = 0; k < NA; ++k) {
-            s.a.z[k][0] += e.a.z[k][0];
-            s.a.z[k][1] += e.a.z[k][1];
+            for (int k = 0; k < NS; ++k) {
+                carry.u(k) = shfl(v.u(k), src);
+                carry.v(k) = shfl(v.v(k), src);
+            }
         }
-    }
-    if constexpr (NB > 0) {
-#pragma unroll
-        for (int k = 0; k < NB; ++k) {
-            s.b.z[k][0] += e.b.z[k][0];
-            s.b.z[k][1] += e.b.z[k][1];
-        }
+        p = carry;
     }
 
-    // second run from the true start state, emitting outputs
+    // zero state run per chunk; lane 0 also carries the block start state
+    // (A^kChunk p) into its element, so that the in-wave scan yields the true
+    // state at the end of every chunk
+    BankPair<NA, NB> s;
+    s.zero();
+    {
+        Coeffs<0, NA> ca;
+        Coeffs<NA, NB> cb;
+        ca.load(t, t.c0a);
+        cb.load(t, t.c0b);
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) {
+            double xa, xb;
+            chunk_inputs(m, in[i], ramp_weight<Mode>(edge, j0 + i, len), j0 + i, len, xa, xb);
+            if constexpr (NA > 0) ca.step(s.a, xa);
+            if constexpr (NB > 0) cb.step(s.b, xb);
+        }
+    }
+    if (lane == 0) {
+        BankPair<NA, NB> c = p;
+        c.power(t, 0, s);
+        s = c;
+    }
+    s.scan(t, 0, lane);
+
+    // lane start state = end state of the chunk before it (p for lane 0)
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const double su = shfl_up(s.u(k), 1), sv = shfl_up(s.v(k), 1);
+        s.u(k) = lane == 0 ? p.u(k) : su;
+        s.v(k) = lane == 0 ? p.v(k) : sv;
+    }
+
+    // second run from the true start state (coefficients read again)
+    const IirTable &t2 = *reload(table);
+    Coeffs<0, NA> ca;
+    Coeffs<NA, NB> cb;
+    ca.load(t2, t2.c0a);
+    cb.load(t2, t2.c0b);
+    float out[Mode::kOutputs][kChunk];
     double acc = 0.0;
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) {
         const int64_t j = j0 + i;
-        double xa = 0.0, xb = 0.0;
-        const int64_t n = Mode::kReverse ? len - 1 - j : j;
-        if (j < len) m.inputs(n, in[i], xa, xb);
+        const double w = ramp_weight<Mode>(edge, j, len);
+        double xa, xb;
+        chunk_inputs(m, in[i], w, j, len, xa, xb);
         double ya = 0.0, yb = 0.0;
         if constexpr (NA > 0) ya = ca.step(s.a, xa);
         if constexpr (NB > 0) yb = cb.step(s.b, xb);
-        if (j < len) m.emit(row, n, ya, yb, acc, consts);
+        float o[Mode::kOutputs];
+        const double before = acc;
+        m.compute(w, ya, yb, acc, sh, o);
+        if (j >= len) acc = before;  // past the end of the row
+#pragma unroll
+        for (int q = 0; q < Mode::kOutputs; ++q) out[q][i] = j < len ? o[q] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < Mode::kOutputs; ++q) {
+        float *dst = m.dst(row, q);
+        if (dst != nullptr) store_chunk(dst, out[q], Mode::kReverse, j0, len);
     }
 
     if constexpr (Mode::kAccumulates) {
         acc = wave_sum(acc);
-        if (lane == 0) accum[wave] = acc;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            double total = accum[0];
-            for (int i = 1; i < kWaves; ++i) total += accum[i];
-            m.finish(row, blk, total);
+        if (lane == 0) m.finish(row, blk, acc);
+    }
+}
+
+// Host side: aggregate (+ prefix for long rows) and output launches of one
+// scan pass over `rows` rows; `aggr` holds rows * (NA + NB) * nblk * 2 doubles.
+template <int NA, int NB, class Mode>
+int launch_scan(const Mode &m, const IirTable *table, double *aggr, int64_t rows, int64_t len,
+                bool aggregate, bool output, hipStream_t stream) {
+    constexpr int NS = NA + NB;
+    const int64_t nblk = cdiv(len, kBlockSpan);
+    const unsigned grid = static_cast<unsigned>(rows * nblk);
+    const bool prefixed = nblk > kLookbackBlocks;
+    if (grid == 0) return PESQ_OK;
+    if (aggregate) {
+        hipLaunchKernelGGL((iir_aggregate_kernel<NA, NB, Mode>), dim3(grid), dim3(kWave), 0,
+                           stream, m, table, aggr, len, static_cast<int>(nblk));
+        PESQ_CHECK_LAUNCH("iir aggregate");
+        if (prefixed) {
+            const int64_t nseq = rows * NS;
+            hipLaunchKernelGGL(iir_prefix_kernel<NS>,
+                               dim3(static_cast<unsigned>(cdiv(nseq, kPrefixWaves))),
+                               dim3(kWave * kPrefixWaves), 0, stream, table, aggr,
+                               static_cast<int>(nblk), nseq);
+            PESQ_CHECK_LAUNCH("iir prefix");
         }
     }
+    if (output) {
+        hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode>), dim3(grid), dim3(kWave), 0, stream,
+                           m, table, static_cast<const double *>(aggr), len,
+                           static_cast<int>(nblk), prefixed ? 1 : 0);
+        PESQ_CHECK_LAUNCH("iir output");
+    }
+    return PESQ_OK;
 }
 
 }  // namespace pesq

@@ -7,6 +7,8 @@ namespace pesq {
 template <bool kRev>
 struct SingleMode {
     static constexpr int kInputs = 1;
+    static constexpr int kOutputs = 1;
+    static constexpr bool kRamp = false;
     static constexpr bool kReverse = kRev;
     static constexpr bool kAccumulates = false;
 
@@ -14,20 +16,16 @@ struct SingleMode {
     float *y;
     int64_t len;
 
-    __device__ __forceinline__ void load(int row, int64_t n, float *in) const {
-        in[0] = x[int64_t(row) * len + n];
-    }
-    __device__ __forceinline__ void inputs(int64_t, const float *in, double &xa, double &) const {
+    __device__ __forceinline__ const float *src(int row, int) const { return x + int64_t(row) * len; }
+    __device__ __forceinline__ float *dst(int row, int) const { return y + int64_t(row) * len; }
+    __device__ __forceinline__ void inputs(double, const float *in, double &xa, double &xb) const {
         xa = in[0];
+        xb = 0.0;
     }
-    __device__ __forceinline__ float observe(float o, const float *) const { return o; }
-    __device__ __forceinline__ float reduce_observed(float o) const { return o; }
-    __device__ __forceinline__ float combine_observed(float a, float) const { return a; }
-    __device__ __forceinline__ void observed(int, int, float) const {}
-    __device__ __forceinline__ void setup(int, int, double *, int) const {}
-    __device__ __forceinline__ void emit(int row, int64_t n, double ya, double, double &,
-                                         const double *) const {
-        y[int64_t(row) * len + n] = static_cast<float>(ya);
+    __device__ __forceinline__ void setup(int, double *, int) const {}
+    __device__ __forceinline__ void compute(double, double ya, double, double &, const double *,
+                                            float *out) const {
+        out[0] = static_cast<float>(ya);
     }
     __device__ __forceinline__ void finish(int, int, double) const {}
 };
@@ -36,17 +34,7 @@ template <int NS, bool kRev>
 static int launch_single(const float *x, float *y, int64_t rows, int64_t len,
                          const IirTable *table, double *aggr, hipStream_t stream) {
     SingleMode<kRev> m{x, y, len};
-    const int64_t nblk = cdiv(len, kBlockSpan);
-    const unsigned grid = static_cast<unsigned>(rows * nblk);
-    hipLaunchKernelGGL((iir_aggregate_kernel<NS, 0, SingleMode<kRev>>), dim3(grid),
-                       dim3(kWave * kWaves), 0, stream, m, table, aggr, len,
-                       static_cast<int>(nblk));
-    PESQ_CHECK_LAUNCH("iir aggregate");
-    hipLaunchKernelGGL((iir_output_kernel<NS, 0, SingleMode<kRev>>), dim3(grid),
-                       dim3(kWave * kWaves), 0, stream, m, table,
-                       static_cast<const double *>(aggr), len, static_cast<int>(nblk));
-    PESQ_CHECK_LAUNCH("iir output");
-    return PESQ_OK;
+    return launch_scan<NS, 0>(m, table, aggr, rows, len, true, true, stream);
 }
 
 template <bool kRev>

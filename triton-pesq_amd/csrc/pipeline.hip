@@ -2,10 +2,9 @@
 //
 // Forward (5 kernels):
 //   1. iir_aggregate  <power, pre>   per block end states of both filters on the
-//                                    raw inputs, per block peak |s|
-//   2. iir_output     <power, pre>   p = pre(ramp(x)), f = power(x) (kept when a
-//                                    gradient is needed), per block sum f^2;
-//                                    x = s / peak, peak = max(|ref|, |deg|) per item
+//                                    raw inputs
+//   2. iir_output     <power, pre>   p = pre(ramp(s)), f = power(s) (kept when a
+//                                    gradient is needed), per block sum f^2
 //   3. stft_fwd       per (item, 16 frames): frames of scale * p, FFT, |X|^2,
 //                                    Bark sums, silent frames, band partials
 //   4. chain_fwd      per (item, 16 frames): band and frame equalisation,
@@ -17,14 +16,18 @@
 //                                    spectra recomputed, adjoint FFT, overlap-add
 //   8. iir_aggregate  <power^T, pre^T> on (f, dL/dp), time reversed
 //   9. iir_output     <power^T, pre^T> and the level alignment adjoint:
-//        dL/ds = (scale ramp(pre^T g_p) - scale S / E power^T f) / peak
+//        dL/ds = scale ramp(pre^T g_p) - scale S / E power^T f,  S = sum g_p p
+// Rows longer than kLookbackBlocks scan blocks add an iir_prefix launch
+// between 1 and 2 and between 8 and 9.
 //
 // The level alignment (torch_pesq/loss.py:127-139) is folded in: with
 // E = sum f^2 the aligned, pre-emphasised signal is p_aligned = scale * p,
 // scale = sqrt(1e7 (len + 5120) 1.04684 / E), because the ramp and the
-// pre-emphasis filter are linear.  The peak normalisation
-// (torch_pesq/loss.py:179-183) is applied at the output of the scans, which
-// run on the raw inputs.
+// pre-emphasis filter are linear.  The peak normalisation that precedes it
+// (torch_pesq/loss.py:179-183) multiplies s by 1 / peak, which scales p by
+// 1 / peak and scale by peak: p_aligned does not depend on it, so the scans
+// run on the raw signal s and the peak is never formed.  (Its gradient path
+// is zero for the same reason: the loss is invariant under s -> c s.)
 #include <cmath>
 
 #include "pipeline_layout.hpp"
@@ -41,52 +44,38 @@ constexpr int kPreSections = 1;    // pre-emphasis biquad
 
 struct PipeFwdMode {
     static constexpr int kInputs = 1;
+    static constexpr int kOutputs = 2;  // p, f
+    static constexpr bool kRamp = true;
     static constexpr bool kReverse = false;
     static constexpr bool kAccumulates = true;
 
     const float *ref, *deg;
     float *p, *f;             // outputs; f may be null
-    float *peak;              // [rows, nblk] aggregate-pass output
-    const float *peak_in;     // same buffer, read by the output pass
     double *energy;           // [rows, nblk]
     int64_t len;
     int batch, nblk, row0, nrg;
 
-    __device__ __forceinline__ void load(int row, int64_t n, float *in) const {
-        in[0] = row < batch ? ref[int64_t(row) * len + n] : deg[int64_t(row - batch) * len + n];
+    __device__ __forceinline__ const float *src(int row, int) const {
+        return row < batch ? ref + int64_t(row) * len : deg + int64_t(row - batch) * len;
     }
-    __device__ __forceinline__ void inputs(int64_t n, const float *in, double &xa,
+    __device__ __forceinline__ float *dst(int row, int q) const {
+        if (q == 0) return p + int64_t(row) * len;
+        return f != nullptr && row >= row0 && row < row0 + nrg ? f + int64_t(row - row0) * len
+                                                               : nullptr;
+    }
+    // filter A (level alignment band pass) sees the signal, filter B
+    // (pre-emphasis) the edge ramped signal
+    __device__ __forceinline__ void inputs(double w, const float *in, double &xa,
                                            double &xb) const {
         xa = in[0];
-        xb = in[0] * edge_weight(n, len);
+        xb = static_cast<double>(in[0]) * w;
     }
-    __device__ __forceinline__ float observe(float o, const float *in) const {
-        return fmaxf(o, fabsf(in[0]));
-    }
-    __device__ __forceinline__ float reduce_observed(float o) const { return wave_max(o); }
-    __device__ __forceinline__ float combine_observed(float a, float b) const { return fmaxf(a, b); }
-    __device__ __forceinline__ void observed(int row, int blk, float o) const {
-        peak[int64_t(row) * nblk + blk] = o;
-    }
-    __device__ __forceinline__ void setup(int row, int, double *sh, int lane) const {
-        const int item = row % batch;
-        float m = 0.0f;
-        for (int i = lane; i < nblk; i += kWave) {
-            m = fmaxf(m, peak_in[int64_t(item) * nblk + i]);
-            m = fmaxf(m, peak_in[int64_t(item + batch) * nblk + i]);
-        }
-        m = wave_max(m);
-        if (lane == 0) sh[0] = 1.0 / static_cast<double>(m);
-    }
-    __device__ __forceinline__ void emit(int row, int64_t n, double ya, double yb, double &acc,
-                                         const double *sh) const {
-        const double inv = sh[0];
-        const double fx = ya * inv;
-        p[int64_t(row) * len + n] = static_cast<float>(yb * inv);
-        if (f != nullptr && row >= row0 && row < row0 + nrg) {
-            f[int64_t(row - row0) * len + n] = static_cast<float>(fx);
-        }
-        acc = fma(fx, fx, acc);
+    __device__ __forceinline__ void setup(int, double *, int) const {}
+    __device__ __forceinline__ void compute(double, double ya, double yb, double &acc,
+                                            const double *, float *out) const {
+        out[0] = static_cast<float>(yb);
+        out[1] = static_cast<float>(ya);
+        acc = fma(ya, ya, acc);
     }
     __device__ __forceinline__ void finish(int row, int blk, double total) const {
         energy[int64_t(row) * nblk + blk] = total;
@@ -95,46 +84,44 @@ struct PipeFwdMode {
 
 struct PipeBwdMode {
     static constexpr int kInputs = 2;
+    static constexpr int kOutputs = 1;
+    static constexpr bool kRamp = true;
     static constexpr bool kReverse = true;
     static constexpr bool kAccumulates = false;
 
     const float *f, *gp;      // [nrg, len] each
-    const double *rowconst;   // [rows, 4]: 1/peak, E, scale
+    const double *rowconst;   // [rows, 4]: -, E, scale, -
     const double *spart;      // [nrg, nhoptile]
     float *g_ref, *g_deg;
     int64_t len;
     int batch, row0, nhoptile;
 
-    __device__ __forceinline__ void load(int row, int64_t n, float *in) const {
-        in[0] = f[int64_t(row) * len + n];
-        in[1] = gp[int64_t(row) * len + n];
+    // filter A (power^T) runs on f, filter B (pre^T) on dL/dp
+    __device__ __forceinline__ const float *src(int row, int q) const {
+        return (q == 0 ? f : gp) + int64_t(row) * len;
     }
-    __device__ __forceinline__ void inputs(int64_t, const float *in, double &xa, double &xb) const {
+    __device__ __forceinline__ float *dst(int row, int) const {
+        const int stacked = row0 + row;
+        return stacked < batch ? g_ref + int64_t(stacked) * len
+                               : g_deg + int64_t(stacked - batch) * len;
+    }
+    __device__ __forceinline__ void inputs(double, const float *in, double &xa, double &xb) const {
         xa = in[0];
         xb = in[1];
     }
-    __device__ __forceinline__ float observe(float o, const float *) const { return o; }
-    __device__ __forceinline__ float reduce_observed(float o) const { return o; }
-    __device__ __forceinline__ float combine_observed(float a, float) const { return a; }
-    __device__ __forceinline__ void observed(int, int, float) const {}
-    __device__ __forceinline__ void setup(int row, int, double *sh, int lane) const {
-        double s = 0.0;
-        for (int i = lane; i < nhoptile; i += kWave) s += spart[int64_t(row) * nhoptile + i];
+    // scale and scale S / E, S = sum of the per hop tile partials of dL/dp . p
+    __device__ __forceinline__ void setup(int row, double *sh, int lane) const {
+        const int nmine = lane < nhoptile ? (nhoptile - 1 - lane) / kWave + 1 : 0;
+        double s = nmine > 0 ? strided_sum(spart + int64_t(row) * nhoptile + lane, nmine, kWave)
+                             : 0.0;
         s = wave_sum(s);
-        if (lane == 0) {
-            const double *rc = rowconst + int64_t(row0 + row) * 4;
-            sh[0] = rc[0];                 // 1 / peak
-            sh[1] = rc[2];                 // scale
-            sh[2] = rc[2] * s / rc[1];     // scale S / E
-        }
+        const double *rc = rowconst + int64_t(row0 + row) * 4;
+        sh[1] = rc[2];
+        sh[2] = rc[2] * s / rc[1];
     }
-    __device__ __forceinline__ void emit(int row, int64_t n, double ya, double yb, double &,
-                                         const double *sh) const {
-        const double g = sh[0] * (sh[1] * edge_weight(n, len) * yb - sh[2] * ya);
-        const int stacked = row0 + row;
-        float *dst = stacked < batch ? g_ref + int64_t(stacked) * len
-                                     : g_deg + int64_t(stacked - batch) * len;
-        dst[n] = static_cast<float>(g);
+    __device__ __forceinline__ void compute(double w, double ya, double yb, double &,
+                                            const double *sh, float *out) const {
+        out[0] = static_cast<float>(sh[1] * w * yb - sh[2] * ya);
     }
     __device__ __forceinline__ void finish(int, int, double) const {}
 };
@@ -209,23 +196,16 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
     const int side = wave / 4;                   // 0 = reference, 1 = degraded
     const int row = side * L.batch + item;
 
-    // row constants: 1 / peak, E, scale
-    const float *peak = region<float>(a.ws, L.peak);
-    const double *energy = region<double>(a.ws, L.energy);
-    float m = 0.0f;
-    double e = 0.0;
-    for (int i = lane; i < L.nblk; i += kWave) {
-        m = fmaxf(m, fmaxf(peak[int64_t(item) * L.nblk + i],
-                           peak[int64_t(item + L.batch) * L.nblk + i]));
-        e += energy[int64_t(row) * L.nblk + i];
-    }
-    m = wave_max(m);
+    // row constants: -, E, scale, -
+    const double *energy = region<double>(a.ws, L.energy) + int64_t(row) * L.nblk;
+    const int nmine = lane < L.nblk ? static_cast<int>((L.nblk - 1 - lane) / kWave + 1) : 0;
+    double e = nmine > 0 ? strided_sum(energy + lane, nmine, kWave) : 0.0;
     e = wave_sum(e);
     const double power = e / static_cast<double>(L.len + 5120) / 1.04684;
     const double scale = sqrt(1e7 / power);
     if (tile == 0 && (wave & 3) == 0 && lane == 0) {
         double *rc = region<double>(a.ws, L.rowconst) + int64_t(row) * 4;
-        rc[0] = 1.0 / static_cast<double>(m);
+        rc[0] = 1.0;
         rc[1] = e;
         rc[2] = scale;
         rc[3] = 0.0;
@@ -236,6 +216,18 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
     float *bark = region<float>(a.ws, L.bark) + int64_t(row) * L.frames * kBands;
     cplx<real> *buf = fftbuf[wave];
     real *power_buf = reinterpret_cast<real *>(buf);
+    Twiddles tw;
+    tw.load(t.tw256, t.tw512, lane);
+    float win[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        win[2 * r] = t.window[2 * (lane + 64 * r)];
+        win[2 * r + 1] = t.window[2 * (lane + 64 * r) + 1];
+    }
+    const int band_lo = lane < kBands ? t.band_start[lane] : 0;
+    const int band_hi = lane < kBands ? t.band_end[lane] : 0;
+    const double corr = lane < kBands ? t.corr[lane] : 0.0;
+    const double th100 = lane < kBands ? 100.0 * t.threshs[lane] : 0.0;
 
     for (int q = 0; q < 4; ++q) {
         const int local = (wave & 3) * 4 + q;
@@ -244,10 +236,12 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
         const int64_t start = frame * kHop;
         auto u = [&](int k) -> real {
             const int64_t n = start + k;
-            return n < L.len ? static_cast<real>(p[n]) * static_cast<real>(t.window[k]) : real(0);
+            // k = 2 (lane + 64 r) + {0, 1}: the window value is in win[2 r + {0, 1}]
+            const float w = win[2 * (k >> 7) + (k & 1)];
+            return static_cast<real>(load_or_zero(p, n, L.len)) * static_cast<real>(w);
         };
         cplx<real> x[4];
-        frame_spectrum<real>(u, x, buf, t.tw256, t.tw512, lane);
+        frame_spectrum<real>(u, x, buf, tw, lane);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int fbin = lane + 64 * r;
@@ -257,10 +251,10 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
         double val = 0.0;
         if (lane < kBands) {
             double acc = 0.0;
-            for (int fbin = t.band_start[lane]; fbin < t.band_end[lane]; ++fbin) {
+            for (int fbin = band_lo; fbin < band_hi; ++fbin) {
                 acc += static_cast<double>(power_buf[fbin]);
             }
-            const float v = static_cast<float>(acc * t.corr[lane]);
+            const float v = static_cast<float>(acc * corr);
             bark[frame * kBands + lane] = v;
             barks[side][local][lane] = v;
             val = v;
@@ -268,7 +262,7 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
         wave_lds_fence();
         if (side == 0) {
             // silent frame: audible (> 100 th) energy of the reference below 1e7
-            const double aud = lane < kBands && val > 100.0 * t.threshs[lane] ? val : 0.0;
+            const double aud = lane < kBands && val > th100 ? val : 0.0;
             const double total = wave_sum(aud);
             if (lane == 0) {
                 const float k = total >= 1e7 ? 1.0f : 0.0f;
@@ -315,6 +309,7 @@ __device__ __forceinline__ BandConsts band_consts(const ModelTable &t, int lane)
 constexpr int kChainWaves = 4;
 
 __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs a) {
+    constexpr int kPer = kTile / kChainWaves;  // frames per wavefront
     __shared__ double rs[kBands];
 
     const ModelTable &t = *a.tab;
@@ -325,15 +320,29 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs 
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
     const double frames_f = static_cast<double>(L.frames);
+    const int64_t f0 = t0 + wave * kPer;  // first frame of this wavefront
+
+    // Bark values of frames f0 - 1 .. f0 + kPer - 1, loaded up front (indices
+    // clamped into the array; out of range frames and bands are masked later)
+    float R[kPer + 1], G[kPer + 1];
+    {
+        const int band = lane < kBands ? lane : kBands - 1;
+        const float *bref = a.bark_ref + int64_t(item) * L.frames * kBands;
+        const float *bdeg = a.bark_deg + int64_t(item) * L.frames * kBands;
+#pragma unroll
+        for (int q = 0; q <= kPer; ++q) {
+            int64_t frame = f0 - 1 + q;
+            frame = frame < 0 ? 0 : (frame >= L.frames ? L.frames - 1 : frame);
+            R[q] = bref[frame * kBands + band];
+            G[q] = bdeg[frame * kBands + band];
+        }
+    }
 
     if (wave == 0 && lane < kBands) {
         const double *pr = region<double>(a.ws, L.bandref) + int64_t(item) * L.ntile * kBands;
         const double *pd = region<double>(a.ws, L.banddeg) + int64_t(item) * L.ntile * kBands;
-        double sr = 0.0, sd = 0.0;
-        for (int i = 0; i < L.ntile; ++i) {
-            sr += pr[i * kBands + lane];
-            sd += pd[i * kBands + lane];
-        }
+        const double sr = strided_sum(pr + lane, static_cast<int>(L.ntile), kBands);
+        const double sd = strided_sum(pd + lane, static_cast<int>(L.ntile), kBands);
         const double mref = sr / frames_f;
         const double mdeg = sd / frames_f;
         const double ratio = (mdeg + 1000.0) / (mref + 1000.0);
@@ -350,44 +359,35 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs 
     const BandConsts c = band_consts(t, lane);
     const bool live = lane < kBands;
     const double r = live ? rs[lane] : 0.0;
-    const float *bref = a.bark_ref + int64_t(item) * L.frames * kBands;
-    const float *bdeg = a.bark_deg + int64_t(item) * L.frames * kBands;
     const double sqrt_w = sqrt(t.total_width);
     const double W = t.total_width;
 
-    auto totals = [&](int64_t frame, double &taer, double &tad) {
-        double vr = 0.0, vd = 0.0;
-        if (live) {
-            const double er = r * static_cast<double>(bref[frame * kBands + lane]);
-            const double g = bdeg[frame * kBands + lane];
-            vr = er > c.th ? er : 0.0;
-            vd = g > c.th ? g : 0.0;
-        }
-        taer = wave_sum(vr);
-        tad = wave_sum(vd);
-    };
+    // per frame totals of the audible energies; slot q is frame f0 - 1 + q
+    double taer[kPer + 1], tad[kPer + 1];
+#pragma unroll
+    for (int q = 0; q <= kPer; ++q) {
+        const int64_t frame = f0 - 1 + q;
+        const bool ok = live && frame >= 0 && frame < L.frames;
+        const double er = r * static_cast<double>(R[q]);
+        const double g = G[q];
+        taer[q] = wave_sum(ok && er > c.th ? er : 0.0);
+        tad[q] = wave_sum(ok && g > c.th ? g : 0.0);
+    }
 
-    for (int q = 0; q < kTile / kChainWaves; ++q) {
-        const int64_t frame = t0 + wave * (kTile / kChainWaves) + q;
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const int64_t frame = f0 + q;
         if (frame >= L.frames) break;
-        double taer, tad;
-        totals(frame, taer, tad);
-        const double fpr0 = (taer + 5e3) / (tad + 5e3);
-        const double h = pow((taer + 1e5) / 1e7, 0.04);
-        double fpr1 = fpr0;
-        if (frame > 0) {
-            double taer_p, tad_p;
-            totals(frame - 1, taer_p, tad_p);
-            fpr1 = fpr0 * 0.8 + ((taer_p + 5e3) / (tad_p + 5e3)) * 0.2;
-        }
+        const double fpr0 = (taer[q + 1] + 5e3) / (tad[q + 1] + 5e3);
+        const double h = pow((taer[q + 1] + 1e5) / 1e7, 0.04);
+        const double fpr1 =
+            frame > 0 ? fpr0 * 0.8 + ((taer[q] + 5e3) / (tad[q] + 5e3)) * 0.2 : fpr0;
         const double fpr = fmin(fmax(fpr1, 3e-4), 5.0);
 
         double v2 = 0.0, ya = 0.0;
         if (live) {
-            const double R = bref[frame * kBands + lane];
-            const double G = bdeg[frame * kBands + lane];
-            const double er = r * R;
-            const double ed = fpr * G;
+            const double er = r * static_cast<double>(R[q + 1]);
+            const double ed = fpr * static_cast<double>(G[q + 1]);
             const double lr = loudness(er, c.th, c.e, c.ls);
             const double ld = loudness(ed, c.th, c.e, c.ls);
             const double u = ld - lr;
@@ -405,8 +405,8 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs 
         const double asymm_raw = W * wave_sum(ya);
         if (lane == 0) {
             const int64_t o = int64_t(item) * L.frames + frame;
-            frame_array(a, kTaer)[o] = taer;
-            frame_array(a, kTad)[o] = tad;
+            frame_array(a, kTaer)[o] = taer[q + 1];
+            frame_array(a, kTad)[o] = tad[q + 1];
             frame_array(a, kFpr0)[o] = fpr0;
             frame_array(a, kFpr1)[o] = fpr1;
             frame_array(a, kH)[o] = h;
@@ -473,27 +473,35 @@ __global__ void __launch_bounds__(kFinalThreads) chain_final_kernel(PipeArgs a) 
 // 6. chain backward per (item, 16 frames)
 // ---------------------------------------------------------------------------
 
-// d d / d s_t of d = sqrt(mean_l psqm_l^2), psqm_l = (mean_{j<20} s_{10 l + j}^6)^(1/6)
-__device__ __forceinline__ double psqm_adjoint(const PipeLayout &L, const double *psqm,
-                                               double d, double s, int64_t frame) {
+// PSQM windows that touch the frames t0 .. t0 + kTile of one chain tile:
+// l in [t0 / kStride - 1, (t0 + kTile) / kStride], at most kPsqmSlots of them.
+constexpr int kPsqmSlots = (kTile + kStride - 1) / kStride + 2;
+
+// d d / d s_t of d = sqrt(mean_l psqm_l^2), psqm_l = (mean_{j<20} s_{10 l + j}^6)^(1/6);
+// pl[i] holds psqm_{lbase + i}
+__device__ __forceinline__ double psqm_adjoint(const PipeLayout &L, const double *pl,
+                                               int64_t lbase, double d, double s, int64_t frame) {
     if (!(d > 0.0)) return 0.0;
     double acc = 0.0;
     const int64_t hi = frame / kStride;
     for (int64_t l = hi - 1; l <= hi; ++l) {
         if (l < 0 || l >= L.nwin || frame >= l * kStride + kWin) continue;
-        const double pl = psqm[l];
-        if (!(pl > 0.0)) continue;
-        const double ratio = s / pl;
+        const double p = pl[l - lbase];
+        if (!(p > 0.0)) continue;
+        const double ratio = s / p;
         const double r2 = ratio * ratio;
-        acc += pl / (static_cast<double>(L.nwin) * d) * (r2 * r2 * ratio) / kWin;
+        acc += p / (static_cast<double>(L.nwin) * d) * (r2 * r2 * ratio) / kWin;
     }
     return acc;
 }
 
 __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs a) {
     constexpr int kPer = kTile / kChainWaves;
+    constexpr int kSlots = kTile + 1;  // the tile's frames and the next one
     __shared__ double rs[kBands];
-    __shared__ double gfpr[kTile + 1], gh[kTile + 1];
+    __shared__ double fr[kFrameArrays][kSlots];
+    __shared__ double pl[2][kPsqmSlots];
+    __shared__ double gfpr[kSlots], gh[kSlots];
     __shared__ double part[kChainWaves][kBands];
 
     const ModelTable &t = *a.tab;
@@ -504,7 +512,37 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
     const bool live = lane < kBands;
+    const int64_t fo = int64_t(item) * L.frames;
+    const int64_t lbase = t0 / kStride - 1;
 
+    // Bark values of this wavefront's frames (slot q = local frame wave kPer + q)
+    float R[kPer + 1], G[kPer + 1];
+    {
+        const int band = live ? lane : kBands - 1;
+        const float *bref = a.bark_ref + int64_t(item) * L.frames * kBands;
+        const float *bdeg = a.bark_deg + int64_t(item) * L.frames * kBands;
+#pragma unroll
+        for (int q = 0; q <= kPer; ++q) {
+            const int64_t frame = t0 + wave * kPer + q;
+            const int64_t fc = frame < L.frames ? frame : L.frames - 1;
+            R[q] = bref[fc * kBands + band];
+            G[q] = bdeg[fc * kBands + band];
+        }
+    }
+
+    // the tile's per frame chain state and PSQM windows, one load per thread
+    if (threadIdx.x < kFrameArrays * kSlots) {
+        const int which = threadIdx.x / kSlots;
+        const int q = threadIdx.x - which * kSlots;
+        const int64_t frame = t0 + q < L.frames ? t0 + q : L.frames - 1;
+        fr[which][q] = frame_array(a, which)[fo + frame];
+    } else if (threadIdx.x >= 192 && threadIdx.x < 192 + 2 * kPsqmSlots) {
+        const int side = (threadIdx.x - 192) / kPsqmSlots;
+        const int i = threadIdx.x - 192 - side * kPsqmSlots;
+        int64_t l = lbase + i;
+        l = l < 0 ? 0 : (l >= L.nwin ? L.nwin - 1 : l);
+        pl[side][i] = region<double>(a.ws, L.psqm)[(int64_t(side) * L.batch + item) * L.nwin + l];
+    }
     if (wave == 0 && live) rs[lane] = band_array(a, kR)[item * kBands + lane];
 
     // upstream gradients of the two distances, MOS and loss folded in
@@ -527,42 +565,37 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
 
     const BandConsts c = band_consts(t, lane);
     const double r = live ? rs[lane] : 0.0;
-    const float *bref = a.bark_ref + int64_t(item) * L.frames * kBands;
-    const float *bdeg = a.bark_deg + int64_t(item) * L.frames * kBands;
-    const double *psqm_s = region<double>(a.ws, L.psqm) + int64_t(item) * L.nwin;
-    const double *psqm_a = region<double>(a.ws, L.psqm) + (int64_t(L.batch) + item) * L.nwin;
     const double W = t.total_width;
-    const int64_t fo = int64_t(item) * L.frames;
 
     // phase 1: adjoint of the per frame distances down to equ_ref / equ_deg
     double g_er[kPer + 1], g_ed[kPer + 1];
     const int nmine = wave == kChainWaves - 1 ? kPer + 1 : kPer;
-    for (int q = 0; q < nmine; ++q) {
+#pragma unroll
+    for (int q = 0; q <= kPer; ++q) {
         const int local = wave * kPer + q;
         const int64_t frame = t0 + local;
         g_er[q] = g_ed[q] = 0.0;
-        if (frame >= L.frames) continue;
+        if (q >= nmine || frame >= L.frames) continue;
 
-        const double s_sy = frame_array(a, kSymm)[fo + frame];
-        const double s_as = frame_array(a, kAsymm)[fo + frame];
-        const double g_sy = gds * psqm_adjoint(L, psqm_s, ds, s_sy, frame);
-        const double g_as = gda * psqm_adjoint(L, psqm_a, da, s_as, frame);
-        const double raw_s = frame_array(a, kSymmRaw)[fo + frame];
-        const double raw_a = frame_array(a, kAsymmRaw)[fo + frame];
-        const double h = frame_array(a, kH)[fo + frame];
+        const double s_sy = fr[kSymm][local];
+        const double s_as = fr[kAsymm][local];
+        const double g_sy = gds * psqm_adjoint(L, pl[0], lbase, ds, s_sy, frame);
+        const double g_as = gda * psqm_adjoint(L, pl[1], lbase, da, s_as, frame);
+        const double raw_s = fr[kSymmRaw][local];
+        const double raw_a = fr[kAsymmRaw][local];
+        const double h = fr[kH][local];
         const double pre_s = fmax(raw_s, 1e-20), pre_a = fmax(raw_a, 1e-20);
         const double g_ps = pre_s / h <= 45.0 ? g_sy : 0.0;
         const double g_pa = pre_a / h <= 45.0 ? g_as : 0.0;
         const double g_hh = -(g_ps * pre_s + g_pa * pre_a) / (h * h);
         const double g_rs = raw_s >= 1e-20 ? g_ps / h : 0.0;
         const double g_ra = raw_a >= 1e-20 ? g_pa / h : 0.0;
-        const double fpr = fmin(fmax(frame_array(a, kFpr1)[fo + frame], 3e-4), 5.0);
+        const double fpr = fmin(fmax(fr[kFpr1][local], 3e-4), 5.0);
 
         double my_er = 0.0, my_ed = 0.0, gf = 0.0;
         if (live) {
-            const double R = bref[frame * kBands + lane];
-            const double G = bdeg[frame * kBands + lane];
-            const double er = r * R, ed = fpr * G;
+            const double Rq = R[q], Gq = G[q];
+            const double er = r * Rq, ed = fpr * Gq;
             const double lr = loudness(er, c.th, c.e, c.ls);
             const double ld = loudness(ed, c.th, c.e, c.ls);
             const double u = ld - lr;
@@ -592,7 +625,7 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
                 my_ed += g_asc * 1.2 * asc_raw / (ed + 50.0);
                 my_er -= g_asc * 1.2 * asc_raw / (er + 50.0);
             }
-            gf = my_ed * G;
+            gf = my_ed * Gq;
         }
         gf = wave_sum(gf);
         g_er[q] = my_er;
@@ -606,34 +639,34 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
 
     // phase 2: frame power ratio, h and the total audible energies
     double acc = 0.0;
+#pragma unroll
     for (int q = 0; q < kPer; ++q) {
         const int local = wave * kPer + q;
         const int64_t frame = t0 + local;
         if (frame >= L.frames) break;
-        const double f1 = frame_array(a, kFpr1)[fo + frame];
+        const double f1 = fr[kFpr1][local];
         const double g1 = (f1 >= 3e-4 && f1 <= 5.0) ? gfpr[local] : 0.0;
         double g1n = 0.0;
         if (frame + 1 < L.frames) {
-            const double f1n = frame_array(a, kFpr1)[fo + frame + 1];
+            const double f1n = fr[kFpr1][local + 1];
             g1n = (f1n >= 3e-4 && f1n <= 5.0) ? gfpr[local + 1] : 0.0;
         }
         const double g0 = (frame == 0 ? g1 : 0.8 * g1) + 0.2 * g1n;
-        const double taer = frame_array(a, kTaer)[fo + frame];
-        const double tad = frame_array(a, kTad)[fo + frame];
-        const double fpr0 = frame_array(a, kFpr0)[fo + frame];
-        const double h = frame_array(a, kH)[fo + frame];
+        const double taer = fr[kTaer][local];
+        const double tad = fr[kTad][local];
+        const double fpr0 = fr[kFpr0][local];
+        const double h = fr[kH][local];
         const double g_taer = g0 / (tad + 5e3) + gh[local] * 0.04 * h / (taer + 1e5);
         const double g_tad = -g0 * fpr0 / (tad + 5e3);
         const double fpr = fmin(fmax(f1, 3e-4), 5.0);
         if (live) {
-            const double R = bref[frame * kBands + lane];
-            const double G = bdeg[frame * kBands + lane];
+            const double Rq = R[q], Gq = G[q];
             double ger = g_er[q];
-            if (r * R > c.th) ger += g_taer;
-            const double ged = g_ed[q] * fpr + (G > c.th ? g_tad : 0.0);
+            if (r * Rq > c.th) ger += g_taer;
+            const double ged = g_ed[q] * fpr + (Gq > c.th ? g_tad : 0.0);
             a.gbark_ref[(int64_t(item) * L.frames + frame) * kBands + lane] = static_cast<float>(ger * r);
             a.gbark_deg[(int64_t(item) * L.frames + frame) * kBands + lane] = static_cast<float>(ged);
-            acc += ger * R;
+            acc += ger * Rq;
         }
     }
     if (live) part[wave][lane] = acc;
@@ -671,8 +704,7 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_bwd_kernel(PipeArgs a)
     // adjoint of the band power ratio and its clamp, then of the mean band powers
     if (wave == 0 && lane < kBands) {
         const double *gp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
-        double g = 0.0;
-        for (int k = 0; k < L.ntile; ++k) g += gp[k * kBands + lane];
+        const double g = strided_sum(gp + lane, static_cast<int>(L.ntile), kBands);
         const double ratio = band_array(a, kRatio)[item * kBands + lane];
         const double mref = band_array(a, kMref)[item * kBands + lane];
         const double gr = (ratio >= 0.01 && ratio <= 100.0) ? g : 0.0;
@@ -686,6 +718,16 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_bwd_kernel(PipeArgs a)
     const int64_t frame = j0 - 1 + wave;
     cplx<real> *buf = fftbuf[wave];
     if (frame >= 0 && frame < L.frames) {
+        Twiddles tw;
+        tw.load(t.tw256, t.tw512, lane);
+        float win[8];
+        int bin_band[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            win[2 * r] = t.window[2 * (lane + 64 * r)];
+            win[2 * r + 1] = t.window[2 * (lane + 64 * r) + 1];
+            bin_band[r] = t.bin_band[lane + 64 * r];
+        }
         const int64_t fo = frame * kBands;
         if (lane < kBands) {
             const float *bk = region<float>(a.ws, L.bark) + int64_t(row) * L.frames * kBands;
@@ -701,27 +743,26 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_bwd_kernel(PipeArgs a)
         const int64_t start = frame * kHop;
         auto u = [&](int k) -> real {
             const int64_t n = start + k;
-            return n < L.len ? static_cast<real>(p[n]) * static_cast<real>(t.window[k]) : real(0);
+            const float w = win[2 * (k >> 7) + (k & 1)];
+            return static_cast<real>(load_or_zero(p, n, L.len)) * static_cast<real>(w);
         };
         cplx<real> x[4];
-        frame_spectrum<real>(u, x, buf, t.tw256, t.tw512, lane);
+        frame_spectrum<real>(u, x, buf, tw, lane);
         cplx<real> v[4];
         const real s = static_cast<real>(scale);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int fbin = lane + 64 * r;
-            const int band = t.bin_band[fbin];
+            const int band = bin_band[r];
             const real gpw = band >= 0 ? static_cast<real>(gband[wave][band]) * s : real(0);
             v[r] = {gpw * x[r].re, gpw * x[r].im};
         }
         real ev[4], od[4];
-        frame_adjoint<real>(v, ev, od, buf, t.tw256, t.tw512, lane);
+        frame_adjoint<real>(v, ev, od, buf, tw, lane);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int n = lane + 64 * r;
-            contrib[wave][2 * n] = static_cast<float>(ev[r] * static_cast<real>(t.window[2 * n]));
-            contrib[wave][2 * n + 1] =
-                static_cast<float>(od[r] * static_cast<real>(t.window[2 * n + 1]));
+            contrib[wave][2 * n] = static_cast<float>(ev[r] * static_cast<real>(win[2 * r]));
+            contrib[wave][2 * n + 1] = static_cast<float>(od[r] * static_cast<real>(win[2 * r + 1]));
         }
     } else {
         for (int k = lane; k < kNfft; k += kWave) contrib[wave][k] = 0.0f;
@@ -792,8 +833,7 @@ __global__ void __launch_bounds__(kWave) chain_meanpow_kernel(PipeArgs a) {
     const int lane = threadIdx.x;
     if (lane >= kBands) return;
     const double *gp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
-    double g = 0.0;
-    for (int k = 0; k < L.ntile; ++k) g += gp[k * kBands + lane];
+    const double g = strided_sum(gp + lane, static_cast<int>(L.ntile), kBands);
     const double ratio = band_array(a, kRatio)[item * kBands + lane];
     const double mref = band_array(a, kMref)[item * kBands + lane];
     const double gr = (ratio >= 0.01 && ratio <= 100.0) ? g : 0.0;
@@ -847,11 +887,13 @@ __global__ void __launch_bounds__(kWave *kPlainWaves) stft_plain_fwd_kernel(Stft
     const int64_t start = frame * kHop;
     auto u = [&](int k) -> real {
         const int64_t n = start + k;
-        return n < a.len ? static_cast<real>(x[n]) * static_cast<real>(t.window[k]) : real(0);
+        return static_cast<real>(load_or_zero(x, n, a.len)) * static_cast<real>(t.window[k]);
     };
     cplx<real> *buf = fftbuf[wave];
     cplx<real> spec[4];
-    frame_spectrum<real>(u, spec, buf, t.tw256, t.tw512, lane);
+    Twiddles tw;
+    tw.load(t.tw256, t.tw512, lane);
+    frame_spectrum<real>(u, spec, buf, tw, lane);
     real *power = reinterpret_cast<real *>(buf);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -888,10 +930,12 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_plain_bwd_kernel(StftA
         const int64_t start = frame * kHop;
         auto u = [&](int k) -> real {
             const int64_t n = start + k;
-            return n < a.len ? static_cast<real>(x[n]) * static_cast<real>(t.window[k]) : real(0);
+            return static_cast<real>(load_or_zero(x, n, a.len)) * static_cast<real>(t.window[k]);
         };
         cplx<real> spec[4], v[4];
-        frame_spectrum<real>(u, spec, fftbuf[wave], t.tw256, t.tw512, lane);
+        Twiddles tw;
+        tw.load(t.tw256, t.tw512, lane);
+        frame_spectrum<real>(u, spec, fftbuf[wave], tw, lane);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int band = t.bin_band[lane + 64 * r];
@@ -899,7 +943,7 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_plain_bwd_kernel(StftA
             v[r] = {g * spec[r].re, g * spec[r].im};
         }
         real ev[4], od[4];
-        frame_adjoint<real>(v, ev, od, fftbuf[wave], t.tw256, t.tw512, lane);
+        frame_adjoint<real>(v, ev, od, fftbuf[wave], tw, lane);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int n = lane + 64 * r;
@@ -1004,8 +1048,6 @@ extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, 
     m.deg = deg;
     m.p = region<float>(a.ws, L.p);
     m.f = grad_mask ? region<float>(a.ws, L.f) : nullptr;
-    m.peak = region<float>(a.ws, L.peak);
-    m.peak_in = m.peak;
     m.energy = region<double>(a.ws, L.energy);
     m.len = len;
     m.batch = static_cast<int>(batch);
@@ -1013,19 +1055,12 @@ extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, 
     m.row0 = static_cast<int>(L.row0);
     m.nrg = static_cast<int>(L.nrg);
     double *aggr = region<double>(a.ws, L.aggr);
-    const unsigned grid_iir = static_cast<unsigned>(L.rows * L.nblk);
 
-    if (stages & 1u) {
-        hipLaunchKernelGGL((iir_aggregate_kernel<kPowerSections, kPreSections, PipeFwdMode>),
-                           dim3(grid_iir), dim3(kWave * kWaves), 0, stream, m, iir, aggr, len,
-                           static_cast<int>(L.nblk));
-        PESQ_CHECK_LAUNCH("pipeline iir aggregate");
-    }
-    if (stages & 2u) {
-        hipLaunchKernelGGL((iir_output_kernel<kPowerSections, kPreSections, PipeFwdMode>),
-                           dim3(grid_iir), dim3(kWave * kWaves), 0, stream, m, iir,
-                           static_cast<const double *>(aggr), len, static_cast<int>(L.nblk));
-        PESQ_CHECK_LAUNCH("pipeline iir output");
+    if (stages & 3u) {
+        if (int st = launch_scan<kPowerSections, kPreSections>(m, iir, aggr, L.rows, len,
+                                                               stages & 1u, stages & 2u, stream)) {
+            return st;
+        }
     }
     if (stages & 4u) {
         hipLaunchKernelGGL(stft_fwd_kernel<StftReal>, dim3(static_cast<unsigned>(batch * L.ntile)),
@@ -1106,18 +1141,9 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
     m.row0 = static_cast<int>(L.row0);
     m.nhoptile = static_cast<int>(L.nhoptile);
     double *aggr = region<double>(a.bw, L.aggr_b);
-    const unsigned grid_iir = static_cast<unsigned>(L.nrg * L.nblk);
-    if (stages & 4u) {
-        hipLaunchKernelGGL((iir_aggregate_kernel<kPowerSections, kPreSections, PipeBwdMode>),
-                           dim3(grid_iir), dim3(kWave * kWaves), 0, stream, m, iir, aggr, len,
-                           static_cast<int>(L.nblk));
-        PESQ_CHECK_LAUNCH("pipeline iir aggregate (adjoint)");
-    }
-    if (stages & 8u) {
-        hipLaunchKernelGGL((iir_output_kernel<kPowerSections, kPreSections, PipeBwdMode>),
-                           dim3(grid_iir), dim3(kWave * kWaves), 0, stream, m, iir,
-                           static_cast<const double *>(aggr), len, static_cast<int>(L.nblk));
-        PESQ_CHECK_LAUNCH("pipeline iir output (adjoint)");
+    if (stages & 12u) {
+        return launch_scan<kPowerSections, kPreSections>(m, iir, aggr, L.nrg, len, stages & 4u,
+                                                         stages & 8u, stream);
     }
     return PESQ_OK;
 }

@@ -27,7 +27,7 @@ struct PipeLayout {
     int grad_mask = 0;
 
     // forward workspace
-    size_t aggr = 0, peak = 0, energy = 0, p = 0, f = 0, rowconst = 0, bark = 0, keep = 0;
+    size_t aggr = 0, energy = 0, p = 0, f = 0, rowconst = 0, bark = 0, keep = 0;
     size_t bandref = 0, banddeg = 0, frame = 0, band = 0, psqm = 0, dist = 0, fwd_bytes = 0;
     // backward workspace
     size_t gbark = 0, grpart = 0, gp = 0, spart = 0, aggr_b = 0, bwd_bytes = 0;
@@ -59,7 +59,6 @@ struct PipeLayout {
             off = align(off + bytes);
         };
         take(aggr, size_t(rows) * nblk * nstate * sizeof(double));
-        take(peak, size_t(rows) * nblk * sizeof(float));
         take(energy, size_t(rows) * nblk * sizeof(double));
         take(p, size_t(rows) * len * sizeof(float));
         take(f, size_t(nrg) * len * sizeof(float));
@@ -116,7 +115,7 @@ struct PipeLayout {
             size_t off, end;
         };
         const Entry table[] = {
-            {"aggr", aggr, peak},       {"peak", peak, energy},     {"energy", energy, p},
+            {"aggr", aggr, energy},     {"energy", energy, p},
             {"p", p, f},                {"f", f, rowconst},         {"rowconst", rowconst, bark},
             {"bark", bark, keep},       {"keep", keep, bandref},    {"bandref", bandref, banddeg},
             {"banddeg", banddeg, frame}, {"frame", frame, band},    {"band", band, psqm},

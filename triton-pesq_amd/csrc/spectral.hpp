@@ -55,10 +55,31 @@ __device__ __forceinline__ void wave_lds_fence() {
     __builtin_amdgcn_wave_barrier();
 }
 
+// Per lane twiddles of every FFT pass and of the real-FFT fold, loaded once
+// per kernel so that no pass waits on a memory load:
+//   pass[p][r - 1] = e^{-2 pi i k r / (4 ns)}, ns = 4^p (p = 1..3), k = lane mod ns
+//   fold[r]        = e^{-2 pi i f / 512},      f = lane + 64 r
+// (pass 0 has ns = 1 and only unit twiddles).
+struct Twiddles {
+    double2 pass[3][3];
+    double2 fold[4];
+
+    __device__ __forceinline__ void load(const double2 *tw256, const double2 *tw512, int lane) {
+#pragma unroll
+        for (int p = 1; p < 4; ++p) {
+            const int ns = 1 << (2 * p);
+            const int k = lane & (ns - 1);
+#pragma unroll
+            for (int r = 1; r < 4; ++r) pass[p - 1][r - 1] = tw256[(k * r * (64 / ns)) & 255];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) fold[r] = tw512[lane + 64 * r];
+    }
+};
+
 // In: v[r] = z_{lane + 64 r}.  Out: buf[n] = Z_n (natural order), unnormalised.
-// tw[m] = e^{-2 pi i m / 256}.
 template <typename real, bool kInverse>
-__device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, const double2 *tw,
+__device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, const Twiddles &tw,
                                        int lane) {
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
@@ -67,16 +88,16 @@ __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, cons
 #pragma unroll
             for (int r = 0; r < 4; ++r) v[r] = buf[lane + 64 * r];
             wave_lds_fence();
-        }
-        const int k = lane & (ns - 1);
 #pragma unroll
-        for (int r = 1; r < 4; ++r) {
-            const double2 w = tw[(k * r * (64 / ns)) & 255];
-            const cplx<real> c = {static_cast<real>(w.x),
-                                  static_cast<real>(kInverse ? -w.y : w.y)};
-            v[r] = cmul(v[r], c);
+            for (int r = 1; r < 4; ++r) {
+                const double2 w = tw.pass[pass - 1][r - 1];
+                const cplx<real> c = {static_cast<real>(w.x),
+                                      static_cast<real>(kInverse ? -w.y : w.y)};
+                v[r] = cmul(v[r], c);
+            }
         }
         dft4<real, kInverse>(v);
+        const int k = lane & (ns - 1);
         const int base = (lane / ns) * ns * 4 + k;
 #pragma unroll
         for (int r = 0; r < 4; ++r) buf[base + r * ns] = v[r];
@@ -86,18 +107,17 @@ __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, cons
 
 // Spectrum of one frame: X_f for f = lane + 64 r (r = 0..3), given the frame
 // samples u (already windowed) through the load functor u(k), k < 512.
-// tw512[f] = e^{-2 pi i f / 512}.
+// tw holds the per lane twiddles (Twiddles::load).
 template <typename real, class Load>
 __device__ __forceinline__ void frame_spectrum(Load u, cplx<real> (&x)[4], cplx<real> *buf,
-                                               const double2 *tw256, const double2 *tw512,
-                                               int lane) {
+                                               const Twiddles &tw, int lane) {
     cplx<real> v[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int n = lane + 64 * r;
         v[r] = {u(2 * n), u(2 * n + 1)};
     }
-    fft256<real, false>(v, buf, tw256, lane);
+    fft256<real, false>(v, buf, tw, lane);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int f = lane + 64 * r;
@@ -106,7 +126,7 @@ __device__ __forceinline__ void frame_spectrum(Load u, cplx<real> (&x)[4], cplx<
         // E = (Zf + conj Zm) / 2,  O = -i (Zf - conj Zm) / 2
         const cplx<real> e = {(zf.re + zm.re) * real(0.5), (zf.im - zm.im) * real(0.5)};
         const cplx<real> o = {(zf.im + zm.im) * real(0.5), -(zf.re - zm.re) * real(0.5)};
-        const double2 w = tw512[f];
+        const double2 w = tw.fold[r];
         const cplx<real> c = {static_cast<real>(w.x), static_cast<real>(w.y)};
         const cplx<real> t = cmul(c, o);
         x[r] = {e.re + t.re, e.im + t.im};
@@ -118,8 +138,7 @@ __device__ __forceinline__ void frame_spectrum(Load u, cplx<real> (&x)[4], cplx<
 // g_u_{2n+1} for n = lane + 64 r in (even[r], odd[r]).  V_256 is zero.
 template <typename real>
 __device__ __forceinline__ void frame_adjoint(const cplx<real> (&vf)[4], real (&even)[4],
-                                              real (&odd)[4], cplx<real> *buf,
-                                              const double2 *tw256, const double2 *tw512,
+                                              real (&odd)[4], cplx<real> *buf, const Twiddles &tw,
                                               int lane) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) buf[lane + 64 * r] = vf[r];
@@ -133,14 +152,14 @@ __device__ __forceinline__ void frame_adjoint(const cplx<real> (&vf)[4], real (&
         const cplx<real> b = f == 0 ? cplx<real>{real(0), real(0)} : buf[kHalf - f];
         const cplx<real> s = {a.re + b.re, a.im - b.im};   // V_f + conj V_{256-f}
         const cplx<real> d = {a.re - b.re, a.im + b.im};   // V_f - conj V_{256-f}
-        const double2 w = tw512[f];
+        const double2 w = tw.fold[r];
         const cplx<real> c = {static_cast<real>(w.x), static_cast<real>(-w.y)};  // e^{+...}
         const cplx<real> t = cmul(c, d);
         // Z' = s + i t
         v[r] = {s.re - t.im, s.im + t.re};
     }
     wave_lds_fence();
-    fft256<real, true>(v, buf, tw256, lane);
+    fft256<real, true>(v, buf, tw, lane);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const cplx<real> z = buf[lane + 64 * r];
