@@ -158,6 +158,15 @@ __device__ __forceinline__ double *band_array(const PipeArgs &a, int which) {
     return region<double>(a.ws, a.L.band) + int64_t(which) * a.L.batch * kBands;
 }
 
+// Band `lane` of the per tile band partials base[tile][49], summed over tiles
+// part, part + parts, part + 2 parts, ... (in that order); 0 when there are none.
+__device__ __forceinline__ double tile_partial(const double *base, int64_t ntile, int part,
+                                               int parts, int lane) {
+    const int n = ntile > part ? static_cast<int>((ntile - 1 - part) / parts) + 1 : 0;
+    return n > 0 ? strided_sum(base + int64_t(part) * kBands + lane, n, int64_t(parts) * kBands)
+                 : 0.0;
+}
+
 // Zwicker loudness sl (2 th)^e ((0.5 + 0.5 x / th)^e - 1) above the threshold,
 // written as loud_scale expm1(e log1p((x - th) / (2 th))) so that bands just
 // above their threshold keep full precision.
@@ -306,11 +315,11 @@ __device__ __forceinline__ BandConsts band_consts(const ModelTable &t, int lane)
     return c;
 }
 
-constexpr int kChainWaves = 4;
+constexpr int kChainWaves = 16;  // one frame of the 16 frame tile per wavefront
 
 __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs a) {
     constexpr int kPer = kTile / kChainWaves;  // frames per wavefront
-    __shared__ double rs[kBands];
+    __shared__ double part[2][kChainWaves][kBands];
 
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
@@ -338,27 +347,36 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs 
         }
     }
 
-    if (wave == 0 && lane < kBands) {
+    // mean band powers over all frames of the item: wavefront w sums the band
+    // partials of tiles w, w + kChainWaves, ...; the partial sums are then
+    // added in wavefront order, the same order in every workgroup
+    if (lane < kBands) {
         const double *pr = region<double>(a.ws, L.bandref) + int64_t(item) * L.ntile * kBands;
         const double *pd = region<double>(a.ws, L.banddeg) + int64_t(item) * L.ntile * kBands;
-        const double sr = strided_sum(pr + lane, static_cast<int>(L.ntile), kBands);
-        const double sd = strided_sum(pd + lane, static_cast<int>(L.ntile), kBands);
-        const double mref = sr / frames_f;
-        const double mdeg = sd / frames_f;
-        const double ratio = (mdeg + 1000.0) / (mref + 1000.0);
-        const double r = fmin(fmax(ratio, 0.01), 100.0);
-        rs[lane] = r;
-        if (tile == 0) {
-            band_array(a, kR)[item * kBands + lane] = r;
-            band_array(a, kRatio)[item * kBands + lane] = ratio;
-            band_array(a, kMref)[item * kBands + lane] = mref;
-        }
+        part[0][wave][lane] = tile_partial(pr, L.ntile, wave, kChainWaves, lane);
+        part[1][wave][lane] = tile_partial(pd, L.ntile, wave, kChainWaves, lane);
     }
     __syncthreads();
 
     const BandConsts c = band_consts(t, lane);
     const bool live = lane < kBands;
-    const double r = live ? rs[lane] : 0.0;
+    double r = 0.0;
+    if (live) {
+        double sr = 0.0, sd = 0.0;
+        for (int w = 0; w < kChainWaves; ++w) {
+            sr += part[0][w][lane];
+            sd += part[1][w][lane];
+        }
+        const double mref = sr / frames_f;
+        const double mdeg = sd / frames_f;
+        const double ratio = (mdeg + 1000.0) / (mref + 1000.0);
+        r = fmin(fmax(ratio, 0.01), 100.0);
+        if (tile == 0 && wave == 0) {
+            band_array(a, kR)[item * kBands + lane] = r;
+            band_array(a, kRatio)[item * kBands + lane] = ratio;
+            band_array(a, kMref)[item * kBands + lane] = mref;
+        }
+    }
     const double sqrt_w = sqrt(t.total_width);
     const double W = t.total_width;
 
@@ -686,7 +704,7 @@ template <typename real>
 __global__ void __launch_bounds__(kWave *kBwdFrames) stft_bwd_kernel(PipeArgs a) {
     __shared__ cplx<real> fftbuf[kBwdFrames][kHalf];
     __shared__ float contrib[kBwdFrames][kNfft];
-    __shared__ double gm[kBands];
+    __shared__ double gpart[kBwdFrames][kBands];
     __shared__ float gband[kBwdFrames][kBands];
     __shared__ double scratch[kBwdFrames];
 
@@ -701,17 +719,22 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_bwd_kernel(PipeArgs a)
     const int lane = threadIdx.x % kWave;
     const int64_t j0 = int64_t(ht) * kBwdHops;   // first output hop block
 
-    // adjoint of the band power ratio and its clamp, then of the mean band powers
-    if (wave == 0 && lane < kBands) {
-        const double *gp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
-        const double g = strided_sum(gp + lane, static_cast<int>(L.ntile), kBands);
+    // adjoint of the band power ratio and its clamp, then of the mean band
+    // powers: wavefront w sums the band partials of tiles w, w + kBwdFrames, ...
+    // and every wavefront adds the partial sums in wavefront order
+    const double *grp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
+    if (lane < kBands) gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kBwdFrames, lane);
+    __syncthreads();
+    double gm = 0.0;
+    if (lane < kBands) {
+        double g = 0.0;
+        for (int w = 0; w < kBwdFrames; ++w) g += gpart[w][lane];
         const double ratio = band_array(a, kRatio)[item * kBands + lane];
         const double mref = band_array(a, kMref)[item * kBands + lane];
         const double gr = (ratio >= 0.01 && ratio <= 100.0) ? g : 0.0;
         const double inv = 1.0 / (mref + 1000.0);
-        gm[lane] = (is_ref ? -gr * ratio * inv : gr * inv) / static_cast<double>(L.frames);
+        gm = (is_ref ? -gr * ratio * inv : gr * inv) / static_cast<double>(L.frames);
     }
-    __syncthreads();
 
     const double scale = region<double>(a.ws, L.rowconst)[int64_t(row) * 4 + 2];
     const float *p = region<float>(a.ws, L.p) + int64_t(row) * L.len;
@@ -735,7 +758,7 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_bwd_kernel(PipeArgs a)
             const float keep = region<float>(a.ws, L.keep)[int64_t(item) * L.frames + frame];
             double g = gbk[fo + lane];
             if (keep != 0.0f && static_cast<double>(bk[fo + lane]) > 100.0 * t.threshs[lane]) {
-                g += gm[lane];
+                g += gm;
             }
             gband[wave][lane] = static_cast<float>(g * t.corr[lane]);
         }
@@ -833,7 +856,8 @@ __global__ void __launch_bounds__(kWave) chain_meanpow_kernel(PipeArgs a) {
     const int lane = threadIdx.x;
     if (lane >= kBands) return;
     const double *gp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
-    const double g = strided_sum(gp + lane, static_cast<int>(L.ntile), kBands);
+    double g = 0.0;  // the summation order of stft_bwd_kernel
+    for (int w = 0; w < kBwdFrames; ++w) g += tile_partial(gp, L.ntile, w, kBwdFrames, lane);
     const double ratio = band_array(a, kRatio)[item * kBands + lane];
     const double mref = band_array(a, kMref)[item * kBands + lane];
     const double gr = (ratio >= 0.01 && ratio <= 100.0) ? g : 0.0;
