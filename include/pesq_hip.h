@@ -124,7 +124,7 @@ int pesq_pipeline_backward_workspace(int64_t batch, int64_t len, int grad_mask, 
  * Replaces PesqLossTriton.raw / mos / forward
  * (torch_pesq/triton_ops/loss.py:104-147,203-215): peak normalisation,
  * level alignment, pre-emphasis, STFT, Bark, perceptual chain and the MOS
- * epilogue, in five kernels (six for rows longer than 131072 samples).  The
+ * epilogue, in six kernels.  The
  * peak normalisation cancels in the level alignment and is not formed; the
  * workspace's "p" and "f" hold the pre-emphasised and band-passed signals in
  * the units of the input.  grad_mask (PESQ_GRAD_*) selects which inputs

@@ -58,6 +58,14 @@ static int fill_sections(IirTable &t, int first, const pesq_iir_sections &s, dou
             std::memcpy(t.pw[level][q], p, sizeof(p));
             mat_mul(p, p, p);
         }
+        // lane start powers A^(kChunk lane): product of the levels of the set bits
+        for (int lane = 0; lane < kWave; ++lane) {
+            double m[4] = {1.0, 0.0, 0.0, 1.0};
+            for (int level = 0; level < kLevelBlock; ++level) {
+                if (lane & (1 << level)) mat_mul(t.pw[level][q], m, m);
+            }
+            std::memcpy(t.lane_pw[q][lane], m, sizeof(m));
+        }
     }
     return PESQ_OK;
 }
@@ -129,11 +137,11 @@ extern "C" int pesq_model_table_pack(const pesq_model_constants *c, void *out) {
     int prev = 0;
     for (int i = 0; i < kBands; ++i) {
         const int lo = c->band_start[i], hi = c->band_end[i];
-        if (lo < prev || hi < lo || hi > kHalf) {
+        if (lo < prev || hi < lo || hi > kHalf || hi - lo > kMaxBandBins) {
             delete t;
-            set_error("Bark band %d covers [%d, %d): bands must be sorted, disjoint and "
-                      "inside [0, 256)",
-                      i, lo, hi);
+            set_error("Bark band %d covers [%d, %d): bands must be sorted, disjoint, "
+                      "inside [0, 256) and at most %d bins wide",
+                      i, lo, hi, kMaxBandBins);
             return PESQ_ERR_ARGUMENT;
         }
         t->band_start[i] = lo;

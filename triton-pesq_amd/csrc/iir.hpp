@@ -18,14 +18,13 @@
 // shared between wavefronts, so the kernels have no LDS and no barriers.
 //   aggregate: zero state run per chunk, in-wave Kogge-Stone scan; the block's
 //              end state per section (given a zero state before the block) is
-//              written to `aggr`, laid out [row][section][block][2];
-//   prefix:    rows of more than kLookbackBlocks blocks only: per (row,
-//              section) an exclusive scan of the block aggregates, written over
-//              them (aggr[b] becomes the state at the start of block b);
-//   output:    zero state run, in-wave scan, block start state (scanned from
-//              the preceding blocks' aggregates, or read after the prefix
-//              kernel) injected at lane 0 of the in-wave scan, so that the
-//              scan gives the true state at the start of every chunk, second
+//              written to `aggr`, laid out [row][section][block][2], and every
+//              lane's start state given a zero block start state to `lanes`,
+//              laid out [row][block][section][lane][2];
+//   prefix:    per (row, section) an exclusive scan of the block aggregates,
+//              written over them (aggr[b] becomes the state at the start of
+//              block b), one wavefront per sequence;
+//   output:    lane start state = lanes[lane] + A^(kChunk lane) aggr[block];
 //              run from it; per sample y = c0 x + y_0 + y_1 + ... in this order.
 // The time axis can be reversed (adjoint filter) by the Mode policy.
 //
@@ -50,12 +49,6 @@ constexpr int kMaxSections = PESQ_IIR_MAX_SECTIONS;
 constexpr int kLevelBlock = 6;
 constexpr int kLevels = 14;
 static_assert(kSpan == kChunk << kLevelBlock, "a block is 2^6 chunks");
-// rows of at most this many blocks scan their preceding block aggregates in
-// the output kernel; longer rows run the prefix kernel first
-#ifndef PESQ_LOOKBACK_BLOCKS
-#define PESQ_LOOKBACK_BLOCKS 128
-#endif
-constexpr int kLookbackBlocks = PESQ_LOOKBACK_BLOCKS;
 
 struct IirTable {
     int32_t na, nb;      // sections of filter A, then of filter B
@@ -63,7 +56,18 @@ struct IirTable {
     double b0[kMaxSections], b1[kMaxSections], b2[kMaxSections];  // b2 = 0 (packing)
     double a1[kMaxSections], a2[kMaxSections];
     double pw[kLevels][kMaxSections][4];     // A_k^(kChunk 2^j), row major 2x2
+    double lane_pw[kMaxSections][kWave][4];  // A_k^(kChunk lane), lane start powers
 };
+
+// Scan workspace of `rows` rows of nblk blocks: the block aggregates
+// [row][section][block][2], then the lane states [row][block][section][lane][2]
+// (sized for kMaxSections sections).
+__host__ __device__ __forceinline__ int64_t scan_aggr_doubles(int64_t rows, int64_t nblk) {
+    return rows * nblk * kMaxSections * 2;
+}
+__host__ __device__ __forceinline__ int64_t scan_workspace_doubles(int64_t rows, int64_t nblk) {
+    return scan_aggr_doubles(rows, nblk) * (1 + kWave);
+}
 
 // --------------------------------------------------------------------------
 // per lane state of a bank of NS sections starting at section S0
@@ -180,23 +184,6 @@ struct BankPair {
     __device__ __forceinline__ double &v(int k) { return k < NA ? a.v[k] : b.v[k - NA]; }
 };
 
-// The aggregates of blocks base + lane (zero past blk) of one row.
-template <int NA, int NB>
-__device__ __forceinline__ BankPair<NA, NB> load_group(const double *row_aggr, int nblk, int base,
-                                                       int blk, int lane) {
-    BankPair<NA, NB> v;
-    const int jb = base + lane;
-    const int jc = jb < blk ? jb : (blk > 0 ? blk - 1 : 0);
-#pragma unroll
-    for (int k = 0; k < NA + NB; ++k) {
-        const double *src = row_aggr + (int64_t(k) * nblk + jc) * 2;
-        const double u = src[0], w = src[1];
-        v.u(k) = jb < blk ? u : 0.0;
-        v.v(k) = jb < blk ? w : 0.0;
-    }
-    return v;
-}
-
 // --------------------------------------------------------------------------
 // the kernels, parametrised by a Mode policy:
 //   Mode::kInputs                 raw inputs per sample (1 or 2)
@@ -308,7 +295,7 @@ __device__ __forceinline__ void chunk_inputs(const Mode &m, const float (&in)[Mo
 template <int NA, int NB, class Mode>
 __global__ void __launch_bounds__(kWave)
     iir_aggregate_kernel(Mode m, const IirTable *__restrict__ table, double *__restrict__ aggr,
-                         int64_t len, int nblk) {
+                         double *__restrict__ lanes, int64_t len, int nblk) {
     constexpr int NS = NA + NB;
     const IirTable &t = *table;
     const int row = blockIdx.x / nblk;
@@ -344,6 +331,13 @@ __global__ void __launch_bounds__(kWave)
             dst[0] = s.u(k);
             dst[1] = s.v(k);
         }
+    }
+    // start state of every lane's chunk (the end state of the chunk before it)
+    double2 *dst = reinterpret_cast<double2 *>(lanes) + (int64_t(row) * nblk + blk) * NS * kWave;
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const double u = shfl_up(s.u(k), 1), v = shfl_up(s.v(k), 1);
+        dst[k * kWave + lane] = lane == 0 ? make_double2(0.0, 0.0) : make_double2(u, v);
     }
 }
 
@@ -401,7 +395,8 @@ __global__ void __launch_bounds__(kWave *kPrefixWaves)
 template <int NA, int NB, class Mode>
 __global__ void __launch_bounds__(kWave)
     iir_output_kernel(Mode m, const IirTable *__restrict__ table,
-                      const double *__restrict__ aggr, int64_t len, int nblk, int prefixed) {
+                      const double *__restrict__ aggr, const double *__restrict__ lanes,
+                      int64_t len, int nblk) {
     constexpr int NS = NA + NB;
     const IirTable &t = *table;
     const int row = blockIdx.x / nblk;
@@ -410,84 +405,43 @@ __global__ void __launch_bounds__(kWave)
     const int64_t j0 = int64_t(blk) * kSpan + int64_t(lane) * kChunk;
     const bool edge = j0 < kEdge || j0 + kChunk + kEdge > len;
 
-    // the block start states (or the first group of aggregates), the row
-    // constants and the raw inputs are all requested before any of them is used
+    // everything this wavefront reads is requested up front: the block start
+    // states, the lane start states, the row constants and the raw inputs
     const double *row_aggr = aggr + int64_t(row) * NS * nblk * 2;
     BankPair<NA, NB> p;
-    if (prefixed) {
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const double *src = row_aggr + (int64_t(k) * nblk + blk) * 2;
+        p.u(k) = src[0];
+        p.v(k) = src[1];
+    }
+    BankPair<NA, NB> s;
+    {
+        const double2 *src =
+            reinterpret_cast<const double2 *>(lanes) + (int64_t(row) * nblk + blk) * NS * kWave;
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
-            const double *src = row_aggr + (int64_t(k) * nblk + blk) * 2;
-            p.u(k) = src[0];
-            p.v(k) = src[1];
+            const double2 w = src[k * kWave + lane];
+            s.u(k) = w.x;
+            s.v(k) = w.y;
         }
-    } else {
-        p = load_group<NA, NB>(row_aggr, nblk, 0, blk, lane);
     }
     double sh[4];
     m.setup(row, sh, lane);
     float in[kChunk][Mode::kInputs];
     load_chunk(m, row, j0, len, in);
 
-    // state at the start of the block, scanned from the preceding blocks'
-    // aggregates while the inputs are in flight (wave-uniform afterwards)
-    if (!prefixed) {
-        BankPair<NA, NB> carry;
-        carry.zero();
-        for (int base = 0; base < blk; base += kWave) {
-            BankPair<NA, NB> v = base == 0 ? p : load_group<NA, NB>(row_aggr, nblk, base, blk, lane);
-            // the state entering the group is carried into its first element
-            if (lane == 0) {
-                BankPair<NA, NB> c = carry;
-                c.power(t, kLevelBlock, v);
-                v = c;
-            }
-            v.scan(t, kLevelBlock, lane);
-            const int src = (blk - base < kWave ? blk - base : kWave) - 1;
-#pragma unroll
-            for (int k = 0; k < NS; ++k) {
-                carry.u(k) = shfl(v.u(k), src);
-                carry.v(k) = shfl(v.v(k), src);
-            }
-        }
-        p = carry;
-    }
-
-    // zero state run per chunk; lane 0 also carries the block start state
-    // (A^kChunk p) into its element, so that the in-wave scan yields the true
-    // state at the end of every chunk
-    BankPair<NA, NB> s;
-    s.zero();
-    {
-        Coeffs<0, NA> ca;
-        Coeffs<NA, NB> cb;
-        ca.load(t, t.c0a);
-        cb.load(t, t.c0b);
-#pragma unroll
-        for (int i = 0; i < kChunk; ++i) {
-            double xa, xb;
-            chunk_inputs(m, in[i], ramp_weight<Mode>(edge, j0 + i, len), j0 + i, len, xa, xb);
-            if constexpr (NA > 0) ca.step(s.a, xa);
-            if constexpr (NB > 0) cb.step(s.b, xb);
-        }
-    }
-    if (lane == 0) {
-        BankPair<NA, NB> c = p;
-        c.power(t, 0, s);
-        s = c;
-    }
-    s.scan(t, 0, lane);
-
-    // lane start state = end state of the chunk before it (p for lane 0)
+    // lane start state = (start state given a zero block start) + A^(kChunk lane) p
+    const IirTable &t2 = *reload(table);
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
-        const double su = shfl_up(s.u(k), 1), sv = shfl_up(s.v(k), 1);
-        s.u(k) = lane == 0 ? p.u(k) : su;
-        s.v(k) = lane == 0 ? p.v(k) : sv;
+        const double *lp = t2.lane_pw[k][lane];
+        const double pu = p.u(k), pv = p.v(k);
+        s.u(k) = fma(lp[0], pu, fma(lp[1], pv, s.u(k)));
+        s.v(k) = fma(lp[2], pu, fma(lp[3], pv, s.v(k)));
     }
 
-    // second run from the true start state (coefficients read again)
-    const IirTable &t2 = *reload(table);
+    // run from the true start state
     Coeffs<0, NA> ca;
     Coeffs<NA, NB> cb;
     ca.load(t2, t2.c0a);
@@ -522,33 +476,33 @@ __global__ void __launch_bounds__(kWave)
     }
 }
 
-// Host side: aggregate (+ prefix for long rows) and output launches of one
-// scan pass over `rows` rows; `aggr` holds rows * (NA + NB) * nblk * 2 doubles.
+// Host side: aggregate, prefix and output launches of one scan pass over
+// `rows` rows; `ws` holds scan_workspace_doubles(rows, nblk).
 template <int NA, int NB, class Mode>
-int launch_scan(const Mode &m, const IirTable *table, double *aggr, int64_t rows, int64_t len,
+int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, int64_t len,
                 bool aggregate, bool output, hipStream_t stream) {
     constexpr int NS = NA + NB;
+    static_assert(NS <= kMaxSections, "too many sections");
     const int64_t nblk = cdiv(len, kBlockSpan);
+    double *aggr = ws;
+    double *lanes = ws + scan_aggr_doubles(rows, nblk);
     const unsigned grid = static_cast<unsigned>(rows * nblk);
-    const bool prefixed = nblk > kLookbackBlocks;
     if (grid == 0) return PESQ_OK;
     if (aggregate) {
         hipLaunchKernelGGL((iir_aggregate_kernel<NA, NB, Mode>), dim3(grid), dim3(kWave), 0,
-                           stream, m, table, aggr, len, static_cast<int>(nblk));
+                           stream, m, table, aggr, lanes, len, static_cast<int>(nblk));
         PESQ_CHECK_LAUNCH("iir aggregate");
-        if (prefixed) {
-            const int64_t nseq = rows * NS;
-            hipLaunchKernelGGL(iir_prefix_kernel<NS>,
-                               dim3(static_cast<unsigned>(cdiv(nseq, kPrefixWaves))),
-                               dim3(kWave * kPrefixWaves), 0, stream, table, aggr,
-                               static_cast<int>(nblk), nseq);
-            PESQ_CHECK_LAUNCH("iir prefix");
-        }
+        const int64_t nseq = rows * NS;
+        hipLaunchKernelGGL(iir_prefix_kernel<NS>,
+                           dim3(static_cast<unsigned>(cdiv(nseq, kPrefixWaves))),
+                           dim3(kWave * kPrefixWaves), 0, stream, table, aggr,
+                           static_cast<int>(nblk), nseq);
+        PESQ_CHECK_LAUNCH("iir prefix");
     }
     if (output) {
         hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode>), dim3(grid), dim3(kWave), 0, stream,
-                           m, table, static_cast<const double *>(aggr), len,
-                           static_cast<int>(nblk), prefixed ? 1 : 0);
+                           m, table, static_cast<const double *>(aggr),
+                           static_cast<const double *>(lanes), len, static_cast<int>(nblk));
         PESQ_CHECK_LAUNCH("iir output");
     }
     return PESQ_OK;

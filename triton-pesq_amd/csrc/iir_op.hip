@@ -63,7 +63,7 @@ extern "C" int pesq_iir_workspace(int64_t rows, int64_t len, size_t *bytes) {
     PESQ_CHECK_ARG(rows >= 0 && len >= 0 && bytes != nullptr, "invalid sizes");
     const int64_t nblk = cdiv(len, kBlockSpan);
     PESQ_CHECK_ARG(rows * nblk < (int64_t(1) << 31), "too many rows x blocks for one launch");
-    *bytes = size_t(rows) * nblk * 2 * kMaxSections * sizeof(double);
+    *bytes = size_t(scan_workspace_doubles(rows, nblk)) * sizeof(double);
     return PESQ_OK;
 }
 

@@ -17,8 +17,8 @@
 //   8. iir_aggregate  <power^T, pre^T> on (f, dL/dp), time reversed
 //   9. iir_output     <power^T, pre^T> and the level alignment adjoint:
 //        dL/ds = scale ramp(pre^T g_p) - scale S / E power^T f,  S = sum g_p p
-// Rows longer than kLookbackBlocks scan blocks add an iir_prefix launch
-// between 1 and 2 and between 8 and 9.
+// Each scan pass also runs iir_prefix (block start states from the block
+// aggregates) between its aggregate and output kernels.
 //
 // The level alignment (torch_pesq/loss.py:127-139) is folded in: with
 // E = sum f^2 the aligned, pre-emphasised signal is p_aligned = scale * p,
@@ -205,6 +205,12 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
     const int side = wave / 4;                   // 0 = reference, 1 = degraded
     const int row = side * L.batch + item;
 
+    // samples of this wavefront's first frame, requested before anything else
+    const float *p = region<float>(a.ws, L.p) + int64_t(row) * L.len;
+    const int64_t f_first = t0 + (wave & 3) * 4;
+    float cur[8];
+    load_frame(p, (f_first < L.frames ? f_first : L.frames - 1) * kHop, L.len, lane, cur);
+
     // row constants: -, E, scale, -
     const double *energy = region<double>(a.ws, L.energy) + int64_t(row) * L.nblk;
     const int nmine = lane < L.nblk ? static_cast<int>((L.nblk - 1 - lane) / kWave + 1) : 0;
@@ -221,7 +227,6 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
     }
     const real scale2 = static_cast<real>(scale * scale);
 
-    const float *p = region<float>(a.ws, L.p) + int64_t(row) * L.len;
     float *bark = region<float>(a.ws, L.bark) + int64_t(row) * L.frames * kBands;
     cplx<real> *buf = fftbuf[wave];
     real *power_buf = reinterpret_cast<real *>(buf);
@@ -242,15 +247,19 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
         const int local = (wave & 3) * 4 + q;
         const int64_t frame = t0 + local;
         if (frame >= L.frames) break;
-        const int64_t start = frame * kHop;
+        // the next frame's samples load while this one is transformed
+        float nxt[8];
+        const int64_t fn = frame + 1 < L.frames ? frame + 1 : frame;
+        load_frame(p, fn * kHop, L.len, lane, nxt);
         auto u = [&](int k) -> real {
-            const int64_t n = start + k;
-            // k = 2 (lane + 64 r) + {0, 1}: the window value is in win[2 r + {0, 1}]
-            const float w = win[2 * (k >> 7) + (k & 1)];
-            return static_cast<real>(load_or_zero(p, n, L.len)) * static_cast<real>(w);
+            // k = 2 (lane + 64 r) + {0, 1}: sample and window value at index 2 r + {0, 1}
+            const int i = 2 * (k >> 7) + (k & 1);
+            return static_cast<real>(cur[i]) * static_cast<real>(win[i]);
         };
         cplx<real> x[4];
         frame_spectrum<real>(u, x, buf, tw, lane);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int fbin = lane + 64 * r;
@@ -259,10 +268,7 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
         wave_lds_fence();
         double val = 0.0;
         if (lane < kBands) {
-            double acc = 0.0;
-            for (int fbin = band_lo; fbin < band_hi; ++fbin) {
-                acc += static_cast<double>(power_buf[fbin]);
-            }
+            const double acc = band_sum(power_buf, band_lo, band_hi);
             const float v = static_cast<float>(acc * corr);
             bark[frame * kBands + lane] = v;
             barks[side][local][lane] = v;
@@ -286,10 +292,10 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
     if (wave < 2 && lane < kBands) {
         const double th100 = 100.0 * t.threshs[lane];
         double acc = 0.0;
+#pragma unroll
         for (int local = 0; local < kTile; ++local) {
-            if (t0 + local >= L.frames) break;
             const double v = barks[wave][local][lane];
-            if (keepflag[local] != 0.0f && v > th100) acc += v;
+            if (t0 + local < L.frames && keepflag[local] != 0.0f && v > th100) acc += v;
         }
         double *dst = region<double>(a.ws, wave == 0 ? L.bandref : L.banddeg);
         dst[(int64_t(item) * L.ntile + tile) * kBands + lane] = acc;
@@ -719,6 +725,19 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_bwd_kernel(PipeArgs a)
     const int lane = threadIdx.x % kWave;
     const int64_t j0 = int64_t(ht) * kBwdHops;   // first output hop block
 
+    // this wavefront's frame: samples and band data are requested first
+    const int64_t frame = j0 - 1 + wave;
+    const bool live = frame >= 0 && frame < L.frames;
+    const int64_t fc = frame < 0 ? 0 : (frame >= L.frames ? L.frames - 1 : frame);
+    const float *p = region<float>(a.ws, L.p) + int64_t(row) * L.len;
+    float smp[8];
+    load_frame(p, fc * kHop, L.len, lane, smp);
+    const int band_l = lane < kBands ? lane : kBands - 1;
+    const int64_t fo = fc * kBands;
+    const float bk_v = region<float>(a.ws, L.bark)[int64_t(row) * L.frames * kBands + fo + band_l];
+    const float gbk_v = region<float>(a.bw, L.gbark)[int64_t(row) * L.frames * kBands + fo + band_l];
+    const float keep = region<float>(a.ws, L.keep)[int64_t(item) * L.frames + fc];
+
     // adjoint of the band power ratio and its clamp, then of the mean band
     // powers: wavefront w sums the band partials of tiles w, w + kBwdFrames, ...
     // and every wavefront adds the partial sums in wavefront order
@@ -737,10 +756,8 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_bwd_kernel(PipeArgs a)
     }
 
     const double scale = region<double>(a.ws, L.rowconst)[int64_t(row) * 4 + 2];
-    const float *p = region<float>(a.ws, L.p) + int64_t(row) * L.len;
-    const int64_t frame = j0 - 1 + wave;
     cplx<real> *buf = fftbuf[wave];
-    if (frame >= 0 && frame < L.frames) {
+    if (live) {
         Twiddles tw;
         tw.load(t.tw256, t.tw512, lane);
         float win[8];
@@ -751,23 +768,15 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_bwd_kernel(PipeArgs a)
             win[2 * r + 1] = t.window[2 * (lane + 64 * r) + 1];
             bin_band[r] = t.bin_band[lane + 64 * r];
         }
-        const int64_t fo = frame * kBands;
         if (lane < kBands) {
-            const float *bk = region<float>(a.ws, L.bark) + int64_t(row) * L.frames * kBands;
-            const float *gbk = region<float>(a.bw, L.gbark) + int64_t(row) * L.frames * kBands;
-            const float keep = region<float>(a.ws, L.keep)[int64_t(item) * L.frames + frame];
-            double g = gbk[fo + lane];
-            if (keep != 0.0f && static_cast<double>(bk[fo + lane]) > 100.0 * t.threshs[lane]) {
-                g += gm;
-            }
+            double g = gbk_v;
+            if (keep != 0.0f && static_cast<double>(bk_v) > 100.0 * t.threshs[lane]) g += gm;
             gband[wave][lane] = static_cast<float>(g * t.corr[lane]);
         }
         wave_lds_fence();
-        const int64_t start = frame * kHop;
         auto u = [&](int k) -> real {
-            const int64_t n = start + k;
-            const float w = win[2 * (k >> 7) + (k & 1)];
-            return static_cast<real>(load_or_zero(p, n, L.len)) * static_cast<real>(w);
+            const int i = 2 * (k >> 7) + (k & 1);
+            return static_cast<real>(smp[i]) * static_cast<real>(win[i]);
         };
         cplx<real> x[4];
         frame_spectrum<real>(u, x, buf, tw, lane);

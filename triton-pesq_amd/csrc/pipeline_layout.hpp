@@ -52,13 +52,12 @@ struct PipeLayout {
         row0 = (mask & PESQ_GRAD_REF) ? 0 : b;
         nrg = mask == (PESQ_GRAD_REF | PESQ_GRAD_DEG) ? 2 * b : (mask ? b : 0);
 
-        constexpr int nstate = 2 * (kMaxSections);  // generous: 2 states x 8 sections
         size_t off = 0;
         auto take = [&](size_t &field, size_t bytes) {
             field = off;
             off = align(off + bytes);
         };
-        take(aggr, size_t(rows) * nblk * nstate * sizeof(double));
+        take(aggr, size_t(scan_workspace_doubles(rows, nblk)) * sizeof(double));
         take(energy, size_t(rows) * nblk * sizeof(double));
         take(p, size_t(rows) * len * sizeof(float));
         take(f, size_t(nrg) * len * sizeof(float));
@@ -78,7 +77,7 @@ struct PipeLayout {
         take(grpart, size_t(batch) * ntile * kBands * sizeof(double));
         take(gp, size_t(nrg) * len * sizeof(float));
         take(spart, size_t(nrg) * nhoptile * sizeof(double));
-        take(aggr_b, size_t(nrg) * nblk * nstate * sizeof(double));
+        take(aggr_b, size_t(scan_workspace_doubles(nrg, nblk)) * sizeof(double));
         bwd_bytes = off;
     }
 

@@ -21,6 +21,34 @@ constexpr int kNfft = 512;
 constexpr int kHop = 256;
 constexpr int kHalf = 256;
 constexpr int kBands = 49;
+constexpr int kMaxBandBins = 25;  // widest Bark band of the 16 kHz table (bins)
+
+// The 8 samples of a 512 sample frame that lane `lane` folds into its 4 complex
+// inputs: s[2 r + e] = x[start + 2 (lane + 64 r) + e] (zero past len).
+__device__ __forceinline__ void load_frame(const float *x, int64_t start, int64_t len, int lane,
+                                           float (&s)[8]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) s[2 * r + e] = load_or_zero(x, start + 2 * (lane + 64 * r) + e, len);
+    }
+}
+
+// sum of p[lo .. hi - 1] in index order (hi - lo <= kMaxBandBins), the reads
+// issued together
+template <typename real>
+__device__ __forceinline__ double band_sum(const real *p, int lo, int hi) {
+    double v[kMaxBandBins];
+#pragma unroll
+    for (int i = 0; i < kMaxBandBins; ++i) {
+        const int f = lo + i;
+        v[i] = static_cast<double>(p[f < kHalf ? f : kHalf - 1]);
+    }
+    double acc = 0.0;
+#pragma unroll
+    for (int i = 0; i < kMaxBandBins; ++i) acc += lo + i < hi ? v[i] : 0.0;
+    return acc;
+}
 
 template <typename real>
 struct cplx {
