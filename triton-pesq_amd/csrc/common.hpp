@@ -57,12 +57,31 @@ __device__ __forceinline__ double shfl(double v, int src) {
     return __shfl(v, src, kWave);
 }
 
-// Butterfly sum over the 64 lanes; every lane ends with the same value and
-// the association order is fixed, so the result is bitwise deterministic.
+// v of the lane `d` below in the same row of 16 lanes, 0 for the first d
+// lanes of a row (DPP row shift, a VALU operation)
+template <int d>
+__device__ __forceinline__ double row_shr(double v) {
+    static_assert(d >= 1 && d <= 15, "row shift");
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), 0x110 + d, 0xF, 0xF, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), 0x110 + d, 0xF, 0xF, true);
+    return __hiloint2double(hi, lo);
+}
+
+__device__ __forceinline__ double read_lane(double v, int lane) {
+    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), lane),
+                            __builtin_amdgcn_readlane(__double2loint(v), lane));
+}
+
+// Sum over the 64 lanes, returned to every lane: an in-row scan by DPP row
+// shifts leaves each row's sum in its last lane, and the four row sums are
+// added in row order.  The association order is fixed, so the result is
+// bitwise deterministic.  All 64 lanes must be active at the call.
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
-    return v;
+    v += row_shr<1>(v);
+    v += row_shr<2>(v);
+    v += row_shr<4>(v);
+    v += row_shr<8>(v);
+    return ((read_lane(v, 15) + read_lane(v, 31)) + read_lane(v, 47)) + read_lane(v, 63);
 }
 
 __device__ __forceinline__ float wave_max(float v) {

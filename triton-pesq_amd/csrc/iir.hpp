@@ -276,20 +276,69 @@ __device__ __forceinline__ void store_chunk(float *base, const float (&out)[kChu
     }
 }
 
-// edge ramp weight at time index j; 1 in chunks at least kEdge from both ends
-template <class Mode>
-__device__ __forceinline__ double ramp_weight(bool edge, int64_t j, int64_t len) {
-    if constexpr (!Mode::kRamp) return 1.0;
-    return edge ? edge_weight(Mode::kReverse ? len - 1 - j : j, len) : 1.0;
+// A chunk is "general" when it reaches within kEdge samples of a row end (or
+// past it): only there do the edge ramp weights differ from 1 and time indices
+// fall outside the row.  Interior chunks take a path without either check.
+__device__ __forceinline__ bool general_chunk(int64_t j0, int64_t len) {
+    return j0 < kEdge || j0 + kChunk + kEdge > len;
 }
 
-// filter inputs of time index j (zero past the end of the row)
-template <class Mode>
-__device__ __forceinline__ void chunk_inputs(const Mode &m, const float (&in)[Mode::kInputs],
-                                             double w, int64_t j, int64_t len, double &xa,
-                                             double &xb) {
+// filter inputs of element i (time index j0 + i) of a chunk
+template <bool kGeneral, class Mode>
+__device__ __forceinline__ void element_inputs(const Mode &m, const float (&in)[Mode::kInputs],
+                                               int64_t j, int64_t len, double &w, double &xa,
+                                               double &xb) {
+    w = 1.0;
+    if constexpr (kGeneral && Mode::kRamp) {
+        if (j < len) w = edge_weight(Mode::kReverse ? len - 1 - j : j, len);
+    }
     m.inputs(w, in, xa, xb);
-    if (j >= len) xa = xb = 0.0;
+    if constexpr (kGeneral) {
+        if (j >= len) xa = xb = 0.0;
+    }
+}
+
+// zero state run over the lane's chunk
+template <bool kGeneral, int NA, int NB, class Mode>
+__device__ __forceinline__ void zero_run(const Mode &m, const Coeffs<0, NA> &ca,
+                                         const Coeffs<NA, NB> &cb,
+                                         const float (&in)[kChunk][Mode::kInputs], int64_t j0,
+                                         int64_t len, BankPair<NA, NB> &s) {
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+        double w, xa, xb;
+        element_inputs<kGeneral>(m, in[i], j0 + i, len, w, xa, xb);
+        if constexpr (NA > 0) ca.step(s.a, xa);
+        if constexpr (NB > 0) cb.step(s.b, xb);
+    }
+}
+
+// run from the true start state s, outputs into out[][i]
+template <bool kGeneral, int NA, int NB, class Mode>
+__device__ __forceinline__ void output_run(const Mode &m, const Coeffs<0, NA> &ca,
+                                           const Coeffs<NA, NB> &cb,
+                                           const float (&in)[kChunk][Mode::kInputs], int64_t j0,
+                                           int64_t len, const double *sh, BankPair<NA, NB> &s,
+                                           float (&out)[Mode::kOutputs][kChunk], double &acc) {
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+        const int64_t j = j0 + i;
+        double w, xa, xb;
+        element_inputs<kGeneral>(m, in[i], j, len, w, xa, xb);
+        double ya = 0.0, yb = 0.0;
+        if constexpr (NA > 0) ya = ca.step(s.a, xa);
+        if constexpr (NB > 0) yb = cb.step(s.b, xb);
+        float o[Mode::kOutputs];
+        const double before = acc;
+        m.compute(w, ya, yb, acc, sh, o);
+        if constexpr (kGeneral) {
+            if (j >= len) acc = before;  // past the end of the row
+        }
+#pragma unroll
+        for (int q = 0; q < Mode::kOutputs; ++q) {
+            out[q][i] = (!kGeneral || j < len) ? o[q] : 0.0f;
+        }
+    }
 }
 
 template <int NA, int NB, class Mode>
@@ -302,10 +351,6 @@ __global__ void __launch_bounds__(kWave)
     const int blk = blockIdx.x - row * nblk;
     const int lane = threadIdx.x;
     const int64_t j0 = int64_t(blk) * kSpan + int64_t(lane) * kChunk;
-    // with len >= 2 kEdge + kChunk only the first and last chunks are edges;
-    // shorter rows take the general path everywhere
-    const bool edge = j0 < kEdge || j0 + kChunk + kEdge > len;
-
     Coeffs<0, NA> ca;
     Coeffs<NA, NB> cb;
     ca.load(t, t.c0a);
@@ -316,12 +361,10 @@ __global__ void __launch_bounds__(kWave)
 
     BankPair<NA, NB> s;
     s.zero();
-#pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-        double xa, xb;
-        chunk_inputs(m, in[i], ramp_weight<Mode>(edge, j0 + i, len), j0 + i, len, xa, xb);
-        if constexpr (NA > 0) ca.step(s.a, xa);
-        if constexpr (NB > 0) cb.step(s.b, xb);
+    if (general_chunk(j0, len)) {
+        zero_run<true>(m, ca, cb, in, j0, len, s);
+    } else {
+        zero_run<false>(m, ca, cb, in, j0, len, s);
     }
     s.scan(t, 0, lane);
     if (lane == kWave - 1) {
@@ -398,12 +441,10 @@ __global__ void __launch_bounds__(kWave)
                       const double *__restrict__ aggr, const double *__restrict__ lanes,
                       int64_t len, int nblk) {
     constexpr int NS = NA + NB;
-    const IirTable &t = *table;
     const int row = blockIdx.x / nblk;
     const int blk = blockIdx.x - row * nblk;
     const int lane = threadIdx.x;
     const int64_t j0 = int64_t(blk) * kSpan + int64_t(lane) * kChunk;
-    const bool edge = j0 < kEdge || j0 + kChunk + kEdge > len;
 
     // everything this wavefront reads is requested up front: the block start
     // states, the lane start states, the row constants and the raw inputs
@@ -432,7 +473,7 @@ __global__ void __launch_bounds__(kWave)
     load_chunk(m, row, j0, len, in);
 
     // lane start state = (start state given a zero block start) + A^(kChunk lane) p
-    const IirTable &t2 = *reload(table);
+    const IirTable &t2 = *table;
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
         const double *lp = t2.lane_pw[k][lane];
@@ -448,21 +489,10 @@ __global__ void __launch_bounds__(kWave)
     cb.load(t2, t2.c0b);
     float out[Mode::kOutputs][kChunk];
     double acc = 0.0;
-#pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-        const int64_t j = j0 + i;
-        const double w = ramp_weight<Mode>(edge, j, len);
-        double xa, xb;
-        chunk_inputs(m, in[i], w, j, len, xa, xb);
-        double ya = 0.0, yb = 0.0;
-        if constexpr (NA > 0) ya = ca.step(s.a, xa);
-        if constexpr (NB > 0) yb = cb.step(s.b, xb);
-        float o[Mode::kOutputs];
-        const double before = acc;
-        m.compute(w, ya, yb, acc, sh, o);
-        if (j >= len) acc = before;  // past the end of the row
-#pragma unroll
-        for (int q = 0; q < Mode::kOutputs; ++q) out[q][i] = j < len ? o[q] : 0.0f;
+    if (general_chunk(j0, len)) {
+        output_run<true>(m, ca, cb, in, j0, len, sh, s, out, acc);
+    } else {
+        output_run<false>(m, ca, cb, in, j0, len, sh, s, out, acc);
     }
 #pragma unroll
     for (int q = 0; q < Mode::kOutputs; ++q) {

@@ -169,16 +169,30 @@ __device__ __forceinline__ double tile_partial(const double *base, int64_t ntile
 
 // Zwicker loudness sl (2 th)^e ((0.5 + 0.5 x / th)^e - 1) above the threshold,
 // written as loud_scale expm1(e log1p((x - th) / (2 th))) so that bands just
-// above their threshold keep full precision.
-__device__ __forceinline__ double loudness(double x, double th, double e, double ls) {
+// above their threshold keep full precision (inv2th = 1 / (2 th)).
+__device__ __forceinline__ double loudness(double x, double th, double inv2th, double e,
+                                           double ls) {
     if (!(x > th)) return 0.0;
-    return ls * expm1(e * log1p(0.5 * (x - th) / th));
+    return ls * expm1(e * log1p((x - th) * inv2th));
 }
 
-// d loudness / dx above the threshold
-__device__ __forceinline__ double loudness_slope(double x, double th, double e, double ls) {
-    if (!(x > th)) return 0.0;
-    return ls * e * 0.5 / th * exp((e - 1.0) * log1p(0.5 * (x - th) / th));
+// loudness and d loudness / dx, sharing the logarithm
+__device__ __forceinline__ void loudness_and_slope(double x, double th, double inv2th, double e,
+                                                   double ls, double &l, double &slope) {
+    if (!(x > th)) {
+        l = slope = 0.0;
+        return;
+    }
+    const double lg = log1p((x - th) * inv2th);
+    l = ls * expm1(e * lg);
+    slope = ls * e * inv2th * exp((e - 1.0) * lg);
+}
+
+// raw asymmetry factor ((ed + 50) / (er + 50))^1.2, inv_er50 = 1 / (er + 50);
+// forward and backward evaluate the same expression, so their clamp decisions
+// (below 3, above 12) agree
+__device__ __forceinline__ double asymmetry(double ed, double inv_er50) {
+    return exp(1.2 * log((ed + 50.0) * inv_er50));
 }
 
 __device__ __forceinline__ double sgn(double v) { return v > 0.0 ? 1.0 : (v < 0.0 ? -1.0 : 0.0); }
@@ -307,13 +321,14 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
 // ---------------------------------------------------------------------------
 
 struct BandConsts {
-    double th, e, ls, w;
+    double th, inv2th, e, ls, w;
 };
 
 __device__ __forceinline__ BandConsts band_consts(const ModelTable &t, int lane) {
-    BandConsts c{1.0, 1.0, 0.0, 0.0};
+    BandConsts c{1.0, 0.5, 1.0, 0.0, 0.0};
     if (lane < kBands) {
         c.th = t.threshs[lane];
+        c.inv2th = 0.5 / c.th;
         c.e = t.exps[lane];
         c.ls = t.loud_scale[lane];
         c.w = t.width[lane];
@@ -383,8 +398,9 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs 
             band_array(a, kMref)[item * kBands + lane] = mref;
         }
     }
-    const double sqrt_w = sqrt(t.total_width);
     const double W = t.total_width;
+    const double inv_sqrt_w = 1.0 / sqrt(t.total_width);
+    const double inv_w = 1.0 / W;
 
     // per frame totals of the audible energies; slot q is frame f0 - 1 + q
     double taer[kPer + 1], tad[kPer + 1];
@@ -403,7 +419,8 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs 
         const int64_t frame = f0 + q;
         if (frame >= L.frames) break;
         const double fpr0 = (taer[q + 1] + 5e3) / (tad[q + 1] + 5e3);
-        const double h = pow((taer[q + 1] + 1e5) / 1e7, 0.04);
+        const double h = exp(0.04 * log((taer[q + 1] + 1e5) / 1e7));
+        const double inv_h = 1.0 / h;
         const double fpr1 =
             frame > 0 ? fpr0 * 0.8 + ((taer[q] + 5e3) / (tad[q] + 5e3)) * 0.2 : fpr0;
         const double fpr = fmin(fmax(fpr1, 3e-4), 5.0);
@@ -412,17 +429,17 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs 
         if (live) {
             const double er = r * static_cast<double>(R[q + 1]);
             const double ed = fpr * static_cast<double>(G[q + 1]);
-            const double lr = loudness(er, c.th, c.e, c.ls);
-            const double ld = loudness(ed, c.th, c.e, c.ls);
+            const double lr = loudness(er, c.th, c.inv2th, c.e, c.ls);
+            const double ld = loudness(ed, c.th, c.inv2th, c.e, c.ls);
             const double u = ld - lr;
             const double z = fabs(u) - 0.25 * fmin(ld, lr);
             const double dist = sgn(u) * fmax(z, 0.0);
-            const double asc_raw = pow((ed + 50.0) / (er + 50.0), 1.2);
+            const double asc_raw = asymmetry(ed, 1.0 / (er + 50.0));
             const double asc = asc_raw < 3.0 ? 0.0 : fmin(asc_raw, 12.0);
             if (lane >= 1) {
-                const double v = c.w * dist / sqrt_w;
+                const double v = c.w * dist * inv_sqrt_w;
                 v2 = v * v;
-                ya = fabs(c.w * (dist * asc) / W);
+                ya = fabs(c.w * (dist * asc) * inv_w);
             }
         }
         const double symm_raw = W * sqrt(wave_sum(v2));
@@ -436,8 +453,8 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs 
             frame_array(a, kH)[o] = h;
             frame_array(a, kSymmRaw)[o] = symm_raw;
             frame_array(a, kAsymmRaw)[o] = asymm_raw;
-            frame_array(a, kSymm)[o] = fmin(fmax(symm_raw, 1e-20) / h, 45.0);
-            frame_array(a, kAsymm)[o] = fmin(fmax(asymm_raw, 1e-20) / h, 45.0);
+            frame_array(a, kSymm)[o] = fmin(fmax(symm_raw, 1e-20) * inv_h, 45.0);
+            frame_array(a, kAsymm)[o] = fmin(fmax(asymm_raw, 1e-20) * inv_h, 45.0);
         }
     }
 }
@@ -503,8 +520,10 @@ constexpr int kPsqmSlots = (kTile + kStride - 1) / kStride + 2;
 
 // d d / d s_t of d = sqrt(mean_l psqm_l^2), psqm_l = (mean_{j<20} s_{10 l + j}^6)^(1/6);
 // pl[i] holds psqm_{lbase + i}
+// (inv_nd = 1 / (nwin d))
 __device__ __forceinline__ double psqm_adjoint(const PipeLayout &L, const double *pl,
-                                               int64_t lbase, double d, double s, int64_t frame) {
+                                               int64_t lbase, double d, double inv_nd, double s,
+                                               int64_t frame) {
     if (!(d > 0.0)) return 0.0;
     double acc = 0.0;
     const int64_t hi = frame / kStride;
@@ -514,7 +533,7 @@ __device__ __forceinline__ double psqm_adjoint(const PipeLayout &L, const double
         if (!(p > 0.0)) continue;
         const double ratio = s / p;
         const double r2 = ratio * ratio;
-        acc += p / (static_cast<double>(L.nwin) * d) * (r2 * r2 * ratio) / kWin;
+        acc += p * inv_nd * (r2 * r2 * ratio) * (1.0 / kWin);
     }
     return acc;
 }
@@ -572,6 +591,8 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
     // upstream gradients of the two distances, MOS and loss folded in
     const double *dist = region<double>(a.ws, L.dist) + int64_t(item) * 2;
     const double ds = dist[0], da = dist[1];
+    const double inv_nds = ds > 0.0 ? 1.0 / (static_cast<double>(L.nwin) * ds) : 0.0;
+    const double inv_nda = da > 0.0 ? 1.0 / (static_cast<double>(L.nwin) * da) : 0.0;
     double gds = a.g_symm ? a.g_symm[item] : 0.0;
     double gda = a.g_asymm ? a.g_asymm[item] : 0.0;
     if (a.g_loss) {
@@ -603,35 +624,39 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
 
         const double s_sy = fr[kSymm][local];
         const double s_as = fr[kAsymm][local];
-        const double g_sy = gds * psqm_adjoint(L, pl[0], lbase, ds, s_sy, frame);
-        const double g_as = gda * psqm_adjoint(L, pl[1], lbase, da, s_as, frame);
+        const double g_sy = gds * psqm_adjoint(L, pl[0], lbase, ds, inv_nds, s_sy, frame);
+        const double g_as = gda * psqm_adjoint(L, pl[1], lbase, da, inv_nda, s_as, frame);
         const double raw_s = fr[kSymmRaw][local];
         const double raw_a = fr[kAsymmRaw][local];
         const double h = fr[kH][local];
+        const double inv_h = 1.0 / h;  // the forward's clamp used the same product
         const double pre_s = fmax(raw_s, 1e-20), pre_a = fmax(raw_a, 1e-20);
-        const double g_ps = pre_s / h <= 45.0 ? g_sy : 0.0;
-        const double g_pa = pre_a / h <= 45.0 ? g_as : 0.0;
-        const double g_hh = -(g_ps * pre_s + g_pa * pre_a) / (h * h);
-        const double g_rs = raw_s >= 1e-20 ? g_ps / h : 0.0;
-        const double g_ra = raw_a >= 1e-20 ? g_pa / h : 0.0;
+        const double g_ps = pre_s * inv_h <= 45.0 ? g_sy : 0.0;
+        const double g_pa = pre_a * inv_h <= 45.0 ? g_as : 0.0;
+        const double g_hh = -(g_ps * pre_s + g_pa * pre_a) * (inv_h * inv_h);
+        const double g_rs = raw_s >= 1e-20 ? g_ps * inv_h : 0.0;
+        const double g_ra = raw_a >= 1e-20 ? g_pa * inv_h : 0.0;
+        const double inv_raw_s = raw_s > 0.0 ? 1.0 / raw_s : 0.0;
         const double fpr = fmin(fmax(fr[kFpr1][local], 3e-4), 5.0);
 
         double my_er = 0.0, my_ed = 0.0, gf = 0.0;
         if (live) {
             const double Rq = R[q], Gq = G[q];
             const double er = r * Rq, ed = fpr * Gq;
-            const double lr = loudness(er, c.th, c.e, c.ls);
-            const double ld = loudness(ed, c.th, c.e, c.ls);
+            double lr, ld, slope_r, slope_d;
+            loudness_and_slope(er, c.th, c.inv2th, c.e, c.ls, lr, slope_r);
+            loudness_and_slope(ed, c.th, c.inv2th, c.e, c.ls, ld, slope_d);
             const double u = ld - lr;
             const double z = fabs(u) - 0.25 * fmin(ld, lr);
             const double su = sgn(u);
             const double dst = su * fmax(z, 0.0);
-            const double asc_raw = pow((ed + 50.0) / (er + 50.0), 1.2);
+            const double inv_er50 = 1.0 / (er + 50.0), inv_ed50 = 1.0 / (ed + 50.0);
+            const double asc_raw = asymmetry(ed, inv_er50);
             const double asc = asc_raw < 3.0 ? 0.0 : fmin(asc_raw, 12.0);
 
             double g_dist = 0.0, g_asc = 0.0;
             if (lane >= 1) {
-                if (raw_s > 0.0) g_dist = g_rs * W * c.w * c.w * dst / raw_s;
+                if (raw_s > 0.0) g_dist = g_rs * W * c.w * c.w * dst * inv_raw_s;
                 const double gy = g_ra * c.w * sgn(dst * asc);
                 g_dist += gy * asc;
                 g_asc = gy * dst;
@@ -643,11 +668,11 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
             const double wr = lr < ld ? 1.0 : (ld == lr ? 0.5 : 0.0);
             const double g_ld = g_u + g_min * wd;
             const double g_lr = -g_u + g_min * wr;
-            my_er = g_lr * loudness_slope(er, c.th, c.e, c.ls);
-            my_ed = g_ld * loudness_slope(ed, c.th, c.e, c.ls);
+            my_er = g_lr * slope_r;
+            my_ed = g_ld * slope_d;
             if (asc_raw >= 3.0 && asc_raw <= 12.0) {
-                my_ed += g_asc * 1.2 * asc_raw / (ed + 50.0);
-                my_er -= g_asc * 1.2 * asc_raw / (er + 50.0);
+                my_ed += g_asc * 1.2 * asc_raw * inv_ed50;
+                my_er -= g_asc * 1.2 * asc_raw * inv_er50;
             }
             gf = my_ed * Gq;
         }
@@ -680,8 +705,9 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
         const double tad = fr[kTad][local];
         const double fpr0 = fr[kFpr0][local];
         const double h = fr[kH][local];
-        const double g_taer = g0 / (tad + 5e3) + gh[local] * 0.04 * h / (taer + 1e5);
-        const double g_tad = -g0 * fpr0 / (tad + 5e3);
+        const double inv_tad = 1.0 / (tad + 5e3);
+        const double g_taer = g0 * inv_tad + gh[local] * 0.04 * h / (taer + 1e5);
+        const double g_tad = -g0 * fpr0 * inv_tad;
         const double fpr = fmin(fmax(f1, 3e-4), 5.0);
         if (live) {
             const double Rq = R[q], Gq = G[q];
@@ -707,7 +733,7 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
 // ---------------------------------------------------------------------------
 
 template <typename real>
-__global__ void __launch_bounds__(kWave *kBwdFrames) stft_bwd_kernel(PipeArgs a) {
+__global__ void __launch_bounds__(kWave *kBwdFrames, 4) stft_bwd_kernel(PipeArgs a) {
     __shared__ cplx<real> fftbuf[kBwdFrames][kHalf];
     __shared__ float contrib[kBwdFrames][kNfft];
     __shared__ double gpart[kBwdFrames][kBands];

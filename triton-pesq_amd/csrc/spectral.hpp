@@ -75,6 +75,13 @@ __device__ __forceinline__ void dft4(cplx<real> (&v)[4]) {
     v[3] = {a1.re - a3.re, a1.im - a3.im};
 }
 
+// LDS slot of complex element i of a frame buffer.  The radix-4 passes write
+// elements 4 l + r and 16 (l / 4) + l % 4 + 4 r from lane l, which put the 16
+// lanes of one LDS cycle on only 4 different bank groups of a 16-byte element;
+// xoring bits 4-5 of the index into bits 0-3 (times 5) spreads every pass over
+// all 16 groups and keeps the unit stride reads conflict free.
+__device__ __forceinline__ int slot(int i) { return i ^ (((i >> 4) & 3) * 5); }
+
 // The wavefront's lanes only touch their own LDS buffer; LDS accesses of one
 // wavefront complete in program order, so a compiler level barrier between
 // the read and the write phases of a pass is all the ordering needed.
@@ -105,7 +112,7 @@ struct Twiddles {
     }
 };
 
-// In: v[r] = z_{lane + 64 r}.  Out: buf[n] = Z_n (natural order), unnormalised.
+// In: v[r] = z_{lane + 64 r}.  Out: buf[slot(n)] = Z_n, unnormalised.
 template <typename real, bool kInverse>
 __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, const Twiddles &tw,
                                        int lane) {
@@ -114,7 +121,7 @@ __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, cons
         const int ns = 1 << (2 * pass);
         if (pass > 0) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) v[r] = buf[lane + 64 * r];
+            for (int r = 0; r < 4; ++r) v[r] = buf[slot(lane + 64 * r)];
             wave_lds_fence();
 #pragma unroll
             for (int r = 1; r < 4; ++r) {
@@ -128,7 +135,7 @@ __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, cons
         const int k = lane & (ns - 1);
         const int base = (lane / ns) * ns * 4 + k;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) buf[base + r * ns] = v[r];
+        for (int r = 0; r < 4; ++r) buf[slot(base + r * ns)] = v[r];
         wave_lds_fence();
     }
 }
@@ -149,8 +156,8 @@ __device__ __forceinline__ void frame_spectrum(Load u, cplx<real> (&x)[4], cplx<
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int f = lane + 64 * r;
-        const cplx<real> zf = buf[f];
-        const cplx<real> zm = buf[(kHalf - f) & (kHalf - 1)];
+        const cplx<real> zf = buf[slot(f)];
+        const cplx<real> zm = buf[slot((kHalf - f) & (kHalf - 1))];
         // E = (Zf + conj Zm) / 2,  O = -i (Zf - conj Zm) / 2
         const cplx<real> e = {(zf.re + zm.re) * real(0.5), (zf.im - zm.im) * real(0.5)};
         const cplx<real> o = {(zf.im + zm.im) * real(0.5), -(zf.re - zm.re) * real(0.5)};
@@ -169,7 +176,7 @@ __device__ __forceinline__ void frame_adjoint(const cplx<real> (&vf)[4], real (&
                                               real (&odd)[4], cplx<real> *buf, const Twiddles &tw,
                                               int lane) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) buf[lane + 64 * r] = vf[r];
+    for (int r = 0; r < 4; ++r) buf[slot(lane + 64 * r)] = vf[r];
     wave_lds_fence();
     cplx<real> v[4];
 #pragma unroll
@@ -177,7 +184,7 @@ __device__ __forceinline__ void frame_adjoint(const cplx<real> (&vf)[4], real (&
         const int f = lane + 64 * r;
         const cplx<real> a = vf[r];
         // V_{256 - f}; f = 0 pairs with the Nyquist bin, which is zero
-        const cplx<real> b = f == 0 ? cplx<real>{real(0), real(0)} : buf[kHalf - f];
+        const cplx<real> b = f == 0 ? cplx<real>{real(0), real(0)} : buf[slot(kHalf - f)];
         const cplx<real> s = {a.re + b.re, a.im - b.im};   // V_f + conj V_{256-f}
         const cplx<real> d = {a.re - b.re, a.im + b.im};   // V_f - conj V_{256-f}
         const double2 w = tw.fold[r];
@@ -190,7 +197,7 @@ __device__ __forceinline__ void frame_adjoint(const cplx<real> (&vf)[4], real (&
     fft256<real, true>(v, buf, tw, lane);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const cplx<real> z = buf[lane + 64 * r];
+        const cplx<real> z = buf[slot(lane + 64 * r)];
         even[r] = z.re;
         odd[r] = z.im;
     }
