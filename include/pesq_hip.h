@@ -32,6 +32,7 @@ extern "C" {
 #define PESQ_ERR_UNSUPPORTED 3
 
 #define PESQ_IIR_MAX_SECTIONS 8
+#define PESQ_IIR_MAX_CASCADE 32 /* biquads of a cascade (order <= 64) */
 #define PESQ_NBARKS 49
 #define PESQ_NFFT 512
 
@@ -78,6 +79,16 @@ size_t pesq_iir_table_bytes(void);
  * design of TritonIIR: torch_pesq/triton_ops/iir.py:520-667 (_state_space,
  * _tables). */
 int pesq_iir_table_pack(const pesq_iir_sections *filter, void *out);
+
+/* Pack a cascade (series) of `sections` full biquads into `out` (host
+ * memory, sections * pesq_iir_table_bytes() bytes), one table per section.
+ * `sos` is [sections][6] row major, each row (b0, b1, b2, a0, a1, a2) of
+ * (b0 + b1 z^-1 + b2 z^-2) / (a0 + a1 z^-1 + a2 z^-2) as scipy.signal.tf2sos
+ * returns it; 1 <= sections <= PESQ_IIR_MAX_CASCADE, a0 != 0.  The cascade
+ * realisation of TritonIIR's _state_space (torch_pesq/triton_ops/iir.py:187-273
+ * _cascade, :599-666), for filters whose parallel form is not accurate
+ * (repeated or clustered poles, numerators longer than the denominator). */
+int pesq_iir_cascade_pack(const double *sos, int sections, void *out);
 
 /* Constants of the PESQ model (PesqLoss.__init__, torch_pesq/loss.py:61-108;
  * BarkScale, torch_pesq/bark.py:131-173; Loudness, torch_pesq/loudness.py:44-55). */
@@ -179,6 +190,18 @@ int pesq_iir_workspace(int64_t rows, int64_t len, size_t *bytes);
  * count of the packed filter (pesq_iir_sections.count). */
 int pesq_iir_apply(const float *x, float *y, int64_t rows, int64_t len, const void *iir_table,
                    int sections, int reverse, void *workspace, hipStream_t stream);
+
+/* Workspace of pesq_iir_cascade_apply: the scan workspace plus up to two
+ * float64 [rows, len] intermediate signals. */
+int pesq_iir_cascade_workspace(int64_t rows, int64_t len, int sections, size_t *bytes);
+
+/* y = lfilter(x) through a packed cascade of `sections` biquads (TritonIIR
+ * forward / _IIRFunction, iir.py:1232-1258,1451-1482): one scan pass per
+ * section with float64 state, float64 signals between the passes; reverse
+ * != 0 applies the adjoint (every pass time reversed). */
+int pesq_iir_cascade_apply(const float *x, float *y, int64_t rows, int64_t len,
+                           const void *cascade_tables, int sections, int reverse,
+                           void *workspace, hipStream_t stream);
 
 /* ----------------------------------------------------------------------- */
 /* resampler (TritonResample, torch_pesq/triton_ops/resample.py:442-574)    */

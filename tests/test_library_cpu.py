@@ -13,12 +13,12 @@ from pathlib import Path
 import numpy as np
 import pytest
 import torch
-from scipy.signal import butter, lfilter
+from scipy.signal import butter, lfilter, sosfilt
 
 from torch_pesq import BarkScale, Loudness, PesqLoss, _lib
 from torch_pesq import bark as bark_mod
 from torch_pesq import loudness as loud_mod
-from torch_pesq.hip_ops.iir import parallel_sections
+from torch_pesq.hip_ops.iir import HipIIR, parallel_sections, realise
 
 ROOT = Path(__file__).resolve().parents[1]
 TABLES = json.loads((ROOT / "tests" / "golden" / "tables.json").read_text())
@@ -104,6 +104,90 @@ def test_parallel_realisation_rejects_repeated_poles():
     a = np.poly([0.5, 0.5, 0.5])
     with pytest.raises(RuntimeError):
         parallel_sections([1.0], a)
+
+
+@pytest.mark.parametrize(
+    "b,a,basis",
+    [
+        (*butter(5, [325, 3250], fs=16000, btype="band"), "parallel"),
+        (*butter(8, [325, 3250], fs=16000, btype="band"), "cascade"),
+        ([1.0, 0.0, 0.0, 0.0], np.poly([0.7, 0.7, 0.7]), "cascade"),
+        ([1.0, 2.0, 3.0, 4.0, 5.0], [1.0, -0.5, 0.0, 0.0, 0.0], "cascade"),
+        ([1.0, 2.0, 3.0], [1.0, -0.5, 0.0], "cascade"),
+        ([2.740826, -5.4816519, 2.740826], [1.0, -1.9444777, 0.94597794], "cascade"),
+    ],
+)
+def test_realisation_choice_and_fidelity(b, a, basis):
+    """The chosen realisation reproduces the float64 difference equation.
+
+    The parallel form needs distinct poles and no FIR tail; repeated poles
+    (the triple pole), numerators longer than the denominator and order 16
+    band passes (clustered poles) take the cascade, order <= 2 a single full
+    biquad.  The check runs the realisation itself (sums of biquads, or
+    ``sosfilt`` over the sections) on noise against ``lfilter`` of (b, a).
+    """
+
+    real = realise(b, a)
+    assert real.basis == basis
+    x = np.random.default_rng(3).standard_normal(6000)
+    want = lfilter(np.asarray(b, float), np.asarray(a, float), x)
+    if real.basis == "parallel":
+        got = real.c0 * x + sum(lfilter(s[:3], [1.0, s[3], s[4]], x) for s in real.sections)
+    else:
+        got = sosfilt(real.sections, x)
+    err = np.abs(got - want).max() / np.abs(want).max()
+    assert err <= max(10 * real.score, 1e-12), (err, real.score)
+    assert real.score < 1e-6
+
+
+def test_realisation_rating_matches_the_reference_limits():
+    """Order 20 band pass: usable but degraded (warns); order 30: rejected.
+
+    The reference's ``test_degraded_filter_warns`` and
+    ``test_unrepresentable_filter_raises_instead_of_returning_nan``
+    (``test_triton_iir.py:860-884``) with its limits 1e3 and 1e5 times 2^-24.
+    """
+
+    with pytest.warns(RuntimeWarning, match="degraded"):
+        HipIIR(*butter(10, [325, 3250], fs=16000, btype="band"))
+    with pytest.raises(RuntimeError, match="realisation"):
+        HipIIR(*butter(15, [325, 3250], fs=16000, btype="band"))
+
+
+def test_realisation_argument_errors():
+    with pytest.raises(ValueError):
+        realise([1.0, 0.5], [0.0, 1.0])
+    with pytest.raises(ValueError):
+        realise([1.0], [1.0])
+    with pytest.raises(ValueError):
+        HipIIR([1.0, 0.5], [1.0, -0.5], chunk_size=100)
+    with pytest.raises(ValueError):
+        HipIIR([1.0, 0.5], [1.0, -0.5], method="direct")
+    mod = HipIIR(*butter(8, [325, 3250], fs=16000, btype="band"), chunk_size="tune")
+    assert (mod.order, mod.states, mod.sections) == (16, 16, 8)
+    assert mod.candidates == (64, 128, 256, 512)
+
+
+def test_iir_cascade_pack_validates():
+    lib = _lib.library()
+    size = lib.pesq_iir_table_bytes()
+    sos = np.array([[1.0, 0.5, 0.25, 1.0, -0.5, 0.1]] * 2)
+    buf = (ctypes.c_ubyte * (2 * size))()
+    ptr = sos.ctypes.data_as(ctypes.c_void_p)
+    assert lib.pesq_iir_cascade_pack(ptr, 2, buf) == 0
+    assert lib.pesq_iir_cascade_pack(ptr, 0, buf) != 0
+    assert b"sections" in lib.pesq_last_error()
+    assert lib.pesq_iir_cascade_pack(ptr, _lib.MAX_CASCADE + 1, buf) != 0
+    bad = sos.copy()
+    bad[1, 3] = 0.0
+    assert lib.pesq_iir_cascade_pack(bad.ctypes.data_as(ctypes.c_void_p), 2, buf) != 0
+    assert b"leading denominator" in lib.pesq_last_error()
+    out = ctypes.c_size_t(0)
+    assert lib.pesq_iir_cascade_workspace(4, 5000, 3, ctypes.byref(out)) == 0
+    # the scan workspace of one section plus two float64 intermediate signals
+    nblk = -(-5000 // 1024)
+    assert out.value == (4 * nblk * 2 * 65 + 2 * 4 * 5000) * 8
+    assert lib.pesq_iir_cascade_workspace(4, 5000, 0, ctypes.byref(out)) != 0
 
 
 def test_iir_table_pack_validates():

@@ -32,7 +32,12 @@ static void mat_mul(const double *x, const double *y, double *out) {
 // rewritten as the direct term b2 / a2 plus the section
 // (b0 - b2 / a2) + (b1 - a1 b2 / a2) z^-1 over the same denominator, which is
 // the same transfer function.  `direct` accumulates the direct terms.
-static int fill_sections(IirTable &t, int first, const pesq_iir_sections &s, double &direct) {
+// Section coefficients and scan powers of s into table sections first.. of t.
+// With fold_b2 (parallel form) a section's b2 becomes the direct term b2/a2
+// plus a section without z^-2 in its numerator; otherwise b2 is kept (the
+// full biquads of a cascade).
+static int fill_sections(IirTable &t, int first, const pesq_iir_sections &s, double &direct,
+                         bool fold_b2 = true) {
     PESQ_CHECK_ARG(s.count >= 1 && first + s.count <= kMaxSections,
                    "an IIR filter needs 1..%d sections in total, got %d", kMaxSections,
                    first + s.count);
@@ -41,13 +46,13 @@ static int fill_sections(IirTable &t, int first, const pesq_iir_sections &s, dou
         PESQ_CHECK_ARG(std::isfinite(s.b0[k]) && std::isfinite(s.b1[k]) && std::isfinite(s.b2[k]) &&
                            std::isfinite(s.a1[k]) && std::isfinite(s.a2[k]),
                        "non finite IIR coefficient in section %d", k);
-        PESQ_CHECK_ARG(s.b2[k] == 0.0 || s.a2[k] != 0.0,
+        PESQ_CHECK_ARG(!fold_b2 || s.b2[k] == 0.0 || s.a2[k] != 0.0,
                        "section %d has b2 != 0 over a first order denominator (an FIR tail)", k);
-        const double d = s.b2[k] == 0.0 ? 0.0 : s.b2[k] / s.a2[k];
+        const double d = (!fold_b2 || s.b2[k] == 0.0) ? 0.0 : s.b2[k] / s.a2[k];
         direct += d;
         t.b0[q] = s.b0[k] - d;
         t.b1[q] = s.b1[k] - s.a1[k] * d;
-        t.b2[q] = 0.0;
+        t.b2[q] = fold_b2 ? 0.0 : s.b2[k];
         t.a1[q] = s.a1[k];
         t.a2[q] = s.a2[k];
         // chunk transfer powers: level 0 = A^kChunk, level j = A^(kChunk 2^j)
@@ -99,6 +104,31 @@ extern "C" int pesq_iir_table_pack(const pesq_iir_sections *filter, void *out) {
     IirTable t;
     if (int st = pack_iir(t, filter, nullptr)) return st;
     std::memcpy(out, &t, sizeof(t));
+    return PESQ_OK;
+}
+
+extern "C" int pesq_iir_cascade_pack(const double *sos, int sections, void *out) {
+    PESQ_CHECK_ARG(sos != nullptr && out != nullptr, "null argument");
+    PESQ_CHECK_ARG(sections >= 1 && sections <= PESQ_IIR_MAX_CASCADE,
+                   "a cascade has 1..%d sections, got %d", PESQ_IIR_MAX_CASCADE, sections);
+    IirTable *tables = static_cast<IirTable *>(out);
+    for (int k = 0; k < sections; ++k) {
+        const double *row = sos + 6 * k;
+        PESQ_CHECK_ARG(row[3] != 0.0 && std::isfinite(row[3]),
+                       "section %d has a zero leading denominator coefficient", k);
+        pesq_iir_sections one{};
+        one.count = 1;
+        one.b0[0] = row[0] / row[3];
+        one.b1[0] = row[1] / row[3];
+        one.b2[0] = row[2] / row[3];
+        one.a1[0] = row[4] / row[3];
+        one.a2[0] = row[5] / row[3];
+        IirTable t;
+        std::memset(&t, 0, sizeof(t));
+        t.na = 1;
+        if (int st = fill_sections(t, 0, one, t.c0a, false)) return st;
+        std::memcpy(&tables[k], &t, sizeof(t));
+    }
     return PESQ_OK;
 }
 

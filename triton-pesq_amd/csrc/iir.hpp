@@ -53,20 +53,24 @@ static_assert(kSpan == kChunk << kLevelBlock, "a block is 2^6 chunks");
 struct IirTable {
     int32_t na, nb;      // sections of filter A, then of filter B
     double c0a, c0b;     // direct feed through of A and B
-    double b0[kMaxSections], b1[kMaxSections], b2[kMaxSections];  // b2 = 0 (packing)
+    // b2 = 0 in a parallel form table (folded by the packing); kept in the
+    // per section tables of a cascade
+    double b0[kMaxSections], b1[kMaxSections], b2[kMaxSections];
     double a1[kMaxSections], a2[kMaxSections];
     double pw[kLevels][kMaxSections][4];     // A_k^(kChunk 2^j), row major 2x2
     double lane_pw[kMaxSections][kWave][4];  // A_k^(kChunk lane), lane start powers
 };
 
-// Scan workspace of `rows` rows of nblk blocks: the block aggregates
-// [row][section][block][2], then the lane states [row][block][section][lane][2]
-// (sized for kMaxSections sections).
-__host__ __device__ __forceinline__ int64_t scan_aggr_doubles(int64_t rows, int64_t nblk) {
-    return rows * nblk * kMaxSections * 2;
+// Scan workspace of `rows` rows of nblk blocks and `ns` sections: the block
+// aggregates [row][section][block][2], then the lane states
+// [row][block][section][lane][2].
+__host__ __device__ __forceinline__ int64_t scan_aggr_doubles(int64_t rows, int64_t nblk,
+                                                              int ns = kMaxSections) {
+    return rows * nblk * ns * 2;
 }
-__host__ __device__ __forceinline__ int64_t scan_workspace_doubles(int64_t rows, int64_t nblk) {
-    return scan_aggr_doubles(rows, nblk) * (1 + kWave);
+__host__ __device__ __forceinline__ int64_t scan_workspace_doubles(int64_t rows, int64_t nblk,
+                                                                   int ns = kMaxSections) {
+    return scan_aggr_doubles(rows, nblk, ns) * (1 + kWave);
 }
 
 // --------------------------------------------------------------------------
@@ -96,10 +100,12 @@ __device__ __forceinline__ const T *reload(const T *p) {
     return reinterpret_cast<const T *>((uint64_t(hi) << 32) | lo);
 }
 
-// Coefficients of NS sections starting at section S0 (b2 = 0 in the table).
-template <int S0, int NS>
+// Coefficients of NS sections starting at section S0.  With kB2 the sections
+// are full biquads (z2' = b2 x - a2 y_k, the cascade passes); without it b2 is
+// 0 (the parallel form, whose table packing folds b2 into the direct term).
+template <int S0, int NS, bool kB2 = false>
 struct Coeffs {
-    double b0[NS > 0 ? NS : 1], b1[NS > 0 ? NS : 1];
+    double b0[NS > 0 ? NS : 1], b1[NS > 0 ? NS : 1], b2[NS > 0 ? NS : 1];
     double a1[NS > 0 ? NS : 1], a2[NS > 0 ? NS : 1];
     double c0;
 
@@ -108,6 +114,7 @@ struct Coeffs {
         for (int k = 0; k < NS; ++k) {
             b0[k] = t.b0[S0 + k];
             b1[k] = t.b1[S0 + k];
+            b2[k] = kB2 ? t.b2[S0 + k] : 0.0;
             a1[k] = t.a1[S0 + k];
             a2[k] = t.a2[S0 + k];
         }
@@ -121,7 +128,7 @@ struct Coeffs {
         for (int k = 0; k < NS; ++k) {
             const double yk = fma(b0[k], x, s.u[k]);
             s.u[k] = fma(-a1[k], yk, fma(b1[k], x, s.v[k]));
-            s.v[k] = -a2[k] * yk;
+            s.v[k] = kB2 ? fma(b2[k], x, -a2[k] * yk) : -a2[k] * yk;
             y += yk;
         }
         return y;
@@ -188,6 +195,9 @@ struct BankPair {
 // the kernels, parametrised by a Mode policy:
 //   Mode::kInputs                 raw inputs per sample (1 or 2)
 //   Mode::kOutputs                outputs per sample (1 or 2)
+//   Mode::In, Mode::Out           element types of the raw inputs and the
+//                                 outputs in memory (float or double)
+//   Mode::kB2                     full biquad sections (b2 read from the table)
 //   Mode::kReverse                process the time axis back to front
 //   Mode::kAccumulates            the output pass reduces a per block sum
 //   Mode::kRamp                   the Mode uses the edge ramp weight w of the
@@ -217,25 +227,40 @@ __device__ __forceinline__ int64_t chunk_lo(int64_t j0, int64_t len) {
     return kRev ? len - j0 - kChunk : j0;
 }
 
+// 16-byte vector moves of float (4 per vector) and double (2 per vector)
+__device__ __forceinline__ void load16(const float *p, float *dst) {
+    const float4 w = *reinterpret_cast<const float4 *>(p);
+    dst[0] = w.x;
+    dst[1] = w.y;
+    dst[2] = w.z;
+    dst[3] = w.w;
+}
+__device__ __forceinline__ void load16(const double *p, double *dst) {
+    const double2 w = *reinterpret_cast<const double2 *>(p);
+    dst[0] = w.x;
+    dst[1] = w.y;
+}
+__device__ __forceinline__ void store16(float *p, const float *src) {
+    *reinterpret_cast<float4 *>(p) = make_float4(src[0], src[1], src[2], src[3]);
+}
+__device__ __forceinline__ void store16(double *p, const double *src) {
+    *reinterpret_cast<double2 *>(p) = make_double2(src[0], src[1]);
+}
+
 template <class Mode>
 __device__ __forceinline__ void load_chunk(const Mode &m, int row, int64_t j0, int64_t len,
-                                           float (&in)[kChunk][Mode::kInputs]) {
+                                           typename Mode::In (&in)[kChunk][Mode::kInputs]) {
+    using T = typename Mode::In;
+    constexpr int kVec = 16 / sizeof(T);
     const bool full = j0 + kChunk <= len;
     const int64_t lo = chunk_lo<Mode::kReverse>(j0, len);
 #pragma unroll
     for (int q = 0; q < Mode::kInputs; ++q) {
-        const float *base = m.src(row, q);
-        float buf[kChunk];
+        const T *base = m.src(row, q);
+        T buf[kChunk];
         if (full && (reinterpret_cast<uintptr_t>(base + lo) & 15) == 0) {
-            const float4 *p4 = reinterpret_cast<const float4 *>(base + lo);
 #pragma unroll
-            for (int r = 0; r < kChunk / 4; ++r) {
-                const float4 w = p4[r];
-                buf[4 * r] = w.x;
-                buf[4 * r + 1] = w.y;
-                buf[4 * r + 2] = w.z;
-                buf[4 * r + 3] = w.w;
-            }
+            for (int r = 0; r < kChunk / kVec; ++r) load16(base + lo + kVec * r, buf + kVec * r);
 #pragma unroll
             for (int i = 0; i < kChunk; ++i) in[i][q] = buf[Mode::kReverse ? kChunk - 1 - i : i];
         } else {
@@ -243,30 +268,26 @@ __device__ __forceinline__ void load_chunk(const Mode &m, int row, int64_t j0, i
             for (int i = 0; i < kChunk; ++i) {
                 const int64_t j = j0 + i;
                 const int64_t jc = j < len ? j : len - 1;
-                const float v = base[Mode::kReverse ? len - 1 - jc : jc];
-                in[i][q] = j < len ? v : 0.0f;
+                const T v = base[Mode::kReverse ? len - 1 - jc : jc];
+                in[i][q] = j < len ? v : T(0);
             }
         }
     }
 }
 
 // out[i] is stored at time index j0 + i
-__device__ __forceinline__ void store_chunk(float *base, const float (&out)[kChunk], bool kRev,
+template <typename T>
+__device__ __forceinline__ void store_chunk(T *base, const T (&out)[kChunk], bool kRev,
                                             int64_t j0, int64_t len) {
+    constexpr int kVec = 16 / sizeof(T);
     const bool full = j0 + kChunk <= len;
     const int64_t lo = kRev ? len - j0 - kChunk : j0;
     if (full && (reinterpret_cast<uintptr_t>(base + lo) & 15) == 0) {
-        float4 *p4 = reinterpret_cast<float4 *>(base + lo);
+        T e[kChunk];
 #pragma unroll
-        for (int r = 0; r < kChunk / 4; ++r) {
-            float e[4];
+        for (int i = 0; i < kChunk; ++i) e[i] = out[kRev ? kChunk - 1 - i : i];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int i = 4 * r + c;
-                e[c] = out[kRev ? kChunk - 1 - i : i];
-            }
-            p4[r] = make_float4(e[0], e[1], e[2], e[3]);
-        }
+        for (int r = 0; r < kChunk / kVec; ++r) store16(base + lo + kVec * r, e + kVec * r);
     } else {
 #pragma unroll
         for (int i = 0; i < kChunk; ++i) {
@@ -285,7 +306,8 @@ __device__ __forceinline__ bool general_chunk(int64_t j0, int64_t len) {
 
 // filter inputs of element i (time index j0 + i) of a chunk
 template <bool kGeneral, class Mode>
-__device__ __forceinline__ void element_inputs(const Mode &m, const float (&in)[Mode::kInputs],
+__device__ __forceinline__ void element_inputs(const Mode &m,
+                                               const typename Mode::In (&in)[Mode::kInputs],
                                                int64_t j, int64_t len, double &w, double &xa,
                                                double &xb) {
     w = 1.0;
@@ -300,9 +322,10 @@ __device__ __forceinline__ void element_inputs(const Mode &m, const float (&in)[
 
 // zero state run over the lane's chunk
 template <bool kGeneral, int NA, int NB, class Mode>
-__device__ __forceinline__ void zero_run(const Mode &m, const Coeffs<0, NA> &ca,
-                                         const Coeffs<NA, NB> &cb,
-                                         const float (&in)[kChunk][Mode::kInputs], int64_t j0,
+__device__ __forceinline__ void zero_run(const Mode &m, const Coeffs<0, NA, Mode::kB2> &ca,
+                                         const Coeffs<NA, NB, Mode::kB2> &cb,
+                                         const typename Mode::In (&in)[kChunk][Mode::kInputs],
+                                         int64_t j0,
                                          int64_t len, BankPair<NA, NB> &s) {
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) {
@@ -315,11 +338,13 @@ __device__ __forceinline__ void zero_run(const Mode &m, const Coeffs<0, NA> &ca,
 
 // run from the true start state s, outputs into out[][i]
 template <bool kGeneral, int NA, int NB, class Mode>
-__device__ __forceinline__ void output_run(const Mode &m, const Coeffs<0, NA> &ca,
-                                           const Coeffs<NA, NB> &cb,
-                                           const float (&in)[kChunk][Mode::kInputs], int64_t j0,
-                                           int64_t len, const double *sh, BankPair<NA, NB> &s,
-                                           float (&out)[Mode::kOutputs][kChunk], double &acc) {
+__device__ __forceinline__ void output_run(const Mode &m, const Coeffs<0, NA, Mode::kB2> &ca,
+                                           const Coeffs<NA, NB, Mode::kB2> &cb,
+                                           const typename Mode::In (&in)[kChunk][Mode::kInputs],
+                                           int64_t j0, int64_t len, const double *sh,
+                                           BankPair<NA, NB> &s,
+                                           typename Mode::Out (&out)[Mode::kOutputs][kChunk],
+                                           double &acc) {
 #pragma unroll
     for (int i = 0; i < kChunk; ++i) {
         const int64_t j = j0 + i;
@@ -328,7 +353,7 @@ __device__ __forceinline__ void output_run(const Mode &m, const Coeffs<0, NA> &c
         double ya = 0.0, yb = 0.0;
         if constexpr (NA > 0) ya = ca.step(s.a, xa);
         if constexpr (NB > 0) yb = cb.step(s.b, xb);
-        float o[Mode::kOutputs];
+        typename Mode::Out o[Mode::kOutputs];
         const double before = acc;
         m.compute(w, ya, yb, acc, sh, o);
         if constexpr (kGeneral) {
@@ -336,7 +361,7 @@ __device__ __forceinline__ void output_run(const Mode &m, const Coeffs<0, NA> &c
         }
 #pragma unroll
         for (int q = 0; q < Mode::kOutputs; ++q) {
-            out[q][i] = (!kGeneral || j < len) ? o[q] : 0.0f;
+            out[q][i] = (!kGeneral || j < len) ? o[q] : typename Mode::Out(0);
         }
     }
 }
@@ -351,12 +376,12 @@ __global__ void __launch_bounds__(kWave)
     const int blk = blockIdx.x - row * nblk;
     const int lane = threadIdx.x;
     const int64_t j0 = int64_t(blk) * kSpan + int64_t(lane) * kChunk;
-    Coeffs<0, NA> ca;
-    Coeffs<NA, NB> cb;
+    Coeffs<0, NA, Mode::kB2> ca;
+    Coeffs<NA, NB, Mode::kB2> cb;
     ca.load(t, t.c0a);
     cb.load(t, t.c0b);
 
-    float in[kChunk][Mode::kInputs];
+    typename Mode::In in[kChunk][Mode::kInputs];
     load_chunk(m, row, j0, len, in);
 
     BankPair<NA, NB> s;
@@ -469,7 +494,7 @@ __global__ void __launch_bounds__(kWave)
     }
     double sh[4];
     m.setup(row, sh, lane);
-    float in[kChunk][Mode::kInputs];
+    typename Mode::In in[kChunk][Mode::kInputs];
     load_chunk(m, row, j0, len, in);
 
     // lane start state = (start state given a zero block start) + A^(kChunk lane) p
@@ -483,11 +508,11 @@ __global__ void __launch_bounds__(kWave)
     }
 
     // run from the true start state
-    Coeffs<0, NA> ca;
-    Coeffs<NA, NB> cb;
+    Coeffs<0, NA, Mode::kB2> ca;
+    Coeffs<NA, NB, Mode::kB2> cb;
     ca.load(t2, t2.c0a);
     cb.load(t2, t2.c0b);
-    float out[Mode::kOutputs][kChunk];
+    typename Mode::Out out[Mode::kOutputs][kChunk];
     double acc = 0.0;
     if (general_chunk(j0, len)) {
         output_run<true>(m, ca, cb, in, j0, len, sh, s, out, acc);
@@ -496,7 +521,7 @@ __global__ void __launch_bounds__(kWave)
     }
 #pragma unroll
     for (int q = 0; q < Mode::kOutputs; ++q) {
-        float *dst = m.dst(row, q);
+        typename Mode::Out *dst = m.dst(row, q);
         if (dst != nullptr) store_chunk(dst, out[q], Mode::kReverse, j0, len);
     }
 
@@ -507,7 +532,7 @@ __global__ void __launch_bounds__(kWave)
 }
 
 // Host side: aggregate, prefix and output launches of one scan pass over
-// `rows` rows; `ws` holds scan_workspace_doubles(rows, nblk).
+// `rows` rows; `ws` holds scan_workspace_doubles(rows, nblk, NA + NB).
 template <int NA, int NB, class Mode>
 int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, int64_t len,
                 bool aggregate, bool output, hipStream_t stream) {
@@ -515,7 +540,7 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
     static_assert(NS <= kMaxSections, "too many sections");
     const int64_t nblk = cdiv(len, kBlockSpan);
     double *aggr = ws;
-    double *lanes = ws + scan_aggr_doubles(rows, nblk);
+    double *lanes = ws + scan_aggr_doubles(rows, nblk, NS);
     const unsigned grid = static_cast<unsigned>(rows * nblk);
     if (grid == 0) return PESQ_OK;
     if (aggregate) {

@@ -48,6 +48,9 @@ struct PipeFwdMode {
     static constexpr bool kRamp = true;
     static constexpr bool kReverse = false;
     static constexpr bool kAccumulates = true;
+    static constexpr bool kB2 = false;
+    using In = float;
+    using Out = float;
 
     const float *ref, *deg;
     float *p, *f;             // outputs; f may be null
@@ -88,6 +91,9 @@ struct PipeBwdMode {
     static constexpr bool kRamp = true;
     static constexpr bool kReverse = true;
     static constexpr bool kAccumulates = false;
+    static constexpr bool kB2 = false;
+    using In = float;
+    using Out = float;
 
     const float *f, *gp;      // [nrg, len] each
     const double *rowconst;   // [rows, 4]: -, E, scale, -

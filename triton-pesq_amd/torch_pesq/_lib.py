@@ -24,6 +24,7 @@ __all__ = [
 ]
 
 MAX_SECTIONS = 8
+MAX_CASCADE = 32
 NBARKS = 49
 NFFT = 512
 GRAD_REF = 1
@@ -82,6 +83,7 @@ SIGNATURES = {
     "pesq_last_error": (ctypes.c_char_p, []),
     "pesq_iir_table_bytes": (ctypes.c_size_t, []),
     "pesq_iir_table_pack": (_INT, [ctypes.POINTER(IirSections), _P]),
+    "pesq_iir_cascade_pack": (_INT, [_P, _INT, _P]),
     "pesq_model_table_bytes": (ctypes.c_size_t, []),
     "pesq_model_table_pack": (_INT, [ctypes.POINTER(ModelConstants), _P]),
     "pesq_pipeline_forward_workspace": (_INT, [_I64, _I64, _INT, _SIZE_P]),
@@ -105,6 +107,8 @@ SIGNATURES = {
     ),
     "pesq_iir_workspace": (_INT, [_I64, _I64, _SIZE_P]),
     "pesq_iir_apply": (_INT, [_P, _P, _I64, _I64, _P, _INT, _INT, _P, _P]),
+    "pesq_iir_cascade_workspace": (_INT, [_I64, _I64, _INT, _SIZE_P]),
+    "pesq_iir_cascade_apply": (_INT, [_P, _P, _I64, _I64, _P, _INT, _INT, _P, _P]),
     "pesq_stft_bark_forward": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P]),
     "pesq_stft_bark_backward": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P, _P]),
     "pesq_chain_forward_workspace": (_INT, [_I64, _I64, _SIZE_P]),
