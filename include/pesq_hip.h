@@ -242,6 +242,39 @@ int pesq_stft_bark_backward(const float *g_bark, const float *x, int64_t rows, i
                             int64_t n_padded, const void *model_table, float *g_x,
                             hipStream_t stream);
 
+/* General geometry (TritonStftBark with any n_fft / hop_length / filterbank,
+ * spectral.py:584-774): n_fft a power of two in [32, 1024], hop >= 1, 1..128
+ * bands.  Frames t < 1 + (n_padded - n_fft) / hop start at t * hop. */
+
+/* Size in bytes of a packed general STFT table. */
+size_t pesq_stft_table_bytes(void);
+
+/* Pack the general STFT constants into `out` (host memory,
+ * pesq_stft_table_bytes() bytes): window [n_fft] (already centred), bands
+ * [band_start[i], band_end[i]) over bins 0 .. n_fft / 2 - 1 (sorted, disjoint),
+ * corr [nbarks].  Replaces bark_segments / _twiddles (spectral.py:138-224). */
+int pesq_stft_table_pack(int n_fft, int hop, const float *window, int nbarks,
+                         const int32_t *band_start, const int32_t *band_end,
+                         const double *corr, void *out);
+
+/* Scratch of pesq_stft_backward: [rows, frames, n_fft] float32. */
+int pesq_stft_workspace(int64_t rows, int64_t len, int64_t n_padded, int n_fft, int hop,
+                        size_t *bytes);
+
+/* bark [rows, frames, nbarks] of x [rows, len] (zero beyond len), as
+ * pesq_stft_bark_forward for the general geometry (_fwd_kernel,
+ * spectral.py:229-332). */
+int pesq_stft_forward(const float *x, int64_t rows, int64_t len, int64_t n_padded,
+                      const void *stft_table, int n_fft, int hop, int nbarks, float *bark,
+                      hipStream_t stream);
+
+/* g_x [rows, len] from g_bark, the vector-Jacobian product of
+ * pesq_stft_forward (_bwd_frame_kernel + _bwd_gather_kernel,
+ * spectral.py:334-440); samples no frame covers get zero. */
+int pesq_stft_backward(const float *g_bark, const float *x, int64_t rows, int64_t len,
+                       int64_t n_padded, const void *stft_table, int n_fft, int hop,
+                       int nbarks, float *g_x, void *workspace, hipStream_t stream);
+
 /* ----------------------------------------------------------------------- */
 /* perceptual chain (TritonPesqChain, torch_pesq/triton_ops/chain.py:1024-1126) */
 /* ----------------------------------------------------------------------- */

@@ -71,6 +71,62 @@ def _interp(values, nelms_new):
     return torch.tensor(curve(np.linspace(0, 49.0, nelms_new, endpoint=False)))
 
 
+def bark_fbank(nfreqs: int = 256, nbarks: int = 49) -> torch.Tensor:
+    """Binary Bark filterbank ``[nbarks, nfreqs]`` (``torch_pesq/bark.py:140-165``).
+
+    The default geometry uses the standard's bin counts per band; any other
+    one places band ``i`` at its interpolated centre with its interpolated
+    width (bins of 8000 / nfreqs Hz), clipped to start after the previous band.
+    """
+
+    fbank = torch.zeros(nbarks, nfreqs, dtype=torch.float64)
+    if nfreqs == 256 and nbarks == 49:
+        edges = np.concatenate([[0], np.cumsum(TABLES["nr_of_hz_bands_per_bark_band_16k"])])
+        for band in range(nbarks):
+            fbank[band, int(edges[band]) : int(edges[band + 1])] = 1.0
+        return fbank
+    width_hz = _interp(TABLES["width_of_band_hz_16k"], nbarks)
+    centre_hz = _interp(TABLES["centre_of_band_hz_16k"], nbarks)
+    prev, bin_width = 0, 8000.0 / nfreqs
+    for band in range(nbarks):
+        stride = float(width_hz[band]) / bin_width
+        centre = float(centre_hz[band]) / bin_width
+        start = max(prev, int(math.floor(centre - stride / 2)))
+        end = min(nfreqs, int(math.ceil(centre + stride / 2)))
+        fbank[band, start:end] = 1.0
+        prev = end
+    return fbank
+
+
+def stft_bark_op(signal, window, fbank, corr, n_fft: int, hop: int, n_padded: int = None):
+    """The stand-alone STFT / Bark operator in float64 (``reference.py:79-127``).
+
+    ``signal`` ``[rows, N]`` is zero padded to ``n_padded``; frames
+    ``t < 1 + (n_padded - n_fft) // hop`` start at ``t hop``; ``window`` has at
+    most ``n_fft`` taps and is centred like ``torch.stft`` does; DC dropped,
+    bins ``0 .. n_fft / 2 - 1`` summed per band and scaled by ``corr``.
+    """
+
+    signal = signal.double()
+    n_padded = signal.shape[1] if n_padded is None else n_padded
+    signal = torch.nn.functional.pad(signal, (0, n_padded - signal.shape[1]))
+    window = torch.as_tensor(window).double()
+    spec = torch.stft(
+        signal,
+        n_fft=n_fft,
+        hop_length=hop,
+        win_length=window.shape[0],
+        window=window,
+        center=False,
+        normalized=False,
+        return_complex=True,
+    )
+    spec = spec.abs().pow(2).swapaxes(1, 2)
+    spec = torch.cat([torch.zeros_like(spec[:, :, :1]), spec[:, :, 1:]], dim=2)
+    bark = torch.matmul(spec[:, :, :-1], torch.as_tensor(fbank).double().t())
+    return bark * torch.as_tensor(corr).double().reshape(-1)
+
+
 @lru_cache(maxsize=None)
 def constants(nbarks: int = 49, n_fft: int = 512):
     """All constants of the pipeline as float64 tensors.

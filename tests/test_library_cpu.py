@@ -190,6 +190,49 @@ def test_iir_cascade_pack_validates():
     assert lib.pesq_iir_cascade_workspace(4, 5000, 0, ctypes.byref(out)) != 0
 
 
+def test_stft_construction_validation():
+    """The constructor checks of ``test_triton_spectral.py:200-260``, same messages."""
+
+    from torch_pesq.hip_ops.spectral import HipStftBark
+
+    window = torch.hann_window(64)
+    corr = torch.ones(4)
+    overlapping = torch.zeros(4, 32)
+    overlapping[0, 0:8] = 1.0
+    overlapping[1, 4:12] = 1.0
+    with pytest.raises(ValueError, match="disjoint"):
+        HipStftBark(window, overlapping, corr, 64, 32)
+    gappy = torch.zeros(4, 32)
+    gappy[0, 0] = gappy[0, 5] = 1.0
+    with pytest.raises(ValueError, match="not contiguous"):
+        HipStftBark(window, gappy, corr, 64, 32)
+    weighted = torch.zeros(4, 32)
+    weighted[0, 0:4] = 0.5
+    with pytest.raises(ValueError, match="binary"):
+        HipStftBark(window, weighted, corr, 64, 32)
+    fine = torch.zeros(4, 32)
+    fine[0, 0:4] = 1.0
+    with pytest.raises(ValueError, match="at least 32"):
+        HipStftBark(window[:16], fine[:, :8], corr, 16, 8)
+    with pytest.raises(ValueError, match="512 bins"):
+        HipStftBark(window, fine, corr, 1024, 32)
+    with pytest.raises(ValueError, match="one entry per band"):
+        HipStftBark(window, fine, corr[:2], 64, 32)
+    with pytest.raises(ValueError, match="at most 64 taps"):
+        HipStftBark(torch.hann_window(128), fine, corr, 64, 32)
+    for n_fft in (40, 48, 96, 1000):
+        fb = torch.zeros(4, n_fft // 2)
+        for band in range(4):
+            fb[band, 4 * band : 4 * band + 4] = 1.0
+        with pytest.raises(ValueError, match="power of two"):
+            HipStftBark(torch.hann_window(n_fft), fb, torch.ones(4), n_fft, n_fft // 2)
+    # accepted: the general kernels for anything but the PESQ geometry
+    mod = HipStftBark(window, fine, corr, 64, 32)
+    assert mod.general and mod.novertaps == 2
+    scale = BarkScale(256, 49)
+    assert not HipStftBark(torch.hann_window(512), scale.fbank, scale.pow_dens_correction).general
+
+
 def test_iir_table_pack_validates():
     lib = _lib.library()
     s = _lib.IirSections()
@@ -236,8 +279,12 @@ def test_cpu_inputs_and_bad_shapes_raise():
         m(ref, ref)
     with pytest.raises(ValueError):
         m(ref, torch.zeros(2, 15000))
-    with pytest.raises(NotImplementedError):
+    # the loudness exponents keep the standard's 49 bands, so other band
+    # counts are refused by the chain, as in the reference
+    with pytest.raises(ValueError, match="same number of bands"):
         PesqLoss(1.0, nbarks=32)
+    # other STFT geometries are accepted (general kernels)
+    assert PesqLoss(1.0, sample_rate=16000, n_fft=256, win_length=200, hop_length=128).general
 
 
 def test_graft_entry_exposes_build_and_smoke():

@@ -113,6 +113,62 @@ def test_stft_bark_matches_direct_dft():
     assert torch.all(got[:, :, 0] == 0)
 
 
+@pytest.mark.parametrize(
+    "n_fft,hop,win,nbarks,n,n_padded",
+    [(256, 100, 256, 32, 1500, 1600), (512, 600, 401, 49, 3000, 3000), (64, 7, 33, 17, 300, 330)],
+)
+def test_stft_bark_op_matches_direct_dft(n_fft, hop, win, nbarks, n, n_padded):
+    """The general operator: any hop, short centred windows, zero padding.
+
+    A direct float64 DFT of every frame (window zero padded to n_fft,
+    ``(n_fft - win) // 2`` zeros in front, the ``torch.stft`` rule), DC
+    dropped, bins below n_fft / 2 summed per band.  A window that is not
+    centred, a wrong hop or a frame count off by one fails it.
+    """
+
+    rng = np.random.default_rng(n_fft + hop)
+    x = torch.from_numpy(rng.standard_normal((2, n)))
+    window = torch.hann_window(win, dtype=torch.float64)
+    fbank = O.bark_fbank(n_fft // 2, nbarks)
+    corr = torch.from_numpy(rng.uniform(0.5, 2.0, nbarks))
+    got = O.stft_bark_op(x, window, fbank, corr, n_fft, hop, n_padded)
+    full = np.zeros(n_fft)
+    left = (n_fft - win) // 2
+    full[left : left + win] = window.numpy()
+    xp = np.pad(x.numpy(), ((0, 0), (0, n_padded - n)))
+    frames = 1 + (n_padded - n_fft) // hop
+    k = np.arange(n_fft)
+    basis = np.exp(-2j * np.pi * np.outer(k, np.arange(n_fft // 2)) / n_fft)
+    power = np.stack([np.abs((xp[:, hop * t : hop * t + n_fft] * full) @ basis) ** 2 for t in range(frames)], 1)
+    power[:, :, 0] = 0.0
+    want = power @ fbank.numpy().T * corr.numpy()
+    assert got.shape == (2, frames, nbarks)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-10, atol=1e-12 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("nfreqs", [256, 128, 512, 32])
+@pytest.mark.parametrize("nbarks", [49, 32, 17])
+def test_bark_fbank_is_a_segmentation(nfreqs, nbarks):
+    """``test_triton_spectral.py:176-197``: binary, contiguous, sorted, disjoint.
+
+    At the default geometry the bands are the standard's bin counts.
+    """
+
+    fb = O.bark_fbank(nfreqs, nbarks)
+    assert torch.all((fb == 0) | (fb == 1))
+    prev = 0
+    for band in range(nbarks):
+        nz = torch.nonzero(fb[band]).flatten()
+        if nz.numel() == 0:
+            continue
+        start, end = int(nz[0]), int(nz[-1]) + 1
+        assert end - start == nz.numel() and start >= prev and end <= nfreqs
+        prev = end
+    if (nfreqs, nbarks) == (256, 49):
+        counts = fb.sum(1).numpy().astype(int).tolist()
+        assert counts == TABLES["nr_of_hz_bands_per_bark_band_16k"]
+
+
 def test_stft_bark_gradient_finite_difference():
     c = O.constants()
     x = torch.randn(1, 768, dtype=torch.float64, generator=torch.Generator().manual_seed(3))

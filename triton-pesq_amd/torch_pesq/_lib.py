@@ -111,6 +111,11 @@ SIGNATURES = {
     "pesq_iir_cascade_apply": (_INT, [_P, _P, _I64, _I64, _P, _INT, _INT, _P, _P]),
     "pesq_stft_bark_forward": (_INT, [_P, _I64, _I64, _I64, _P, _P, _P]),
     "pesq_stft_bark_backward": (_INT, [_P, _P, _I64, _I64, _I64, _P, _P, _P]),
+    "pesq_stft_table_bytes": (ctypes.c_size_t, []),
+    "pesq_stft_table_pack": (_INT, [_INT, _INT, _P, _INT, _P, _P, _P, _P]),
+    "pesq_stft_workspace": (_INT, [_I64, _I64, _I64, _INT, _INT, _SIZE_P]),
+    "pesq_stft_forward": (_INT, [_P, _I64, _I64, _I64, _P, _INT, _INT, _INT, _P, _P]),
+    "pesq_stft_backward": (_INT, [_P, _P, _I64, _I64, _I64, _P, _INT, _INT, _INT, _P, _P, _P]),
     "pesq_chain_forward_workspace": (_INT, [_I64, _I64, _SIZE_P]),
     "pesq_chain_backward_workspace": (_INT, [_I64, _I64, _SIZE_P]),
     "pesq_chain_forward": (_INT, [_P, _P, _I64, _I64, _P, _P, _P, _P, _P]),

@@ -1,12 +1,20 @@
 """HIP STFT + Bark operator (``TritonStftBark``, ``torch_pesq/triton_ops/spectral.py:584-774``).
 
-Forward: per frame a 512 point real FFT (wavefront-per-frame radix-4 Stockham
-FFT256 in LDS, float64 arithmetic), |X|^2 with the DC bin dropped, Bark band
-sums times the power density correction.  Backward: spectra recomputed, the
-adjoint through an inverse FFT of ``gP X``, overlap-add gather (no atomics).
-Only the PESQ geometry (``n_fft = 512``, ``hop_length = 256``, 49 bands of a
-binary, contiguous filterbank) is supported.
+Forward: per frame a real FFT of the windowed frame in float64, |X|^2 with
+the DC bin dropped, Bark band sums times the power density correction.
+Backward: spectra recomputed, the adjoint through an inverse FFT of
+``gP X``, overlap-add gather (no atomics).
+
+Two kernel families serve it: the PESQ geometry (``n_fft = 512``,
+``hop_length = 256``, 49 bands of at most 25 bins) runs the specialised
+radix-4 kernels of ``csrc/pipeline.hip``; every other geometry, i.e.
+``n_fft`` a power of two in [32, 1024], any ``hop_length`` (also longer than
+``n_fft``, where uncovered samples get a zero gradient), windows shorter than
+``n_fft`` (centred like ``torch.stft``) and up to 128 bands, runs the general
+radix-2 kernels of ``csrc/stft_generic.hip``.
 """
+
+import ctypes
 
 import numpy as np
 import torch
@@ -41,10 +49,31 @@ def bark_segments(fbank: torch.Tensor):
         if end - start != nz.size:
             raise ValueError(f"Band {band} of the filterbank is not contiguous.")
         if start < prev:
-            raise ValueError(f"Band {band} starts at bin {start} but the previous band ends at {prev}.")
+            raise ValueError(
+                f"Band {band} starts at bin {start} but the previous band ends at {prev}; "
+                "the bands have to be disjoint and sorted."
+            )
         starts[band], ends[band] = start, end
         prev = end
     return starts, ends
+
+
+def _general_table(window, starts, ends, corr, n_fft, hop) -> torch.Tensor:
+    lib = _lib.library()
+    win = np.ascontiguousarray(window.detach().cpu().numpy(), dtype=np.float32)
+    lo = np.ascontiguousarray(starts, dtype=np.int32)
+    hi = np.ascontiguousarray(ends, dtype=np.int32)
+    cor = np.ascontiguousarray(corr.detach().cpu().double().numpy(), dtype=np.float64)
+    buf = (ctypes.c_ubyte * lib.pesq_stft_table_bytes())()
+    _lib.check(
+        lib.pesq_stft_table_pack(
+            n_fft, hop, win.ctypes.data_as(ctypes.c_void_p), lo.shape[0],
+            lo.ctypes.data_as(ctypes.c_void_p), hi.ctypes.data_as(ctypes.c_void_p),
+            cor.ctypes.data_as(ctypes.c_void_p), buf,
+        ),
+        "pesq_stft_table_pack",
+    )
+    return torch.frombuffer(bytearray(buf), dtype=torch.uint8).clone()
 
 
 class _StftBarkFunction(torch.autograd.Function):
@@ -54,13 +83,18 @@ class _StftBarkFunction(torch.autograd.Function):
         frames = 1 + (n_padded - module.n_fft) // module.hop_length
         out = torch.empty((rows, frames, module.nbarks), device=signal.device)
         lib = _lib.library()
+        stream = _lib.stream_handle(signal.device)
         with torch.cuda.device(signal.device):
-            _lib.check(
-                lib.pesq_stft_bark_forward(_lib.ptr(signal), rows, length, n_padded,
-                                           _lib.ptr(module.table), _lib.ptr(out),
-                                           _lib.stream_handle(signal.device)),
-                "pesq_stft_bark_forward",
-            )
+            if module.general:
+                status = lib.pesq_stft_forward(
+                    _lib.ptr(signal), rows, length, n_padded, _lib.ptr(module.table),
+                    module.n_fft, module.hop_length, module.nbarks, _lib.ptr(out), stream)
+                _lib.check(status, "pesq_stft_forward")
+            else:
+                status = lib.pesq_stft_bark_forward(
+                    _lib.ptr(signal), rows, length, n_padded, _lib.ptr(module.table),
+                    _lib.ptr(out), stream)
+                _lib.check(status, "pesq_stft_bark_forward")
         ctx.save_for_backward(signal)
         ctx.module, ctx.n_padded = module, n_padded
         return out
@@ -71,18 +105,34 @@ class _StftBarkFunction(torch.autograd.Function):
         (signal,) = ctx.saved_tensors
         if not ctx.needs_input_grad[0]:
             return None, None, None
+        module = ctx.module
         grad = grad.contiguous().float()
         rows, length = signal.shape
         g_x = torch.empty_like(signal)
         lib = _lib.library()
+        stream = _lib.stream_handle(signal.device)
         with torch.cuda.device(signal.device):
-            _lib.check(
-                lib.pesq_stft_bark_backward(_lib.ptr(grad), _lib.ptr(signal), rows, length,
-                                            ctx.n_padded, _lib.ptr(ctx.module.table), _lib.ptr(g_x),
-                                            _lib.stream_handle(signal.device)),
-                "pesq_stft_bark_backward",
-            )
+            if module.general:
+                size = _lib.size_query(lib.pesq_stft_workspace, rows, length, ctx.n_padded,
+                                       module.n_fft, module.hop_length)
+                scratch = torch.empty(max(size, 4), dtype=torch.uint8, device=signal.device)
+                status = lib.pesq_stft_backward(
+                    _lib.ptr(grad), _lib.ptr(signal), rows, length, ctx.n_padded,
+                    _lib.ptr(module.table), module.n_fft, module.hop_length, module.nbarks,
+                    _lib.ptr(g_x), _lib.ptr(scratch), stream)
+                _lib.check(status, "pesq_stft_backward")
+            else:
+                status = lib.pesq_stft_bark_backward(
+                    _lib.ptr(grad), _lib.ptr(signal), rows, length, ctx.n_padded,
+                    _lib.ptr(module.table), _lib.ptr(g_x), stream)
+                _lib.check(status, "pesq_stft_bark_backward")
         return g_x, None, None
+
+
+#: geometry of the specialised kernels
+_PESQ_GEOMETRY = (512, 256, _lib.NBARKS)
+_MAX_BAND_BINS = 25
+_MAX_BANDS = 128
 
 
 class HipStftBark(torch.nn.Module):
@@ -91,32 +141,60 @@ class HipStftBark(torch.nn.Module):
     Numerically ``torch.stft(center=False)``, ``|X|**2``, DC bin dropped, a
     contraction with the binary Bark filterbank over bins ``0 .. n_fft/2 - 1``
     and the power density correction (``reference.py:79-127``), evaluated
-    with a float64 FFT and returned in float32.
+    with a float64 FFT and returned in float32.  Same constructor and
+    validation as ``TritonStftBark`` (``spectral.py:584-700``).
+
+    Attributes
+    ----------
+    general : bool
+        The configuration runs the general kernels (anything but the PESQ
+        geometry)
+    novertaps : int
+        Frames a sample belongs to at most, ``ceil(n_fft / hop_length)``
     """
 
     def __init__(self, window, fbank, pow_dens_correction, n_fft: int = 512, hop_length: int = 256):
         super().__init__()
-        if n_fft != 512 or hop_length != 256:
-            raise ValueError(
-                f"The HIP spectral op supports n_fft=512 and hop_length=256, got {n_fft} and {hop_length}."
-            )
+        n_fft, hop_length = int(n_fft), int(hop_length)
+        if n_fft < 32:
+            raise ValueError(f"`n_fft` has to be at least 32, got {n_fft}.")
+        half = n_fft // 2
+        if n_fft % 2 or half & (half - 1):
+            raise ValueError(f"`n_fft // 2` has to be a power of two, got n_fft = {n_fft}.")
+        if n_fft > 1024:
+            raise ValueError(f"`n_fft` can be at most 1024 (512 bins), got {n_fft}.")
+        if hop_length < 1:
+            raise ValueError(f"`hop_length` has to be positive, got {hop_length}.")
         if window.ndim != 1 or window.shape[0] > n_fft:
-            raise ValueError(f"The window has to be 1d with at most {n_fft} taps, got {tuple(window.shape)}.")
-        if fbank.shape[1] != n_fft // 2:
-            raise ValueError(f"The filterbank needs {n_fft // 2} bins, got {fbank.shape[1]}.")
-        if pow_dens_correction.shape[0] != fbank.shape[0]:
+            raise ValueError(
+                f"The window has to be 1d with at most {n_fft} taps, got {tuple(window.shape)}."
+            )
+        if fbank.ndim != 2 or fbank.shape[1] != half:
+            raise ValueError(
+                f"The filterbank needs n_fft // 2 = {half} bins, got {tuple(fbank.shape)}."
+            )
+        if pow_dens_correction.reshape(-1).shape[0] != fbank.shape[0]:
             raise ValueError("The power density correction needs one entry per band.")
-        if fbank.shape[0] != _lib.NBARKS:
-            raise ValueError(f"The HIP spectral op needs {_lib.NBARKS} bands, got {fbank.shape[0]}.")
+        if fbank.shape[0] > _MAX_BANDS:
+            raise ValueError(f"At most {_MAX_BANDS} bands are supported, got {fbank.shape[0]}.")
         self.starts, self.ends = bark_segments(fbank)
         self.n_fft, self.hop_length, self.nbarks = n_fft, hop_length, fbank.shape[0]
+        self.novertaps = -(-n_fft // hop_length)
         full = torch.zeros(n_fft)
         left = (n_fft - window.shape[0]) // 2
         full[left : left + window.shape[0]] = window.detach().cpu().float()
-        ones = torch.ones(_lib.NBARKS, dtype=torch.float64)
-        table = pack_model_table(None, None, None, None, full, fbank, pow_dens_correction,
-                                 ones, ones, ones, 1.0, 0.0)
+        corr = pow_dens_correction.reshape(-1)
+        self.general = (n_fft, hop_length, self.nbarks) != _PESQ_GEOMETRY or bool(
+            np.any(self.ends - self.starts > _MAX_BAND_BINS)
+        )
+        if self.general:
+            table = _general_table(full, self.starts, self.ends, corr, n_fft, hop_length)
+        else:
+            ones = torch.ones(_lib.NBARKS, dtype=torch.float64)
+            table = pack_model_table(None, None, None, None, full, fbank, corr,
+                                     ones, ones, ones, 1.0, 0.0)
         self.register_buffer("window", full)
+        self.register_buffer("correction", corr.detach().clone().float())
         self.register_buffer("table", table, persistent=False)
 
     def forward(self, signal: torch.Tensor, n_padded: int = None) -> torch.Tensor:

@@ -7,9 +7,12 @@ reference ``torch_pesq/loss.py:20-322`` (``raw``, ``mos``, ``forward``,
 the GPU through ``libpesq_hip.so``; CPU tensors are rejected with a
 ``RuntimeError``.
 
-``raw``/``mos``/``forward`` go through the fused pipeline (five kernels
-forward, four backward, see ``csrc/pipeline.hip``); ``align_level`` and
-``preemphasize`` are the stand-alone per stage operators.
+``raw``/``mos``/``forward`` go through the fused pipeline (``csrc/pipeline.hip``)
+at the PESQ geometry (49 bands, ``n_fft = win_length = 512``,
+``hop_length = 256``).  Other STFT geometries (``n_fft``, ``win_length``,
+``hop_length``) run the reference's stage sequence (``triton_ops/loss.py:104-147``)
+on the stand-alone operators, with the general STFT kernels.  ``align_level``
+and ``preemphasize`` are the stand-alone per stage operators.
 """
 
 import numpy as np
@@ -57,8 +60,11 @@ class PesqLoss(torch.nn.Module):
     sample_rate : int
         Sampling rate of the inputs; other rates than 16 kHz are resampled
     nbarks, win_length, n_fft, hop_length : int
-        Bark bands and STFT geometry; the HIP pipeline supports the PESQ
-        defaults 49 / 512 / 512 / 256
+        Bark bands and STFT geometry.  The loudness exponents are the
+        standard's 49 values (``loudness.py:44-55`` does not interpolate them),
+        so ``nbarks != 49`` raises ``ValueError`` like the reference's chain
+        does; ``n_fft`` (a power of two in [32, 1024]), ``win_length <=
+        n_fft`` and ``hop_length`` are free.
     """
 
     factor: float
@@ -74,15 +80,11 @@ class PesqLoss(torch.nn.Module):
     ):
         super().__init__()
 
-        if (nbarks, win_length, n_fft, hop_length) != (49, 512, 512, 256):
-            raise NotImplementedError(
-                "The HIP PESQ pipeline supports nbarks=49, win_length=n_fft=512 and "
-                f"hop_length=256, got {(nbarks, win_length, n_fft, hop_length)}."
-            )
-
+        from .hip_ops.chain import HipPesqChain
         from .hip_ops.iir import HipIIR
         from .hip_ops.pipeline import pack_model_table
         from .hip_ops.resample import HipResample
+        from .hip_ops.spectral import HipStftBark
 
         self.factor = factor
         self.source_sample_rate = int(sample_rate)
@@ -105,6 +107,26 @@ class PesqLoss(torch.nn.Module):
         # stand-alone per stage operators (align_level / preemphasize)
         self.power_iir = HipIIR(self.power_filter[0], self.power_filter[1])
         self.pre_iir = HipIIR(self.pre_filter[0], self.pre_filter[1])
+
+        # the per stage operators of the general geometry (triton_ops/loss.py:75-92)
+        self.general = (nbarks, win_length, n_fft, hop_length) != (49, 512, 512, 256)
+        self.spectral = HipStftBark(
+            self.to_spec.window,
+            self.fbank.fbank,
+            self.fbank.pow_dens_correction,
+            n_fft,
+            hop_length,
+        )
+        self.chain = HipPesqChain(
+            self.loudness.threshs.flatten(),
+            self.loudness.exp.flatten(),
+            self.fbank.width_bark,
+            float(self.fbank.total_width),
+            SL,
+        )
+        if self.general:
+            self.register_buffer("model_table", self.spectral.table, persistent=False)
+            return
 
         table = pack_model_table(
             self.power_filter[0],
@@ -160,6 +182,9 @@ class PesqLoss(torch.nn.Module):
                 f"{ref.device}; move it with `.to(...)` first."
             )
 
+        if self.general:
+            return self._run_stages(ref, deg)
+
         if self.source_sample_rate != 16000:
             ref, deg = self.resampler(ref), self.resampler(deg)
 
@@ -181,6 +206,45 @@ class PesqLoss(torch.nn.Module):
                 "that requires a gradient would receive none."
             )
         return PipelineFunction.apply(ref, deg, self.model_table, float(self.factor))
+
+    def _run_stages(self, ref: torch.Tensor, deg: torch.Tensor):
+        """The stage sequence of ``PesqLossTriton.raw`` (``triton_ops/loss.py:104-147``).
+
+        Both signals share one peak and are stacked into one batch of twice
+        the size; resampling, level alignment, pre-emphasis, the ``N % 256``
+        padding, the STFT / Bark operator, the chain and the epilogue follow.
+        """
+
+        from .hip_ops.elementwise import peak_normalize, pesq_epilogue
+
+        if isinstance(self.factor, torch.Tensor) and self.factor.requires_grad:
+            raise RuntimeError(
+                "The loss treats `factor` as a constant, pass a Python float. A tensor "
+                "that requires a gradient would receive none."
+            )
+        batch = ref.shape[0]
+        signal = peak_normalize(ref, deg, stack=True)
+        if self.source_sample_rate != 16000:
+            signal = self.resampler(signal)
+        length = signal.shape[1]
+        if length < 15:
+            raise RuntimeError(
+                f"The edge ramp needs at least 15 samples at 16 kHz, got {length}."
+            )
+        padded = length + length % 256
+        n_fft, hop = self.to_spec.n_fft, self.to_spec.hop_length
+        frames = 1 + (padded - n_fft) // hop if padded >= n_fft else 0
+        if frames < 20:
+            raise ValueError(
+                "The PESQ chain needs at least 20 frames for the overlapping sums, "
+                f"got {frames}."
+            )
+        signal = self.align_level(signal)
+        signal = self.preemphasize(signal)
+        bark = self.spectral(signal, padded)
+        d_symm, d_asymm = self.chain(bark[:batch], bark[batch:])
+        mos, loss = pesq_epilogue(d_symm, d_asymm, float(self.factor))
+        return d_symm, d_asymm, mos, loss
 
     def raw(self, ref: torch.Tensor, deg: torch.Tensor):
         """Symmetric and asymmetric distances, both ``[batch]``."""
