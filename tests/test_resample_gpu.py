@@ -88,3 +88,74 @@ def test_resampled_pipeline_matches_float64(config, items, samples):
     mos, loss = O.epilogue(ds, da, 0.5)
     for g, w in zip(got, (ds, da, mos, loss)):
         assert float(((g.double().cpu() - w).abs() / w.abs()).max()) < 1e-5
+
+
+@pytest.mark.parametrize(
+    "orig,new", [(1000, 999), (13, 7), (7, 13), (8000, 11025), (44100, 48000), (2, 1)]
+)
+def test_exotic_rate_pairs(orig, new):
+    """Coprime and near-unity rate pairs (``test_triton_resample.py:650-666``)."""
+
+    mod = HipResample(orig, new).cuda()
+    x = torch.randn(2, 3001, generator=torch.Generator().manual_seed(23))
+    got = mod(x.cuda())
+    want = O.resample(x.double(), orig, new)
+    assert got.shape == want.shape
+    assert _close(got, want)
+    xg = x.cuda().requires_grad_(True)
+    y = mod(xg)
+    g = torch.randn(y.shape, generator=torch.Generator().manual_seed(orig))
+    (gx,) = torch.autograd.grad(y, xg, grad_outputs=g.cuda())
+    xo = x.double().requires_grad_(True)
+    (gw,) = torch.autograd.grad(O.resample(xo, orig, new), xo, grad_outputs=g.double())
+    assert _close(gx, gw)
+
+
+@pytest.mark.parametrize(
+    "options",
+    [
+        dict(lowpass_filter_width=1),
+        dict(lowpass_filter_width=64),
+        dict(rolloff=0.5),
+        dict(resampling_method="sinc_interp_kaiser", beta=8.0),
+        dict(lowpass_filter_width=16, rolloff=0.945, resampling_method="sinc_interp_kaiser"),
+    ],
+)
+@pytest.mark.parametrize("orig,new", [(48000, 16000), (22050, 16000)])
+def test_filter_design_variants(orig, new, options):
+    """Non default filter designs (``test_triton_resample.py:669-697``); width 64 is the
+    longest accumulation (621 taps at 22.05 kHz)."""
+
+    mod = HipResample(orig, new, **options).cuda()
+    x = torch.randn(2, 4321, generator=torch.Generator().manual_seed(5))
+    got = mod(x.cuda())
+    want = O.resample(x.double(), orig, new, **options)
+    assert _close(got, want)
+    xg = x.cuda().requires_grad_(True)
+    y = mod(xg)
+    g = torch.randn(y.shape, generator=torch.Generator().manual_seed(7))
+    (gx,) = torch.autograd.grad(y, xg, grad_outputs=g.cuda())
+    xo = x.double().requires_grad_(True)
+    (gw,) = torch.autograd.grad(O.resample(xo, orig, new, **options), xo, grad_outputs=g.double())
+    assert _close(gx, gw)
+
+
+@pytest.mark.parametrize("orig,new", RATES)
+def test_output_length_float32_ceil(orig, new):
+    """torchaudio's float32 ``ceil`` of the output length, also where it differs
+    from the exact integer ceil (above ~180k samples at 44.1 kHz)."""
+
+    mod = HipResample(orig, new).cuda()
+    for length in list(range(1, 32)) + [255, 256, 257, 4096, 100_000, 180_000, 180_001,
+                                        180_224, 262_144]:
+        got = mod(torch.zeros(1, length, device="cuda"))
+        assert got.shape == (1, O.resample_length(length, orig, new)), (orig, new, length)
+
+
+def test_moved_after_construction():
+    mod = HipResample(48000, 16000)
+    x = torch.randn(2, 4096, device="cuda")
+    with pytest.raises(RuntimeError, match="move the module"):
+        mod(x)
+    mod = mod.cuda()
+    assert _close(mod(x), O.resample(x.double().cpu(), 48000, 16000))
