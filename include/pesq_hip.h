@@ -225,6 +225,40 @@ int pesq_resample_backward(const float *grad_y, float *grad_x, int64_t rows, int
                            const int32_t *phase_hi, int64_t orig_step, int64_t new_step,
                            int64_t width, int64_t width_total, hipStream_t stream);
 
+/* Tiled resampler.  pesq_resample_plan turns the filter bank (host memory,
+ * [new_step, width_total] float32, with the non-zero tap range of each phase)
+ * into compact zero-padded tap tables for a forward and an adjoint kernel
+ * that stage each workgroup's samples in LDS: it fills `info` and, when
+ * `plan` is not NULL, writes info->bytes bytes of tables (host memory, to be
+ * copied to the device).  fwd_span / bwd_span of 0 mean the rate pair's
+ * window is too wide for the LDS tile; the untiled entry points above then
+ * apply.  Same results as pesq_resample_forward / _backward (the same sums
+ * in the same order).  Replaces _resample_fwd_kernel / _resample_bwd_kernel
+ * (resample.py:113-243). */
+typedef struct pesq_resample_plan_info {
+    int32_t orig_step, new_step, width, width_total;
+    int32_t taps;             /* longest non-zero tap run of one phase */
+    int32_t off_min, off_max; /* extremes of tap_lo[j] - width */
+    int32_t phases;           /* most phases reading one tap column */
+    int32_t sweeps;           /* ceil(width_total / orig_step) */
+    int32_t columns;          /* sweeps * orig_step */
+    int32_t fwd_span, bwd_span; /* floats staged per workgroup, 0 = not tiled */
+    int64_t bytes;            /* size of the plan tables */
+    int64_t off_offs, off_cols, off_col_lo, off_taps64, off_row64; /* table offsets */
+} pesq_resample_plan_info;
+
+int pesq_resample_plan(const float *kernel, const int32_t *tap_lo, const int32_t *tap_hi,
+                       int64_t orig_step, int64_t new_step, int64_t width, int64_t width_total,
+                       pesq_resample_plan_info *info, void *plan);
+
+int pesq_resample_plan_forward(const float *x, float *y, int64_t rows, int64_t n_in,
+                               int64_t n_out, const pesq_resample_plan_info *info,
+                               const void *plan, hipStream_t stream);
+
+int pesq_resample_plan_backward(const float *grad_y, float *grad_x, int64_t rows, int64_t n_in,
+                                int64_t n_out, const pesq_resample_plan_info *info,
+                                const void *plan, hipStream_t stream);
+
 /* ----------------------------------------------------------------------- */
 /* STFT / Bark (TritonStftBark, torch_pesq/triton_ops/spectral.py:584-774)  */
 /* ----------------------------------------------------------------------- */

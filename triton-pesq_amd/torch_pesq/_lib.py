@@ -14,6 +14,7 @@ import torch
 
 __all__ = [
     "IirSections",
+    "ResamplePlanInfo",
     "ModelConstants",
     "library",
     "check",
@@ -33,6 +34,31 @@ GRAD_DEG = 2
 LIB_PATH = Path(os.environ.get("PESQ_HIP_LIB", Path(__file__).with_name("_lib") / "libpesq_hip.so"))
 
 c_double8 = ctypes.c_double * MAX_SECTIONS
+
+
+class ResamplePlanInfo(ctypes.Structure):
+    """``pesq_resample_plan_info``: geometry of a tiled resampler plan."""
+
+    _fields_ = [
+        ("orig_step", ctypes.c_int32),
+        ("new_step", ctypes.c_int32),
+        ("width", ctypes.c_int32),
+        ("width_total", ctypes.c_int32),
+        ("taps", ctypes.c_int32),
+        ("off_min", ctypes.c_int32),
+        ("off_max", ctypes.c_int32),
+        ("phases", ctypes.c_int32),
+        ("sweeps", ctypes.c_int32),
+        ("columns", ctypes.c_int32),
+        ("fwd_span", ctypes.c_int32),
+        ("bwd_span", ctypes.c_int32),
+        ("bytes", ctypes.c_int64),
+        ("off_offs", ctypes.c_int64),
+        ("off_cols", ctypes.c_int64),
+        ("off_col_lo", ctypes.c_int64),
+        ("off_taps64", ctypes.c_int64),
+        ("off_row64", ctypes.c_int64),
+    ]
 
 
 class IirSections(ctypes.Structure):
@@ -135,6 +161,18 @@ SIGNATURES = {
     "pesq_resample_backward": (
         _INT,
         [_P, _P, _I64, _I64, _I64, _P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    ),
+    "pesq_resample_plan": (
+        _INT,
+        [_P, _P, _P, _I64, _I64, _I64, _I64, ctypes.POINTER(ResamplePlanInfo), _P],
+    ),
+    "pesq_resample_plan_forward": (
+        _INT,
+        [_P, _P, _I64, _I64, _I64, ctypes.POINTER(ResamplePlanInfo), _P, _P],
+    ),
+    "pesq_resample_plan_backward": (
+        _INT,
+        [_P, _P, _I64, _I64, _I64, ctypes.POINTER(ResamplePlanInfo), _P, _P],
     ),
 }
 

@@ -8,6 +8,7 @@ forward), which gives a working double backward like the reference's
 ``_ResampleAdjoint`` (``resample.py:381-410``).
 """
 
+import ctypes
 import math
 from typing import Optional
 
@@ -33,6 +34,19 @@ def _launch(fn_name, src, n_out_or_in, module, forward: bool):
         n_out, n_in = src.shape[1], n_out_or_in
         out = torch.empty((rows, n_in), dtype=torch.float32, device=src.device)
         lo, hi = module.phase_lo, module.phase_hi
+    info = module.plan_info
+    tiled = info.fwd_span > 0 if forward else info.bwd_span > 0
+    if tiled:
+        name = "pesq_resample_plan_forward" if forward else "pesq_resample_plan_backward"
+        with torch.cuda.device(src.device):
+            _lib.check(
+                getattr(lib, name)(
+                    _lib.ptr(src), _lib.ptr(out), rows, n_in, n_out, ctypes.byref(info),
+                    _lib.ptr(module.plan), _lib.stream_handle(src.device),
+                ),
+                name,
+            )
+        return out
     with torch.cuda.device(src.device):
         _lib.check(
             getattr(lib, fn_name)(
@@ -140,6 +154,18 @@ class HipResample(torch.nn.Module):
         self.register_buffer("tap_hi", tap_hi)
         self.register_buffer("phase_lo", phase_lo)
         self.register_buffer("phase_hi", phase_hi)
+        # compact tap tables of the tiled kernels (csrc/resample.hip)
+        lib = _lib.library()
+        info = _lib.ResamplePlanInfo()
+        bank = kernel.contiguous()
+        args = (bank.data_ptr(), tap_lo.data_ptr(), tap_hi.data_ptr(),
+                self.orig_step, self.new_step, self.width, ntaps)
+        _lib.check(lib.pesq_resample_plan(*args, ctypes.byref(info), None), "pesq_resample_plan")
+        plan = torch.zeros(max(int(info.bytes), 4), dtype=torch.uint8)
+        _lib.check(lib.pesq_resample_plan(*args, ctypes.byref(info), plan.data_ptr()),
+                   "pesq_resample_plan")
+        self.plan_info = info
+        self.register_buffer("plan", plan)
 
     def output_length(self, n_samples: int) -> int:
         return resample_length(n_samples, self.orig_step, self.new_step)
