@@ -1,12 +1,18 @@
 """Benchmark of the PESQ loss (forward + backward) on one MI355X.
 
 ``python bench.py --gpus 1 --steps K --warmup W`` times K forward+backward
-steps of :class:`torch_pesq.PesqLossTriton` on BASELINE config c2 (B = 8 items
-of 8 s at 16 kHz, gradient w.r.t. the degraded signal) replayed from a HIP
-graph, and prints one JSON line with the metric, the eager time, the HBM
-roofline of the dominant kernel measured with HIP events on the stream the
-kernels run on, and a CPU baseline (the float32 restatement of the reference
-``PesqLoss``, timed on this host).
+steps of the PESQ loss on BASELINE config c2 (B = 8 items of 8 s at 16 kHz,
+gradient w.r.t. the degraded signal): the two C ABI calls that
+``PesqLossTriton``'s autograd makes (``pesq_pipeline_forward`` and
+``pesq_pipeline_backward``) on the resident batch.  It prints one JSON line
+with the metric, the same step through the autograd API and through HIP
+graph replay, per stage device times, the HBM roofline of the dominant stage
+measured with HIP events on the stream the kernels run on, and a CPU baseline
+(the float32 restatement of the reference ``PesqLoss``, timed on this host).
+
+``--config 3|4|5`` prints a diagnostic line for another BASELINE config
+instead (the autograd step, the resampler kernels, per stage times); those
+configs are parity cases, the headline metric is c2.
 
 Synthetic inputs: :func:`synthetic_config` (seeded voiced-speech generator of
 the five BASELINE configs).
@@ -376,6 +382,91 @@ def _profiled_traffic(stage: str):
     return None
 
 
+def diagnose(config: int, steps: int, warmup: int) -> dict:
+    """Autograd step, resampler kernels and fused stages of another BASELINE config.
+
+    The batch is the config's full shape; its items repeat the first 16
+    generated ones (the timing does not depend on the content).
+    """
+
+    import torch
+
+    from torch_pesq import PesqLossTriton
+
+    count, _, fs = CONFIGS[config]
+    k = min(count, 16)
+    ref_np, deg_np, _ = synthetic_config(config, items=k)
+    reps = -(-count // k)
+    ref_np = np.tile(ref_np, (reps, 1))[:count]
+    deg_np = np.tile(deg_np, (reps, 1))[:count]
+    device = torch.device("cuda:0")
+    model = PesqLossTriton(1.0, sample_rate=fs).to(device)
+    ref = torch.from_numpy(ref_np).to(device)
+    deg = torch.from_numpy(deg_np).to(device).requires_grad_(True)
+
+    def timed(fn, n):
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(n):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e3, start.elapsed_time(stop) / n
+
+    def step():
+        loss = model(ref, deg)
+        torch.autograd.grad(loss.sum(), deg)
+
+    wall, dev = timed(step, steps)
+    out = {
+        "diagnostic": True,
+        "config": config,
+        "shape": list(ref_np.shape),
+        "sample_rate": fs,
+        "api_ms_per_step": round(wall, 4),
+        "device_ms_per_step": round(dev, 4),
+        "signals_per_s": round(count / (wall / 1e3), 1),
+    }
+    with torch.no_grad():
+        ref16 = model.resampler(ref) if fs != 16000 else ref
+        deg16 = model.resampler(deg.detach()) if fs != 16000 else deg.detach()
+    if fs != 16000:
+        # one resampler launch each way over the rows the step resamples
+        from torch_pesq.hip_ops.resample import _ResampleAdjoint, _ResampleFunction
+
+        rs = model.resampler
+        n_out = ref16.shape[1]
+        g = torch.ones_like(deg16)
+        fwd_ms = timed(lambda: _ResampleFunction.forward(_Ctx(), ref, rs, n_out), steps)[1]
+        bwd_ms = timed(lambda: _ResampleAdjoint.forward(_Ctx(), g, rs, ref.shape[1]), steps)[1]
+        src_bytes = ref.numel() * 4
+        dst_bytes = ref16.numel() * 4
+        out["resample"] = {
+            "fwd_us": round(fwd_ms * 1e3, 2),
+            "bwd_us": round(bwd_ms * 1e3, 2),
+            "rows": ref.shape[0],
+            "fwd_hbm_frac": round((src_bytes + dst_bytes) / (fwd_ms / 1e3) / HBM_PEAK, 4),
+            "bwd_hbm_frac": round((src_bytes + dst_bytes) / (bwd_ms / 1e3) / HBM_PEAK, 4),
+        }
+    stage_s = _stage_times(model, ref16.contiguous(), deg16.contiguous(), repeats=steps)
+    per_stage, total = model_bytes(ref16.shape[0], ref16.shape[1])
+    out["stages"] = {
+        name: {"us": round(stage_s[name] * 1e6, 2),
+               "frac": round(per_stage[name] / stage_s[name] / HBM_PEAK, 4)}
+        for name in STAGES
+    }
+    out["model_bytes_16k"] = total
+    return out
+
+
+class _Ctx:
+    """Stand-in autograd context for timing a Function's forward alone."""
+
+
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -383,6 +474,8 @@ def main(argv=None):
     parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    parser.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5],
+                        help="BASELINE config; anything but 2 prints a diagnostic line")
     parser.add_argument(
         "--copy-calibration",
         action="store_true",
@@ -404,6 +497,10 @@ def main(argv=None):
     import torch
 
     from torch_pesq import PesqLossTriton
+
+    if args.config != 2:
+        print(json.dumps(diagnose(args.config, args.steps, args.warmup)))
+        return 0
 
     ref_np, deg_np, fs = synthetic_config(2)
     batch, samples = ref_np.shape
