@@ -342,11 +342,18 @@ __device__ __forceinline__ BandConsts band_consts(const ModelTable &t, int lane)
     return c;
 }
 
-constexpr int kChainWaves = 16;  // one frame of the 16 frame tile per wavefront
+// The chain kernels run a 16 frame tile with kWaves wavefronts of kTile /
+// kWaves frames each: one frame per wavefront when the grid has about one
+// workgroup per CU (latency bound), more frames per wavefront for larger
+// batches (throughput bound; more work per wave in flight).  Every sum that
+// crosses wavefronts is taken in the same per frame / per slice order for
+// any kWaves, so the results do not depend on the choice.
+constexpr int kChainSlices = 16;  // fixed split of the band partial sums
 
-__global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs a) {
-    constexpr int kPer = kTile / kChainWaves;  // frames per wavefront
-    __shared__ double part[2][kChainWaves][kBands];
+template <int kWaves>
+__global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
+    constexpr int kPer = kTile / kWaves;  // frames per wavefront
+    __shared__ double part[2][kChainSlices][kBands];
 
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
@@ -374,25 +381,35 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs 
         }
     }
 
-    // mean band powers over all frames of the item: wavefront w sums the band
-    // partials of tiles w, w + kChainWaves, ...; the partial sums are then
-    // added in wavefront order, the same order in every workgroup
+    // band constants and the uniform reciprocals, requested before the barrier
+    // (which would hold back loads issued after it)
+    const BandConsts c = band_consts(t, lane);
+    const double W = t.total_width;
+    const double inv_sqrt_w = 1.0 / sqrt(W);
+    const double inv_w = 1.0 / W;
+
+    // mean band powers over all frames of the item: slice v sums the band
+    // partials of tiles v, v + kChainSlices, ...; the slices are then added in
+    // order, the same order in every workgroup (wavefront w takes slices w,
+    // w + kWaves, ...)
     if (lane < kBands) {
         const double *pr = region<double>(a.ws, L.bandref) + int64_t(item) * L.ntile * kBands;
         const double *pd = region<double>(a.ws, L.banddeg) + int64_t(item) * L.ntile * kBands;
-        part[0][wave][lane] = tile_partial(pr, L.ntile, wave, kChainWaves, lane);
-        part[1][wave][lane] = tile_partial(pd, L.ntile, wave, kChainWaves, lane);
+#pragma unroll
+        for (int v = wave; v < kChainSlices; v += kWaves) {
+            part[0][v][lane] = tile_partial(pr, L.ntile, v, kChainSlices, lane);
+            part[1][v][lane] = tile_partial(pd, L.ntile, v, kChainSlices, lane);
+        }
     }
     __syncthreads();
 
-    const BandConsts c = band_consts(t, lane);
     const bool live = lane < kBands;
     double r = 0.0;
     if (live) {
         double sr = 0.0, sd = 0.0;
-        for (int w = 0; w < kChainWaves; ++w) {
-            sr += part[0][w][lane];
-            sd += part[1][w][lane];
+        for (int v = 0; v < kChainSlices; ++v) {
+            sr += part[0][v][lane];
+            sd += part[1][v][lane];
         }
         const double mref = sr / frames_f;
         const double mdeg = sd / frames_f;
@@ -404,10 +421,6 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_fwd_kernel(PipeArgs 
             band_array(a, kMref)[item * kBands + lane] = mref;
         }
     }
-    const double W = t.total_width;
-    const double inv_sqrt_w = 1.0 / sqrt(t.total_width);
-    const double inv_w = 1.0 / W;
-
     // per frame totals of the audible energies; slot q is frame f0 - 1 + q
     double taer[kPer + 1], tad[kPer + 1];
 #pragma unroll
@@ -544,14 +557,15 @@ __device__ __forceinline__ double psqm_adjoint(const PipeLayout &L, const double
     return acc;
 }
 
-__global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs a) {
-    constexpr int kPer = kTile / kChainWaves;
+template <int kWaves>
+__global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
+    constexpr int kPer = kTile / kWaves;
     constexpr int kSlots = kTile + 1;  // the tile's frames and the next one
     __shared__ double rs[kBands];
     __shared__ double fr[kFrameArrays][kSlots];
     __shared__ double pl[2][kPsqmSlots];
     __shared__ double gfpr[kSlots], gh[kSlots];
-    __shared__ double part[kChainWaves][kBands];
+    __shared__ double part[kTile][kBands];  // per frame band partials
 
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
@@ -593,6 +607,9 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
         pl[side][i] = region<double>(a.ws, L.psqm)[(int64_t(side) * L.batch + item) * L.nwin + l];
     }
     if (wave == 0 && live) rs[lane] = band_array(a, kR)[item * kBands + lane];
+    // band constants, requested before the barrier (which would hold them back)
+    const BandConsts c = band_consts(t, lane);
+    const double W = t.total_width;
 
     // upstream gradients of the two distances, MOS and loss folded in
     const double *dist = region<double>(a.ws, L.dist) + int64_t(item) * 2;
@@ -614,13 +631,11 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
     }
     __syncthreads();
 
-    const BandConsts c = band_consts(t, lane);
     const double r = live ? rs[lane] : 0.0;
-    const double W = t.total_width;
 
     // phase 1: adjoint of the per frame distances down to equ_ref / equ_deg
     double g_er[kPer + 1], g_ed[kPer + 1];
-    const int nmine = wave == kChainWaves - 1 ? kPer + 1 : kPer;
+    const int nmine = wave == kWaves - 1 ? kPer + 1 : kPer;
 #pragma unroll
     for (int q = 0; q <= kPer; ++q) {
         const int local = wave * kPer + q;
@@ -692,8 +707,12 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
     }
     __syncthreads();
 
-    // phase 2: frame power ratio, h and the total audible energies
-    double acc = 0.0;
+    // phase 2: frame power ratio, h and the total audible energies; the
+    // band partials of d/dr are kept per frame and added in frame order
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        if (live) part[wave * kPer + q][lane] = 0.0;
+    }
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
         const int local = wave * kPer + q;
@@ -722,14 +741,13 @@ __global__ void __launch_bounds__(kWave *kChainWaves) chain_bwd_kernel(PipeArgs 
             const double ged = g_ed[q] * fpr + (Gq > c.th ? g_tad : 0.0);
             a.gbark_ref[(int64_t(item) * L.frames + frame) * kBands + lane] = static_cast<float>(ger * r);
             a.gbark_deg[(int64_t(item) * L.frames + frame) * kBands + lane] = static_cast<float>(ged);
-            acc += ger * Rq;
+            part[local][lane] = ger * Rq;
         }
     }
-    if (live) part[wave][lane] = acc;
     __syncthreads();
     if (wave == 0 && live) {
         double s = 0.0;
-        for (int w = 0; w < kChainWaves; ++w) s += part[w][lane];
+        for (int f = 0; f < kTile; ++f) s += part[f][lane];
         region<double>(a.bw, L.grpart)[(int64_t(item) * L.ntile + tile) * kBands + lane] = s;
     }
 }
@@ -1041,6 +1059,28 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_plain_bwd_kernel(StftA
 #endif
 using StftReal = PESQ_STFT_REAL;
 
+// Chain launches: up to about two workgroups per CU of the 256 CU MI355X the
+// kernels are latency bound and run one frame (backward) or two (forward) per
+// wavefront; larger grids run four frames per wavefront (measured best at
+// BASELINE c2 and c5 respectively).  The results are the same either way.
+constexpr unsigned kChainWideGrid = 512;
+
+static void launch_chain_fwd(const PipeArgs &a, unsigned grid, hipStream_t stream) {
+    if (grid <= kChainWideGrid) {
+        hipLaunchKernelGGL(chain_fwd_kernel<8>, dim3(grid), dim3(kWave * 8), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(chain_fwd_kernel<4>, dim3(grid), dim3(kWave * 4), 0, stream, a);
+    }
+}
+
+static void launch_chain_bwd(const PipeArgs &a, unsigned grid, hipStream_t stream) {
+    if (grid <= kChainWideGrid) {
+        hipLaunchKernelGGL(chain_bwd_kernel<16>, dim3(grid), dim3(kWave * 16), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(chain_bwd_kernel<4>, dim3(grid), dim3(kWave * 4), 0, stream, a);
+    }
+}
+
 static int check_sizes(int64_t batch, int64_t len, const PipeLayout &L) {
     PESQ_CHECK_ARG(batch > 0, "batch must be positive, got %lld", (long long)batch);
     PESQ_CHECK_ARG(len >= 15, "the edge ramp needs at least 15 samples, got %lld", (long long)len);
@@ -1133,8 +1173,7 @@ extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, 
         PESQ_CHECK_LAUNCH("pipeline stft");
     }
     if (stages & 8u) {
-        hipLaunchKernelGGL(chain_fwd_kernel, dim3(static_cast<unsigned>(batch * L.ntile)),
-                           dim3(kWave * kChainWaves), 0, stream, a);
+        launch_chain_fwd(a, static_cast<unsigned>(batch * L.ntile), stream);
         PESQ_CHECK_LAUNCH("pipeline chain");
     }
     if (stages & 16u) {
@@ -1183,8 +1222,7 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
     a.gbark_deg = a.gbark_ref + batch * L.frames * kBands;
 
     if (stages & 1u) {
-        hipLaunchKernelGGL(chain_bwd_kernel, dim3(static_cast<unsigned>(batch * L.ntile)),
-                           dim3(kWave * kChainWaves), 0, stream, a);
+        launch_chain_bwd(a, static_cast<unsigned>(batch * L.ntile), stream);
         PESQ_CHECK_LAUNCH("pipeline chain backward");
     }
     if (stages & 2u) {
@@ -1268,7 +1306,7 @@ extern "C" int pesq_chain_forward(const float *ref_bark, const float *deg_bark, 
     const unsigned grid = static_cast<unsigned>(batch * a.L.ntile);
     hipLaunchKernelGGL(chain_partials_kernel, dim3(grid), dim3(kWave), 0, stream, a);
     PESQ_CHECK_LAUNCH("chain partials");
-    hipLaunchKernelGGL(chain_fwd_kernel, dim3(grid), dim3(kWave * kChainWaves), 0, stream, a);
+    launch_chain_fwd(a, grid, stream);
     PESQ_CHECK_LAUNCH("chain");
     hipLaunchKernelGGL(chain_final_kernel, dim3(static_cast<unsigned>(batch)), dim3(kFinalThreads),
                        0, stream, a);
@@ -1294,7 +1332,7 @@ extern "C" int pesq_chain_backward(const float *g_symm, const float *g_asymm, co
     a.g_symm = g_symm;
     a.g_asymm = g_asymm;
     const unsigned grid = static_cast<unsigned>(batch * a.L.ntile);
-    hipLaunchKernelGGL(chain_bwd_kernel, dim3(grid), dim3(kWave * kChainWaves), 0, stream, a);
+    launch_chain_bwd(a, grid, stream);
     PESQ_CHECK_LAUNCH("chain backward");
     hipLaunchKernelGGL(chain_meanpow_kernel, dim3(grid), dim3(kWave), 0, stream, a);
     PESQ_CHECK_LAUNCH("chain mean power backward");
