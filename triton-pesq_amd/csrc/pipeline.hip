@@ -30,6 +30,8 @@
 // is zero for the same reason: the loss is invariant under s -> c s.)
 #include <cmath>
 
+#include <type_traits>
+
 #include "pipeline_layout.hpp"
 #include "tables.hpp"
 
@@ -209,8 +211,11 @@ __device__ __forceinline__ double sgn(double v) { return v > 0.0 ? 1.0 : (v < 0.
 
 constexpr int kStftWaves = 8;
 
-template <typename real>
-__global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a) {
+// kLean: the variant for grids of several workgroups per CU, which keeps
+// fewer values live (no next-frame prefetch, twiddles read again per frame,
+// a rolled band sum) so that more wavefronts fit per SIMD.
+template <typename real, bool kLean>
+__global__ void __launch_bounds__(kWave *kStftWaves, kLean ? 4 : 1) stft_fwd_kernel(PipeArgs a) {
     __shared__ cplx<real> fftbuf[kStftWaves][kHalf];
     __shared__ float barks[2][kTile][kBands];
     __shared__ float keepflag[kTile];
@@ -250,13 +255,21 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
     float *bark = region<float>(a.ws, L.bark) + int64_t(row) * L.frames * kBands;
     cplx<real> *buf = fftbuf[wave];
     real *power_buf = reinterpret_cast<real *>(buf);
-    Twiddles tw;
-    tw.load(t.tw256, t.tw512, lane);
+    // kLean reads the twiddles per pass; otherwise they stay in registers
+    using TW = typename std::conditional<kLean, LazyTwiddles, Twiddles>::type;
+    TW tw;
+    if constexpr (kLean) {
+        tw = TW{t.tw256, t.tw512, lane};
+    } else {
+        tw.load(t.tw256, t.tw512, lane);
+    }
     float win[8];
+    if constexpr (!kLean) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        win[2 * r] = t.window[2 * (lane + 64 * r)];
-        win[2 * r + 1] = t.window[2 * (lane + 64 * r) + 1];
+        for (int r = 0; r < 4; ++r) {
+            win[2 * r] = t.window[2 * (lane + 64 * r)];
+            win[2 * r + 1] = t.window[2 * (lane + 64 * r) + 1];
+        }
     }
     const int band_lo = lane < kBands ? t.band_start[lane] : 0;
     const int band_hi = lane < kBands ? t.band_end[lane] : 0;
@@ -269,8 +282,21 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
         if (frame >= L.frames) break;
         // the next frame's samples load while this one is transformed
         float nxt[8];
-        const int64_t fn = frame + 1 < L.frames ? frame + 1 : frame;
-        load_frame(p, fn * kHop, L.len, lane, nxt);
+        if constexpr (!kLean) {
+            const int64_t fn = frame + 1 < L.frames ? frame + 1 : frame;
+            load_frame(p, fn * kHop, L.len, lane, nxt);
+        } else {
+            if (q > 0) load_frame(p, frame * kHop, L.len, lane, cur);
+            // through reload(): the twiddle and window loads stay inside the
+            // frame loop
+            tw = TW{reload(t.tw256), reload(t.tw512), lane};
+            const float *wp = reload(t.window);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                win[2 * r] = wp[2 * (lane + 64 * r)];
+                win[2 * r + 1] = wp[2 * (lane + 64 * r) + 1];
+            }
+        }
         auto u = [&](int k) -> real {
             // k = 2 (lane + 64 r) + {0, 1}: sample and window value at index 2 r + {0, 1}
             const int i = 2 * (k >> 7) + (k & 1);
@@ -278,8 +304,10 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
         };
         cplx<real> x[4];
         frame_spectrum<real>(u, x, buf, tw, lane);
+        if constexpr (!kLean) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+            for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int fbin = lane + 64 * r;
@@ -288,7 +316,12 @@ __global__ void __launch_bounds__(kWave *kStftWaves) stft_fwd_kernel(PipeArgs a)
         wave_lds_fence();
         double val = 0.0;
         if (lane < kBands) {
-            const double acc = band_sum(power_buf, band_lo, band_hi);
+            double acc = 0.0;
+            if constexpr (kLean) {
+                for (int f = band_lo; f < band_hi; ++f) acc += static_cast<double>(power_buf[f]);
+            } else {
+                acc = band_sum(power_buf, band_lo, band_hi);
+            }
             const float v = static_cast<float>(acc * corr);
             bark[frame * kBands + lane] = v;
             barks[side][local][lane] = v;
@@ -757,7 +790,10 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
 // ---------------------------------------------------------------------------
 
 template <typename real>
-__global__ void __launch_bounds__(kWave *kBwdFrames, 4) stft_bwd_kernel(PipeArgs a) {
+#ifndef PESQ_STFT_BWD_OCC
+#define PESQ_STFT_BWD_OCC 4
+#endif
+__global__ void __launch_bounds__(kWave *kBwdFrames, PESQ_STFT_BWD_OCC) stft_bwd_kernel(PipeArgs a) {
     __shared__ cplx<real> fftbuf[kBwdFrames][kHalf];
     __shared__ float contrib[kBwdFrames][kNfft];
     __shared__ double gpart[kBwdFrames][kBands];
@@ -1168,8 +1204,14 @@ extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, 
         }
     }
     if (stages & 4u) {
-        hipLaunchKernelGGL(stft_fwd_kernel<StftReal>, dim3(static_cast<unsigned>(batch * L.ntile)),
-                           dim3(kWave * kStftWaves), 0, stream, a);
+        const unsigned grid = static_cast<unsigned>(batch * L.ntile);
+        if (grid <= kChainWideGrid) {
+            hipLaunchKernelGGL((stft_fwd_kernel<StftReal, false>), dim3(grid),
+                               dim3(kWave * kStftWaves), 0, stream, a);
+        } else {
+            hipLaunchKernelGGL((stft_fwd_kernel<StftReal, true>), dim3(grid),
+                               dim3(kWave * kStftWaves), 0, stream, a);
+        }
         PESQ_CHECK_LAUNCH("pipeline stft");
     }
     if (stages & 8u) {

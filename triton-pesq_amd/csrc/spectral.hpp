@@ -110,11 +110,27 @@ struct Twiddles {
 #pragma unroll
         for (int r = 0; r < 4; ++r) fold[r] = tw512[lane + 64 * r];
     }
+    __device__ __forceinline__ double2 pass_tw(int p, int r) const { return pass[p - 1][r - 1]; }
+    __device__ __forceinline__ double2 fold_tw(int r) const { return fold[r]; }
+};
+
+// The same twiddles read from the tables when a pass needs them: fewer values
+// live across the transform, one cached load each.
+struct LazyTwiddles {
+    const double2 *tw256, *tw512;
+    int lane;
+
+    __device__ __forceinline__ double2 pass_tw(int p, int r) const {
+        const int ns = 1 << (2 * p);
+        const int k = lane & (ns - 1);
+        return tw256[(k * r * (64 / ns)) & 255];
+    }
+    __device__ __forceinline__ double2 fold_tw(int r) const { return tw512[lane + 64 * r]; }
 };
 
 // In: v[r] = z_{lane + 64 r}.  Out: buf[slot(n)] = Z_n, unnormalised.
-template <typename real, bool kInverse>
-__device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, const Twiddles &tw,
+template <typename real, bool kInverse, class TW>
+__device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, const TW &tw,
                                        int lane) {
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
@@ -125,7 +141,7 @@ __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, cons
             wave_lds_fence();
 #pragma unroll
             for (int r = 1; r < 4; ++r) {
-                const double2 w = tw.pass[pass - 1][r - 1];
+                const double2 w = tw.pass_tw(pass, r);
                 const cplx<real> c = {static_cast<real>(w.x),
                                       static_cast<real>(kInverse ? -w.y : w.y)};
                 v[r] = cmul(v[r], c);
@@ -143,9 +159,9 @@ __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, cons
 // Spectrum of one frame: X_f for f = lane + 64 r (r = 0..3), given the frame
 // samples u (already windowed) through the load functor u(k), k < 512.
 // tw holds the per lane twiddles (Twiddles::load).
-template <typename real, class Load>
+template <typename real, class Load, class TW>
 __device__ __forceinline__ void frame_spectrum(Load u, cplx<real> (&x)[4], cplx<real> *buf,
-                                               const Twiddles &tw, int lane) {
+                                               const TW &tw, int lane) {
     cplx<real> v[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -161,7 +177,7 @@ __device__ __forceinline__ void frame_spectrum(Load u, cplx<real> (&x)[4], cplx<
         // E = (Zf + conj Zm) / 2,  O = -i (Zf - conj Zm) / 2
         const cplx<real> e = {(zf.re + zm.re) * real(0.5), (zf.im - zm.im) * real(0.5)};
         const cplx<real> o = {(zf.im + zm.im) * real(0.5), -(zf.re - zm.re) * real(0.5)};
-        const double2 w = tw.fold[r];
+        const double2 w = tw.fold_tw(r);
         const cplx<real> c = {static_cast<real>(w.x), static_cast<real>(w.y)};
         const cplx<real> t = cmul(c, o);
         x[r] = {e.re + t.re, e.im + t.im};
@@ -171,9 +187,9 @@ __device__ __forceinline__ void frame_spectrum(Load u, cplx<real> (&x)[4], cplx<
 
 // Adjoint: given V_f for f = lane + 64 r (zero at f = 0), returns g_u_{2n} and
 // g_u_{2n+1} for n = lane + 64 r in (even[r], odd[r]).  V_256 is zero.
-template <typename real>
+template <typename real, class TW>
 __device__ __forceinline__ void frame_adjoint(const cplx<real> (&vf)[4], real (&even)[4],
-                                              real (&odd)[4], cplx<real> *buf, const Twiddles &tw,
+                                              real (&odd)[4], cplx<real> *buf, const TW &tw,
                                               int lane) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) buf[slot(lane + 64 * r)] = vf[r];
@@ -187,7 +203,7 @@ __device__ __forceinline__ void frame_adjoint(const cplx<real> (&vf)[4], real (&
         const cplx<real> b = f == 0 ? cplx<real>{real(0), real(0)} : buf[slot(kHalf - f)];
         const cplx<real> s = {a.re + b.re, a.im - b.im};   // V_f + conj V_{256-f}
         const cplx<real> d = {a.re - b.re, a.im + b.im};   // V_f - conj V_{256-f}
-        const double2 w = tw.fold[r];
+        const double2 w = tw.fold_tw(r);
         const cplx<real> c = {static_cast<real>(w.x), static_cast<real>(-w.y)};  // e^{+...}
         const cplx<real> t = cmul(c, d);
         // Z' = s + i t
