@@ -313,20 +313,28 @@ int pesq_stft_backward(const float *g_bark, const float *x, int64_t rows, int64_
 /* perceptual chain (TritonPesqChain, torch_pesq/triton_ops/chain.py:1024-1126) */
 /* ----------------------------------------------------------------------- */
 
-int pesq_chain_forward_workspace(int64_t batch, int64_t frames, size_t *bytes);
-int pesq_chain_backward_workspace(int64_t batch, int64_t frames, size_t *bytes);
+/* Pack the chain constants of `nbands` bands (1 .. 64) into `out` (host
+ * memory, pesq_model_table_bytes() bytes): hearing thresholds (> 0), loudness
+ * exponents, band widths in Bark, their total over bands 1.. and sl.  The
+ * constructor of TritonPesqChain (chain.py:1057-1078).  A table from
+ * pesq_model_table_pack serves the 49 band chain as well. */
+int pesq_chain_table_pack(int nbands, const double *threshs, const double *exps,
+                          const double *widths, double total_width, double sl, void *out);
 
-/* (d_symm, d_asymm)[batch] of two Bark spectrograms [batch, frames, 49];
- * needs at least 20 frames.  Replaces the 7 forward kernels of
- * _ChainFunction.forward (chain.py:768-940). */
+int pesq_chain_forward_workspace(int64_t batch, int64_t frames, int nbands, size_t *bytes);
+int pesq_chain_backward_workspace(int64_t batch, int64_t frames, int nbands, size_t *bytes);
+
+/* (d_symm, d_asymm)[batch] of two Bark spectrograms [batch, frames, nbands]
+ * (nbands 1 .. 64, as packed in model_table); needs at least 20 frames.
+ * Replaces the 7 forward kernels of _ChainFunction.forward (chain.py:768-940). */
 int pesq_chain_forward(const float *ref_bark, const float *deg_bark, int64_t batch,
-                       int64_t frames, const void *model_table, float *d_symm, float *d_asymm,
-                       void *fwd_workspace, hipStream_t stream);
+                       int64_t frames, int nbands, const void *model_table, float *d_symm,
+                       float *d_asymm, void *fwd_workspace, hipStream_t stream);
 
 /* Gradients w.r.t. both spectrograms given those of the distances (NULL =
  * zero).  Replaces _ChainFunction.backward (chain.py:942-1021). */
 int pesq_chain_backward(const float *g_symm, const float *g_asymm, const float *ref_bark,
-                        const float *deg_bark, int64_t batch, int64_t frames,
+                        const float *deg_bark, int64_t batch, int64_t frames, int nbands,
                         const void *model_table, float *g_ref_bark, float *g_deg_bark,
                         const void *fwd_workspace, void *bwd_workspace, hipStream_t stream);
 

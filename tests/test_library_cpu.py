@@ -233,6 +233,25 @@ def test_stft_construction_validation():
     assert not HipStftBark(torch.hann_window(512), scale.fbank, scale.pow_dens_correction).general
 
 
+def test_chain_table_pack_validates():
+    lib = _lib.library()
+    buf = (ctypes.c_ubyte * lib.pesq_model_table_bytes())()
+    th = np.full(17, 2.0)
+    ex = np.full(17, 0.2)
+    wd = np.full(17, 0.5)
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    assert lib.pesq_chain_table_pack(17, ptr(th), ptr(ex), ptr(wd), 8.0, 0.18, buf) == 0
+    assert lib.pesq_chain_table_pack(65, ptr(np.ones(65)), ptr(np.ones(65)), ptr(np.ones(65)),
+                                     8.0, 0.18, buf) != 0
+    assert b"bands" in lib.pesq_last_error()
+    th[3] = 0.0
+    assert lib.pesq_chain_table_pack(17, ptr(th), ptr(ex), ptr(wd), 8.0, 0.18, buf) != 0
+    assert b"strictly positive" in lib.pesq_last_error()
+    out = ctypes.c_size_t(0)
+    assert lib.pesq_chain_forward_workspace(2, 40, 17, ctypes.byref(out)) == 0
+    assert lib.pesq_chain_forward_workspace(2, 40, 0, ctypes.byref(out)) != 0
+
+
 def test_iir_table_pack_validates():
     lib = _lib.library()
     s = _lib.IirSections()

@@ -267,3 +267,42 @@ def test_chain_batch_independence_and_errors(chain):
         chain(ref.cuda(), deg[:, :29].cuda())
     with pytest.raises(RuntimeError):
         chain(ref, deg)
+
+
+@pytest.mark.parametrize("nband", [17, 33, 64])
+def test_chain_other_band_counts(nband):
+    """Band counts other than 49 (``test_triton_chain.py:668-717``): random
+    thresholds, exponents and widths, against the float64 restatement with the
+    same tables, forward and gradients.  The kernels take one band per lane,
+    so 64 is the largest count (65 raises)."""
+
+    gen = torch.Generator().manual_seed(nband)
+    threshs = (10 ** (torch.rand(nband, generator=gen) * 8 - 1)).double()
+    exps = (0.15 + 0.15 * torch.rand(nband, generator=gen)).double()
+    widths = (0.15 + 0.45 * torch.rand(nband, generator=gen)).double()
+    total = float(widths[1:].sum())
+    chain = HipPesqChain(threshs, exps, widths, total, 0.1866055).cuda()
+    level = 10 ** (torch.rand((2, 63, 1), generator=gen, dtype=torch.float64) * 6)
+    tilt = 0.2 + 2.0 * torch.rand((2, 63, nband), generator=gen, dtype=torch.float64)
+    ref = (threshs.reshape(1, 1, -1) * level * tilt).float()
+    deg = (ref.double() * 10 ** (torch.rand((2, 63, nband), generator=gen, dtype=torch.float64) - 0.5)).float()
+    c = dict(O.constants())
+    c.update(threshs=threshs, exp=exps, width_bark=widths, total_width=torch.tensor(total, dtype=torch.float64))
+    r, d = ref.cuda().requires_grad_(True), deg.cuda().requires_grad_(True)
+    ds, da = chain(r, d)
+    ro, do = ref.double().requires_grad_(True), deg.double().requires_grad_(True)
+    wds, wda = O.chain(ro, do, c)
+    assert float(((ds.double().cpu() - wds).abs() / wds).max()) < 1e-5
+    assert float(((da.double().cpu() - wda).abs() / wda).max()) < 1e-5
+    u = torch.tensor([0.7, -1.3], dtype=torch.float64)
+    gr, gd = torch.autograd.grad([ds.sum(), (da * u.float().cuda()).sum()], [r, d])
+    wr, wd = torch.autograd.grad([wds.sum(), (wda * u).sum()], [ro, do])
+    assert float((gr.double().cpu() - wr).abs().max() / wr.abs().max()) < 2e-5
+    assert float((gd.double().cpu() - wd).abs().max() / wd.abs().max()) < 2e-5
+    with pytest.raises(ValueError, match="Bark bands"):
+        chain(ref[:, :, :-1].contiguous().cuda(), deg[:, :, :-1].contiguous().cuda())
+
+
+def test_chain_rejects_more_than_64_bands():
+    with pytest.raises(ValueError, match="at most 64"):
+        HipPesqChain(torch.ones(65), torch.full((65,), 0.2), torch.ones(65), 64.0)

@@ -134,6 +134,33 @@ extern "C" int pesq_iir_cascade_pack(const double *sos, int sections, void *out)
 
 extern "C" size_t pesq_model_table_bytes(void) { return sizeof(ModelTable); }
 
+extern "C" int pesq_chain_table_pack(int nbands, const double *threshs, const double *exps,
+                                     const double *widths, double total_width, double sl,
+                                     void *out) {
+    PESQ_CHECK_ARG(threshs && exps && widths && out, "null argument");
+    PESQ_CHECK_ARG(nbands >= 1 && nbands <= kMaxChainBands, "the chain takes 1 .. %d bands, got %d",
+                   kMaxChainBands, nbands);
+    ModelTable *t = new ModelTable;
+    std::memset(t, 0, sizeof(*t));
+    for (int i = 0; i < nbands; ++i) {
+        if (!(threshs[i] > 0.0) || !std::isfinite(exps[i]) || !std::isfinite(widths[i])) {
+            delete t;
+            set_error("Hearing thresholds have to be strictly positive (band %d).", i);
+            return PESQ_ERR_ARGUMENT;
+        }
+        t->threshs[i] = threshs[i];
+        t->exps[i] = exps[i];
+        t->width[i] = widths[i];
+        t->loud_scale[i] = sl * std::pow(2.0 * threshs[i], exps[i]);
+    }
+    t->total_width = total_width;
+    t->sl = sl;
+    t->nbarks = nbands;
+    std::memcpy(out, t, sizeof(*t));
+    delete t;
+    return PESQ_OK;
+}
+
 extern "C" int pesq_model_table_pack(const pesq_model_constants *c, void *out) {
     PESQ_CHECK_ARG(c != nullptr && out != nullptr, "null argument");
     PESQ_CHECK_ARG(c->nbarks == kBands && c->n_fft == kNfft && c->hop == kHop,

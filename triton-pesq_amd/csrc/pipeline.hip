@@ -163,16 +163,15 @@ __device__ __forceinline__ double *frame_array(const PipeArgs &a, int which) {
 }
 
 __device__ __forceinline__ double *band_array(const PipeArgs &a, int which) {
-    return region<double>(a.ws, a.L.band) + int64_t(which) * a.L.batch * kBands;
+    return region<double>(a.ws, a.L.band) + int64_t(which) * a.L.batch * a.L.nb;
 }
 
-// Band `lane` of the per tile band partials base[tile][49], summed over tiles
+// Band `lane` of the per tile band partials base[tile][nb], summed over tiles
 // part, part + parts, part + 2 parts, ... (in that order); 0 when there are none.
 __device__ __forceinline__ double tile_partial(const double *base, int64_t ntile, int part,
-                                               int parts, int lane) {
+                                               int parts, int lane, int nb) {
     const int n = ntile > part ? static_cast<int>((ntile - 1 - part) / parts) + 1 : 0;
-    return n > 0 ? strided_sum(base + int64_t(part) * kBands + lane, n, int64_t(parts) * kBands)
-                 : 0.0;
+    return n > 0 ? strided_sum(base + int64_t(part) * nb + lane, n, int64_t(parts) * nb) : 0.0;
 }
 
 // Zwicker loudness sl (2 th)^e ((0.5 + 0.5 x / th)^e - 1) above the threshold,
@@ -363,9 +362,9 @@ struct BandConsts {
     double th, inv2th, e, ls, w;
 };
 
-__device__ __forceinline__ BandConsts band_consts(const ModelTable &t, int lane) {
+__device__ __forceinline__ BandConsts band_consts(const ModelTable &t, int lane, int nb) {
     BandConsts c{1.0, 0.5, 1.0, 0.0, 0.0};
-    if (lane < kBands) {
+    if (lane < nb) {
         c.th = t.threshs[lane];
         c.inv2th = 0.5 / c.th;
         c.e = t.exps[lane];
@@ -386,10 +385,11 @@ constexpr int kChainSlices = 16;  // fixed split of the band partial sums
 template <int kWaves>
 __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
     constexpr int kPer = kTile / kWaves;  // frames per wavefront
-    __shared__ double part[2][kChainSlices][kBands];
+    __shared__ double part[2][kChainSlices][kMaxChainBands];
 
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
+    const int nb = L.nb;  // bands, one per lane
     const int item = blockIdx.x / L.ntile;
     const int tile = blockIdx.x - item * L.ntile;
     const int t0 = tile * kTile;
@@ -402,21 +402,21 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
     // clamped into the array; out of range frames and bands are masked later)
     float R[kPer + 1], G[kPer + 1];
     {
-        const int band = lane < kBands ? lane : kBands - 1;
-        const float *bref = a.bark_ref + int64_t(item) * L.frames * kBands;
-        const float *bdeg = a.bark_deg + int64_t(item) * L.frames * kBands;
+        const int band = lane < nb ? lane : nb - 1;
+        const float *bref = a.bark_ref + int64_t(item) * L.frames * nb;
+        const float *bdeg = a.bark_deg + int64_t(item) * L.frames * nb;
 #pragma unroll
         for (int q = 0; q <= kPer; ++q) {
             int64_t frame = f0 - 1 + q;
             frame = frame < 0 ? 0 : (frame >= L.frames ? L.frames - 1 : frame);
-            R[q] = bref[frame * kBands + band];
-            G[q] = bdeg[frame * kBands + band];
+            R[q] = bref[frame * nb + band];
+            G[q] = bdeg[frame * nb + band];
         }
     }
 
     // band constants and the uniform reciprocals, requested before the barrier
     // (which would hold back loads issued after it)
-    const BandConsts c = band_consts(t, lane);
+    const BandConsts c = band_consts(t, lane, nb);
     const double W = t.total_width;
     const double inv_sqrt_w = 1.0 / sqrt(W);
     const double inv_w = 1.0 / W;
@@ -425,18 +425,18 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
     // partials of tiles v, v + kChainSlices, ...; the slices are then added in
     // order, the same order in every workgroup (wavefront w takes slices w,
     // w + kWaves, ...)
-    if (lane < kBands) {
-        const double *pr = region<double>(a.ws, L.bandref) + int64_t(item) * L.ntile * kBands;
-        const double *pd = region<double>(a.ws, L.banddeg) + int64_t(item) * L.ntile * kBands;
+    if (lane < nb) {
+        const double *pr = region<double>(a.ws, L.bandref) + int64_t(item) * L.ntile * nb;
+        const double *pd = region<double>(a.ws, L.banddeg) + int64_t(item) * L.ntile * nb;
 #pragma unroll
         for (int v = wave; v < kChainSlices; v += kWaves) {
-            part[0][v][lane] = tile_partial(pr, L.ntile, v, kChainSlices, lane);
-            part[1][v][lane] = tile_partial(pd, L.ntile, v, kChainSlices, lane);
+            part[0][v][lane] = tile_partial(pr, L.ntile, v, kChainSlices, lane, nb);
+            part[1][v][lane] = tile_partial(pd, L.ntile, v, kChainSlices, lane, nb);
         }
     }
     __syncthreads();
 
-    const bool live = lane < kBands;
+    const bool live = lane < nb;
     double r = 0.0;
     if (live) {
         double sr = 0.0, sd = 0.0;
@@ -449,9 +449,9 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
         const double ratio = (mdeg + 1000.0) / (mref + 1000.0);
         r = fmin(fmax(ratio, 0.01), 100.0);
         if (tile == 0 && wave == 0) {
-            band_array(a, kR)[item * kBands + lane] = r;
-            band_array(a, kRatio)[item * kBands + lane] = ratio;
-            band_array(a, kMref)[item * kBands + lane] = mref;
+            band_array(a, kR)[item * nb + lane] = r;
+            band_array(a, kRatio)[item * nb + lane] = ratio;
+            band_array(a, kMref)[item * nb + lane] = mref;
         }
     }
     // per frame totals of the audible energies; slot q is frame f0 - 1 + q
@@ -594,35 +594,36 @@ template <int kWaves>
 __global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
     constexpr int kPer = kTile / kWaves;
     constexpr int kSlots = kTile + 1;  // the tile's frames and the next one
-    __shared__ double rs[kBands];
+    __shared__ double rs[kMaxChainBands];
     __shared__ double fr[kFrameArrays][kSlots];
     __shared__ double pl[2][kPsqmSlots];
     __shared__ double gfpr[kSlots], gh[kSlots];
-    __shared__ double part[kTile][kBands];  // per frame band partials
+    __shared__ double part[kTile][kMaxChainBands];  // per frame band partials
 
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
+    const int nb = L.nb;  // bands, one per lane
     const int item = blockIdx.x / L.ntile;
     const int tile = blockIdx.x - item * L.ntile;
     const int t0 = tile * kTile;
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
-    const bool live = lane < kBands;
+    const bool live = lane < nb;
     const int64_t fo = int64_t(item) * L.frames;
     const int64_t lbase = t0 / kStride - 1;
 
     // Bark values of this wavefront's frames (slot q = local frame wave kPer + q)
     float R[kPer + 1], G[kPer + 1];
     {
-        const int band = live ? lane : kBands - 1;
-        const float *bref = a.bark_ref + int64_t(item) * L.frames * kBands;
-        const float *bdeg = a.bark_deg + int64_t(item) * L.frames * kBands;
+        const int band = live ? lane : nb - 1;
+        const float *bref = a.bark_ref + int64_t(item) * L.frames * nb;
+        const float *bdeg = a.bark_deg + int64_t(item) * L.frames * nb;
 #pragma unroll
         for (int q = 0; q <= kPer; ++q) {
             const int64_t frame = t0 + wave * kPer + q;
             const int64_t fc = frame < L.frames ? frame : L.frames - 1;
-            R[q] = bref[fc * kBands + band];
-            G[q] = bdeg[fc * kBands + band];
+            R[q] = bref[fc * nb + band];
+            G[q] = bdeg[fc * nb + band];
         }
     }
 
@@ -639,9 +640,9 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
         l = l < 0 ? 0 : (l >= L.nwin ? L.nwin - 1 : l);
         pl[side][i] = region<double>(a.ws, L.psqm)[(int64_t(side) * L.batch + item) * L.nwin + l];
     }
-    if (wave == 0 && live) rs[lane] = band_array(a, kR)[item * kBands + lane];
+    if (wave == 0 && live) rs[lane] = band_array(a, kR)[item * nb + lane];
     // band constants, requested before the barrier (which would hold them back)
-    const BandConsts c = band_consts(t, lane);
+    const BandConsts c = band_consts(t, lane, nb);
     const double W = t.total_width;
 
     // upstream gradients of the two distances, MOS and loss folded in
@@ -772,8 +773,8 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
             double ger = g_er[q];
             if (r * Rq > c.th) ger += g_taer;
             const double ged = g_ed[q] * fpr + (Gq > c.th ? g_tad : 0.0);
-            a.gbark_ref[(int64_t(item) * L.frames + frame) * kBands + lane] = static_cast<float>(ger * r);
-            a.gbark_deg[(int64_t(item) * L.frames + frame) * kBands + lane] = static_cast<float>(ged);
+            a.gbark_ref[(int64_t(item) * L.frames + frame) * nb + lane] = static_cast<float>(ger * r);
+            a.gbark_deg[(int64_t(item) * L.frames + frame) * nb + lane] = static_cast<float>(ged);
             part[local][lane] = ger * Rq;
         }
     }
@@ -781,7 +782,7 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
     if (wave == 0 && live) {
         double s = 0.0;
         for (int f = 0; f < kTile; ++f) s += part[f][lane];
-        region<double>(a.bw, L.grpart)[(int64_t(item) * L.ntile + tile) * kBands + lane] = s;
+        region<double>(a.bw, L.grpart)[(int64_t(item) * L.ntile + tile) * nb + lane] = s;
     }
 }
 
@@ -828,7 +829,7 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, PESQ_STFT_BWD_OCC) stft_bwd
     // powers: wavefront w sums the band partials of tiles w, w + kBwdFrames, ...
     // and every wavefront adds the partial sums in wavefront order
     const double *grp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
-    if (lane < kBands) gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kBwdFrames, lane);
+    if (lane < kBands) gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kBwdFrames, lane, kBands);
     __syncthreads();
     double gm = 0.0;
     if (lane < kBands) {
@@ -916,20 +917,21 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, PESQ_STFT_BWD_OCC) stft_bwd
 __global__ void __launch_bounds__(kWave) chain_partials_kernel(PipeArgs a) {
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
+    const int nb = L.nb;
     const int item = blockIdx.x / L.ntile;
     const int tile = blockIdx.x - item * L.ntile;
     const int t0 = tile * kTile;
     const int lane = threadIdx.x;
-    const bool live = lane < kBands;
+    const bool live = lane < nb;
     const double th100 = live ? 100.0 * t.threshs[lane] : 0.0;
-    const float *bref = a.bark_ref + int64_t(item) * L.frames * kBands;
-    const float *bdeg = a.bark_deg + int64_t(item) * L.frames * kBands;
+    const float *bref = a.bark_ref + int64_t(item) * L.frames * nb;
+    const float *bdeg = a.bark_deg + int64_t(item) * L.frames * nb;
     double pr = 0.0, pd = 0.0;
     for (int local = 0; local < kTile; ++local) {
         const int64_t frame = t0 + local;
         if (frame >= L.frames) break;
-        const double r = live ? static_cast<double>(bref[frame * kBands + lane]) : 0.0;
-        const double d = live ? static_cast<double>(bdeg[frame * kBands + lane]) : 0.0;
+        const double r = live ? static_cast<double>(bref[frame * nb + lane]) : 0.0;
+        const double d = live ? static_cast<double>(bdeg[frame * nb + lane]) : 0.0;
         const double total = wave_sum(live && r > th100 ? r : 0.0);
         const bool keep = total >= 1e7;
         if (lane == 0) region<float>(a.ws, L.keep)[int64_t(item) * L.frames + frame] = keep ? 1.0f : 0.0f;
@@ -937,24 +939,25 @@ __global__ void __launch_bounds__(kWave) chain_partials_kernel(PipeArgs a) {
         if (keep && d > th100) pd += d;
     }
     if (live) {
-        region<double>(a.ws, L.bandref)[(int64_t(item) * L.ntile + tile) * kBands + lane] = pr;
-        region<double>(a.ws, L.banddeg)[(int64_t(item) * L.ntile + tile) * kBands + lane] = pd;
+        region<double>(a.ws, L.bandref)[(int64_t(item) * L.ntile + tile) * nb + lane] = pr;
+        region<double>(a.ws, L.banddeg)[(int64_t(item) * L.ntile + tile) * nb + lane] = pd;
     }
 }
 
 __global__ void __launch_bounds__(kWave) chain_meanpow_kernel(PipeArgs a) {
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
+    const int nb = L.nb;
     const int item = blockIdx.x / L.ntile;
     const int tile = blockIdx.x - item * L.ntile;
     const int t0 = tile * kTile;
     const int lane = threadIdx.x;
-    if (lane >= kBands) return;
-    const double *gp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
+    if (lane >= nb) return;
+    const double *gp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * nb;
     double g = 0.0;  // the summation order of stft_bwd_kernel
-    for (int w = 0; w < kBwdFrames; ++w) g += tile_partial(gp, L.ntile, w, kBwdFrames, lane);
-    const double ratio = band_array(a, kRatio)[item * kBands + lane];
-    const double mref = band_array(a, kMref)[item * kBands + lane];
+    for (int w = 0; w < kBwdFrames; ++w) g += tile_partial(gp, L.ntile, w, kBwdFrames, lane, nb);
+    const double ratio = band_array(a, kRatio)[item * nb + lane];
+    const double mref = band_array(a, kMref)[item * nb + lane];
     const double gr = (ratio >= 0.01 && ratio <= 100.0) ? g : 0.0;
     const double inv = 1.0 / (mref + 1000.0);
     const double frames_f = static_cast<double>(L.frames);
@@ -966,7 +969,7 @@ __global__ void __launch_bounds__(kWave) chain_meanpow_kernel(PipeArgs a) {
         const int64_t frame = t0 + local;
         if (frame >= L.frames) break;
         if (keep[frame] == 0.0f) continue;
-        const int64_t o = (int64_t(item) * L.frames + frame) * kBands + lane;
+        const int64_t o = (int64_t(item) * L.frames + frame) * nb + lane;
         if (static_cast<double>(a.bark_ref[o]) > th100) {
             a.gbark_ref[o] = static_cast<float>(static_cast<double>(a.gbark_ref[o]) + gm_ref);
         }
@@ -1308,37 +1311,43 @@ extern "C" int pesq_pipeline_backward(const float *g_symm, const float *g_asymm,
 // stand-alone chain and STFT entry points
 // ---------------------------------------------------------------------------
 
-static int chain_args(PipeArgs &a, int64_t batch, int64_t frames, const void *model_table) {
+static int chain_args(PipeArgs &a, int64_t batch, int64_t frames, int nbands,
+                      const void *model_table) {
     PESQ_CHECK_ARG(batch > 0, "batch must be positive, got %lld", (long long)batch);
+    PESQ_CHECK_ARG(nbands >= 1 && nbands <= kMaxChainBands, "the chain takes 1 .. %d bands, got %d",
+                   kMaxChainBands, nbands);
     PESQ_CHECK_ARG(frames >= kWin,
                    "The PESQ chain needs at least 20 frames for the overlapping sums, got %lld",
                    (long long)frames);
     PESQ_CHECK_ARG(batch * cdiv(frames, kTile) < (int64_t(1) << 31), "problem too large for one launch");
     PESQ_CHECK_ARG(model_table != nullptr, "null model table");
-    a.L.build_chain(batch, frames);
+    a.L.build_chain(batch, frames, nbands);
     a.tab = static_cast<const ModelTable *>(model_table);
     return PESQ_OK;
 }
 
-extern "C" int pesq_chain_forward_workspace(int64_t batch, int64_t frames, size_t *bytes) {
+extern "C" int pesq_chain_forward_workspace(int64_t batch, int64_t frames, int nbands,
+                                            size_t *bytes) {
     PipeArgs a{};
-    if (int st = chain_args(a, batch, frames, reinterpret_cast<const void *>(1))) return st;
+    if (int st = chain_args(a, batch, frames, nbands, reinterpret_cast<const void *>(1))) return st;
     *bytes = a.L.fwd_bytes;
     return PESQ_OK;
 }
 
-extern "C" int pesq_chain_backward_workspace(int64_t batch, int64_t frames, size_t *bytes) {
+extern "C" int pesq_chain_backward_workspace(int64_t batch, int64_t frames, int nbands,
+                                             size_t *bytes) {
     PipeArgs a{};
-    if (int st = chain_args(a, batch, frames, reinterpret_cast<const void *>(1))) return st;
+    if (int st = chain_args(a, batch, frames, nbands, reinterpret_cast<const void *>(1))) return st;
     *bytes = a.L.bwd_bytes;
     return PESQ_OK;
 }
 
 extern "C" int pesq_chain_forward(const float *ref_bark, const float *deg_bark, int64_t batch,
-                                  int64_t frames, const void *model_table, float *d_symm,
-                                  float *d_asymm, void *fwd_workspace, hipStream_t stream) {
+                                  int64_t frames, int nbands, const void *model_table,
+                                  float *d_symm, float *d_asymm, void *fwd_workspace,
+                                  hipStream_t stream) {
     PipeArgs a{};
-    if (int st = chain_args(a, batch, frames, model_table)) return st;
+    if (int st = chain_args(a, batch, frames, nbands, model_table)) return st;
     PESQ_CHECK_ARG(ref_bark && deg_bark && d_symm && d_asymm && fwd_workspace, "null pointer argument");
     a.ws = static_cast<unsigned char *>(fwd_workspace);
     a.bark_ref = ref_bark;
@@ -1358,11 +1367,11 @@ extern "C" int pesq_chain_forward(const float *ref_bark, const float *deg_bark, 
 
 extern "C" int pesq_chain_backward(const float *g_symm, const float *g_asymm, const float *ref_bark,
                                    const float *deg_bark, int64_t batch, int64_t frames,
-                                   const void *model_table, float *g_ref_bark, float *g_deg_bark,
-                                   const void *fwd_workspace, void *bwd_workspace,
-                                   hipStream_t stream) {
+                                   int nbands, const void *model_table, float *g_ref_bark,
+                                   float *g_deg_bark, const void *fwd_workspace,
+                                   void *bwd_workspace, hipStream_t stream) {
     PipeArgs a{};
-    if (int st = chain_args(a, batch, frames, model_table)) return st;
+    if (int st = chain_args(a, batch, frames, nbands, model_table)) return st;
     PESQ_CHECK_ARG(ref_bark && deg_bark && g_ref_bark && g_deg_bark && fwd_workspace && bwd_workspace,
                    "null pointer argument");
     a.ws = static_cast<unsigned char *>(const_cast<void *>(fwd_workspace));

@@ -25,6 +25,7 @@ struct PipeLayout {
     int64_t nblk = 0, ntile = 0, nhoptile = 0, nwin = 0;
     int64_t row0 = 0, nrg = 0;  // stacked rows that receive gradients
     int grad_mask = 0;
+    int nb = kBands;            // Bark bands (the stand-alone chain takes 1 .. 64)
 
     // forward workspace
     size_t aggr = 0, energy = 0, p = 0, f = 0, rowconst = 0, bark = 0, keep = 0;
@@ -40,6 +41,7 @@ struct PipeLayout {
     }
 
     void build(int64_t b, int64_t n, int mask) {
+        nb = kBands;
         batch = b;
         len = n;
         rows = 2 * b;
@@ -62,19 +64,19 @@ struct PipeLayout {
         take(p, size_t(rows) * len * sizeof(float));
         take(f, size_t(nrg) * len * sizeof(float));
         take(rowconst, size_t(rows) * 4 * sizeof(double));
-        take(bark, size_t(rows) * frames * kBands * sizeof(float));
+        take(bark, size_t(rows) * frames * nb * sizeof(float));
         take(keep, size_t(batch) * frames * sizeof(float));
-        take(bandref, size_t(batch) * ntile * kBands * sizeof(double));
-        take(banddeg, size_t(batch) * ntile * kBands * sizeof(double));
+        take(bandref, size_t(batch) * ntile * nb * sizeof(double));
+        take(banddeg, size_t(batch) * ntile * nb * sizeof(double));
         take(frame, size_t(kFrameArrays) * batch * frames * sizeof(double));
-        take(band, size_t(kBandArrays) * batch * kBands * sizeof(double));
+        take(band, size_t(kBandArrays) * batch * nb * sizeof(double));
         take(psqm, size_t(2) * batch * nwin * sizeof(double));
         take(dist, size_t(batch) * 2 * sizeof(double));
         fwd_bytes = off;
 
         off = 0;
-        take(gbark, size_t(rows) * frames * kBands * sizeof(float));
-        take(grpart, size_t(batch) * ntile * kBands * sizeof(double));
+        take(gbark, size_t(rows) * frames * nb * sizeof(float));
+        take(grpart, size_t(batch) * ntile * nb * sizeof(double));
         take(gp, size_t(nrg) * len * sizeof(float));
         take(spart, size_t(nrg) * nhoptile * sizeof(double));
         take(aggr_b, size_t(scan_workspace_doubles(nrg, nblk)) * sizeof(double));
@@ -83,8 +85,9 @@ struct PipeLayout {
 
     // Regions of the stand-alone perceptual chain over given Bark spectra:
     // only the chain state (forward) and the band partials (backward).
-    void build_chain(int64_t b, int64_t nframes) {
+    void build_chain(int64_t b, int64_t nframes, int nbands) {
         *this = PipeLayout();
+        nb = nbands;
         batch = b;
         rows = 2 * b;
         frames = nframes;
@@ -96,15 +99,15 @@ struct PipeLayout {
             off = align(off + bytes);
         };
         take(keep, size_t(batch) * frames * sizeof(float));
-        take(bandref, size_t(batch) * ntile * kBands * sizeof(double));
-        take(banddeg, size_t(batch) * ntile * kBands * sizeof(double));
+        take(bandref, size_t(batch) * ntile * nb * sizeof(double));
+        take(banddeg, size_t(batch) * ntile * nb * sizeof(double));
         take(frame, size_t(kFrameArrays) * batch * frames * sizeof(double));
-        take(band, size_t(kBandArrays) * batch * kBands * sizeof(double));
+        take(band, size_t(kBandArrays) * batch * nb * sizeof(double));
         take(psqm, size_t(2) * batch * nwin * sizeof(double));
         take(dist, size_t(batch) * 2 * sizeof(double));
         fwd_bytes = off;
         off = 0;
-        take(grpart, size_t(batch) * ntile * kBands * sizeof(double));
+        take(grpart, size_t(batch) * ntile * nb * sizeof(double));
         bwd_bytes = off;
     }
 

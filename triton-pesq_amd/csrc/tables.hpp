@@ -8,6 +8,8 @@
 
 namespace pesq {
 
+constexpr int kMaxChainBands = kWave;  // one band per lane
+
 struct ModelTable {
     IirTable iir;                 // A = level alignment band pass, B = pre-emphasis
     double2 tw256[kHalf];         // e^{-2 pi i m / 256}
@@ -17,10 +19,11 @@ struct ModelTable {
     int32_t band_end[kBands];     // one past the last bin of band i
     int32_t bin_band[kHalf];      // band owning bin f, -1 if none (bin 0 is -1)
     double corr[kBands];          // power density correction per band
-    double threshs[kBands];       // hearing thresholds
-    double exps[kBands];          // Zwicker exponents
-    double loud_scale[kBands];    // sl (2 th)^e
-    double width[kBands];         // band widths in Bark
+    // per band chain constants (the stand-alone chain takes up to 64 bands)
+    double threshs[kMaxChainBands];     // hearing thresholds
+    double exps[kMaxChainBands];        // Zwicker exponents
+    double loud_scale[kMaxChainBands];  // sl (2 th)^e
+    double width[kMaxChainBands];       // band widths in Bark
     double total_width;           // sum of widths of bands 1..
     double sl;                    // loudness calibration constant
     int32_t nbarks;

@@ -142,10 +142,11 @@ SIGNATURES = {
     "pesq_stft_workspace": (_INT, [_I64, _I64, _I64, _INT, _INT, _SIZE_P]),
     "pesq_stft_forward": (_INT, [_P, _I64, _I64, _I64, _P, _INT, _INT, _INT, _P, _P]),
     "pesq_stft_backward": (_INT, [_P, _P, _I64, _I64, _I64, _P, _INT, _INT, _INT, _P, _P, _P]),
-    "pesq_chain_forward_workspace": (_INT, [_I64, _I64, _SIZE_P]),
-    "pesq_chain_backward_workspace": (_INT, [_I64, _I64, _SIZE_P]),
-    "pesq_chain_forward": (_INT, [_P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
-    "pesq_chain_backward": (_INT, [_P, _P, _P, _P, _I64, _I64, _P, _P, _P, _P, _P, _P]),
+    "pesq_chain_forward_workspace": (_INT, [_I64, _I64, _INT, _SIZE_P]),
+    "pesq_chain_backward_workspace": (_INT, [_I64, _I64, _INT, _SIZE_P]),
+    "pesq_chain_table_pack": (_INT, [_INT, _P, _P, _P, ctypes.c_double, ctypes.c_double, _P]),
+    "pesq_chain_forward": (_INT, [_P, _P, _I64, _I64, _INT, _P, _P, _P, _P, _P]),
+    "pesq_chain_backward": (_INT, [_P, _P, _P, _P, _I64, _I64, _INT, _P, _P, _P, _P, _P, _P]),
     "pesq_elementwise_workspace": (_INT, [_I64, _SIZE_P]),
     "pesq_peak_normalize_forward": (_INT, [_P, _P, _I64, _I64, _P, _P, _P, _P, _P]),
     "pesq_peak_normalize_backward": (_INT, [_P, _P, _P, _I64, _I64, _P, _P, _P]),

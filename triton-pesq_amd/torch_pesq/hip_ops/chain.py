@@ -12,23 +12,41 @@ import torch
 
 from .. import _lib
 from ._common import check_input
-from .pipeline import pack_model_table
 
 __all__ = ["HipPesqChain"]
+
+#: bands of the stand-alone chain, one per lane of a wavefront
+_MAX_BANDS = 64
+
+
+def _pack_chain(threshs, exps, widths, total_width, sl) -> torch.Tensor:
+    import ctypes
+
+    import numpy as np
+
+    lib = _lib.library()
+    cols = [np.ascontiguousarray(v.detach().cpu().double().numpy()) for v in (threshs, exps, widths)]
+    buf = (ctypes.c_ubyte * lib.pesq_model_table_bytes())()
+    _lib.check(
+        lib.pesq_chain_table_pack(cols[0].shape[0], *[c.ctypes.data_as(ctypes.c_void_p) for c in cols],
+                                  float(total_width), float(sl), buf),
+        "pesq_chain_table_pack",
+    )
+    return torch.frombuffer(bytearray(buf), dtype=torch.uint8).clone()
 
 
 class _ChainFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, ref, deg, module):
-        batch, frames, _ = ref.shape
+        batch, frames, nb = ref.shape
         lib = _lib.library()
-        ws_bytes = _lib.size_query(lib.pesq_chain_forward_workspace, batch, frames)
+        ws_bytes = _lib.size_query(lib.pesq_chain_forward_workspace, batch, frames, nb)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=ref.device)
         d_symm = torch.empty(batch, device=ref.device)
         d_asymm = torch.empty(batch, device=ref.device)
         with torch.cuda.device(ref.device):
             _lib.check(
-                lib.pesq_chain_forward(_lib.ptr(ref), _lib.ptr(deg), batch, frames,
+                lib.pesq_chain_forward(_lib.ptr(ref), _lib.ptr(deg), batch, frames, nb,
                                        _lib.ptr(module.table), _lib.ptr(d_symm), _lib.ptr(d_asymm),
                                        _lib.ptr(ws), _lib.stream_handle(ref.device)),
                 "pesq_chain_forward",
@@ -44,9 +62,9 @@ class _ChainFunction(torch.autograd.Function):
         ref, deg, ws = ctx.saved_tensors
         if g_symm is None and g_asymm is None:
             return None, None, None
-        batch, frames, _ = ref.shape
+        batch, frames, nb = ref.shape
         lib = _lib.library()
-        bw_bytes = _lib.size_query(lib.pesq_chain_backward_workspace, batch, frames)
+        bw_bytes = _lib.size_query(lib.pesq_chain_backward_workspace, batch, frames, nb)
         scratch = torch.empty(bw_bytes, dtype=torch.uint8, device=ref.device)
         g_ref, g_deg = torch.empty_like(ref), torch.empty_like(deg)
         g_symm = None if g_symm is None else g_symm.contiguous().float()
@@ -54,7 +72,7 @@ class _ChainFunction(torch.autograd.Function):
         with torch.cuda.device(ref.device):
             _lib.check(
                 lib.pesq_chain_backward(_lib.ptr(g_symm), _lib.ptr(g_asymm), _lib.ptr(ref),
-                                        _lib.ptr(deg), batch, frames, _lib.ptr(ctx.module.table),
+                                        _lib.ptr(deg), batch, frames, nb, _lib.ptr(ctx.module.table),
                                         _lib.ptr(g_ref), _lib.ptr(g_deg), _lib.ptr(ws),
                                         _lib.ptr(scratch), _lib.stream_handle(ref.device)),
                 "pesq_chain_backward",
@@ -85,21 +103,19 @@ class HipPesqChain(torch.nn.Module):
             )
         if torch.any(threshs <= 0):
             raise ValueError("Hearing thresholds have to be strictly positive.")
-        if threshs.numel() != _lib.NBARKS:
-            raise ValueError(f"The HIP chain needs {_lib.NBARKS} bands, got {threshs.numel()}.")
+        if threshs.numel() > _MAX_BANDS:
+            raise ValueError(
+                f"The HIP chain takes at most {_MAX_BANDS} bands (one per lane of a "
+                f"wavefront), got {threshs.numel()}."
+            )
         self.total_width, self.sl = float(total_width), float(sl)
         self.register_buffer("threshs", threshs.float())
         self.register_buffer("exp", exps.float())
         self.register_buffer("width_bark", widths.float())
-        # the binary default filterbank and a flat window only fill the table;
-        # the chain reads thresholds, exponents, widths and sl
-        fbank = torch.zeros(_lib.NBARKS, 256)
-        for band in range(_lib.NBARKS):
-            fbank[band, band] = 1.0
-        table = pack_model_table(None, None, None, None, torch.ones(512), fbank,
-                                 torch.ones(_lib.NBARKS), threshs, exps, widths,
-                                 self.total_width, self.sl)
-        self.register_buffer("table", table, persistent=False)
+        # float32 buffers like the reference's (chain.py:1060-1076); the kernels
+        # evaluate the chain in float64 from the float64 constants
+        self.register_buffer("table", _pack_chain(threshs, exps, widths, self.total_width,
+                                                  self.sl), persistent=False)
 
     def forward(self, ref_bark: torch.Tensor, deg_bark: torch.Tensor):
         """``(d_symm, d_asymm)``, both ``[batch]``."""
