@@ -41,6 +41,12 @@ namespace pesq {
 #define PESQ_CHUNK 16
 #endif
 constexpr int kChunk = PESQ_CHUNK;                         // samples per lane
+// Lane states: for grids of up to kLaneStateWaves wavefronts (latency bound)
+// the aggregate pass stores every lane's in-block start state and the output
+// pass reads it; larger grids (bandwidth bound) skip that traffic and the
+// output pass repeats the zero state run and the in-wave scan.  Both compute
+// the same states with the same operations.
+constexpr int64_t kLaneStateWaves = 16384;
 constexpr int kSpan = kWave * kChunk;                      // samples per block
 constexpr int64_t kBlockSpan = kSpan;
 constexpr int kMaxSections = PESQ_IIR_MAX_SECTIONS;
@@ -169,6 +175,57 @@ __device__ __forceinline__ void scan_wave(const IirTable &t, int level0, Bank<NS
     }
 }
 
+// The same inclusive scan with DPP lane moves instead of LDS crossbar
+// shuffles (GFX9 DPP, 64-bit values as two 32-bit moves): Kogge-Stone over
+// the 16 lanes of each row (row_shr 1, 2, 4, 8; lanes shifted in from
+// outside the row read 0), then the last lane of row 0 (of row 2) is carried
+// into row 1 (row 3) with row_bcast:15, and the last lane of row 1 into rows 2
+// and 3 with row_bcast:31, each lane scaling the carry by A^(kChunk m), m its
+// distance in chunks from the carried lane (lane_pw).  For level0 = 0 only.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ double dpp_move(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), kCtrl, kRowMask, 0xF, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), kCtrl, kRowMask, 0xF, true);
+    return __hiloint2double(hi, lo);
+}
+
+template <int kCtrl, int kRowMask, int S0, int NS>
+__device__ __forceinline__ void dpp_level(const double *const (&pw)[NS > 0 ? NS : 1], Bank<NS> &z) {
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const double ou = dpp_move<kCtrl, kRowMask>(z.u[k]);
+        const double ov = dpp_move<kCtrl, kRowMask>(z.v[k]);
+        const double *p = pw[k];
+        z.u[k] = fma(p[0], ou, fma(p[1], ov, z.u[k]));
+        z.v[k] = fma(p[2], ou, fma(p[3], ov, z.v[k]));
+    }
+}
+
+template <int S0, int NS>
+__device__ __forceinline__ void scan_wave_dpp(const IirTable &t, Bank<NS> &z, int lane) {
+    const double *pw[NS > 0 ? NS : 1];
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.pw[0][S0 + k];
+    dpp_level<0x111, 0xF, S0, NS>(pw, z);  // row_shr:1
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.pw[1][S0 + k];
+    dpp_level<0x112, 0xF, S0, NS>(pw, z);  // row_shr:2
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.pw[2][S0 + k];
+    dpp_level<0x114, 0xF, S0, NS>(pw, z);  // row_shr:4
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.pw[3][S0 + k];
+    dpp_level<0x118, 0xF, S0, NS>(pw, z);  // row_shr:8
+    // rows 1 and 3: + A^(kChunk ((lane & 15) + 1)) (lane 15 of rows 0 and 2)
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.lane_pw[S0 + k][(lane & 15) + 1];
+    dpp_level<0x142, 0xA, S0, NS>(pw, z);  // row_bcast:15
+    // rows 2 and 3: + A^(kChunk (lane - 31)) (lane 31)
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.lane_pw[S0 + k][lane >= 32 ? lane - 31 : 0];
+    dpp_level<0x143, 0xC, S0, NS>(pw, z);  // row_bcast:31
+}
+
 template <int NA, int NB>
 struct BankPair {
     Bank<NA> a;
@@ -181,6 +238,11 @@ struct BankPair {
     __device__ __forceinline__ void scan(const IirTable &t, int level0, int lane) {
         if constexpr (NA > 0) scan_wave<0, NA>(t, level0, a, lane);
         if constexpr (NB > 0) scan_wave<NA, NB>(t, level0, b, lane);
+    }
+    // the in-wave chunk scan (level0 = 0) with DPP moves
+    __device__ __forceinline__ void scan_chunks(const IirTable &t, int lane) {
+        if constexpr (NA > 0) scan_wave_dpp<0, NA>(t, a, lane);
+        if constexpr (NB > 0) scan_wave_dpp<NA, NB>(t, b, lane);
     }
     __device__ __forceinline__ void power(const IirTable &t, int level, const BankPair &add) {
         if constexpr (NA > 0) apply_power<0, NA>(t, level, a, add.a);
@@ -366,7 +428,7 @@ __device__ __forceinline__ void output_run(const Mode &m, const Coeffs<0, NA, Mo
     }
 }
 
-template <int NA, int NB, class Mode>
+template <int NA, int NB, class Mode, bool kLaneStates>
 __global__ void __launch_bounds__(kWave)
     iir_aggregate_kernel(Mode m, const IirTable *__restrict__ table, double *__restrict__ aggr,
                          double *__restrict__ lanes, int64_t len, int nblk) {
@@ -391,7 +453,7 @@ __global__ void __launch_bounds__(kWave)
     } else {
         zero_run<false>(m, ca, cb, in, j0, len, s);
     }
-    s.scan(t, 0, lane);
+    s.scan_chunks(t, lane);
     if (lane == kWave - 1) {
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
@@ -400,12 +462,14 @@ __global__ void __launch_bounds__(kWave)
             dst[1] = s.v(k);
         }
     }
+    if constexpr (!kLaneStates) return;
     // start state of every lane's chunk (the end state of the chunk before it)
     double2 *dst = reinterpret_cast<double2 *>(lanes) + (int64_t(row) * nblk + blk) * NS * kWave;
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
-        const double u = shfl_up(s.u(k), 1), v = shfl_up(s.v(k), 1);
-        dst[k * kWave + lane] = lane == 0 ? make_double2(0.0, 0.0) : make_double2(u, v);
+        // wave_shr:1 (lane 0 reads 0)
+        const double u = dpp_move<0x138, 0xF>(s.u(k)), v = dpp_move<0x138, 0xF>(s.v(k));
+        dst[k * kWave + lane] = make_double2(u, v);
     }
 }
 
@@ -460,7 +524,7 @@ __global__ void __launch_bounds__(kWave *kPrefixWaves)
     }
 }
 
-template <int NA, int NB, class Mode>
+template <int NA, int NB, class Mode, bool kLaneStates>
 __global__ void __launch_bounds__(kWave)
     iir_output_kernel(Mode m, const IirTable *__restrict__ table,
                       const double *__restrict__ aggr, const double *__restrict__ lanes,
@@ -482,7 +546,7 @@ __global__ void __launch_bounds__(kWave)
         p.v(k) = src[1];
     }
     BankPair<NA, NB> s;
-    {
+    if constexpr (kLaneStates) {
         const double2 *src =
             reinterpret_cast<const double2 *>(lanes) + (int64_t(row) * nblk + blk) * NS * kWave;
 #pragma unroll
@@ -496,9 +560,28 @@ __global__ void __launch_bounds__(kWave)
     m.setup(row, sh, lane);
     typename Mode::In in[kChunk][Mode::kInputs];
     load_chunk(m, row, j0, len, in);
+    const IirTable &t2 = *table;
+    if constexpr (!kLaneStates) {
+        // the in-block start states again: zero state run, scan, shift by a lane
+        Coeffs<0, NA, Mode::kB2> za;
+        Coeffs<NA, NB, Mode::kB2> zb;
+        za.load(t2, t2.c0a);
+        zb.load(t2, t2.c0b);
+        s.zero();
+        if (general_chunk(j0, len)) {
+            zero_run<true>(m, za, zb, in, j0, len, s);
+        } else {
+            zero_run<false>(m, za, zb, in, j0, len, s);
+        }
+        s.scan_chunks(t2, lane);
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+            s.u(k) = dpp_move<0x138, 0xF>(s.u(k));
+            s.v(k) = dpp_move<0x138, 0xF>(s.v(k));
+        }
+    }
 
     // lane start state = (start state given a zero block start) + A^(kChunk lane) p
-    const IirTable &t2 = *table;
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
         const double *lp = t2.lane_pw[k][lane];
@@ -543,9 +626,16 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
     double *lanes = ws + scan_aggr_doubles(rows, nblk, NS);
     const unsigned grid = static_cast<unsigned>(rows * nblk);
     if (grid == 0) return PESQ_OK;
+    const bool lane_states = grid <= kLaneStateWaves;
     if (aggregate) {
-        hipLaunchKernelGGL((iir_aggregate_kernel<NA, NB, Mode>), dim3(grid), dim3(kWave), 0,
-                           stream, m, table, aggr, lanes, len, static_cast<int>(nblk));
+        if (lane_states) {
+            hipLaunchKernelGGL((iir_aggregate_kernel<NA, NB, Mode, true>), dim3(grid), dim3(kWave),
+                               0, stream, m, table, aggr, lanes, len, static_cast<int>(nblk));
+        } else {
+            hipLaunchKernelGGL((iir_aggregate_kernel<NA, NB, Mode, false>), dim3(grid),
+                               dim3(kWave), 0, stream, m, table, aggr, lanes, len,
+                               static_cast<int>(nblk));
+        }
         PESQ_CHECK_LAUNCH("iir aggregate");
         const int64_t nseq = rows * NS;
         hipLaunchKernelGGL(iir_prefix_kernel<NS>,
@@ -555,9 +645,15 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
         PESQ_CHECK_LAUNCH("iir prefix");
     }
     if (output) {
-        hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode>), dim3(grid), dim3(kWave), 0, stream,
-                           m, table, static_cast<const double *>(aggr),
-                           static_cast<const double *>(lanes), len, static_cast<int>(nblk));
+        if (lane_states) {
+            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true>), dim3(grid), dim3(kWave), 0,
+                               stream, m, table, static_cast<const double *>(aggr),
+                               static_cast<const double *>(lanes), len, static_cast<int>(nblk));
+        } else {
+            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, false>), dim3(grid), dim3(kWave),
+                               0, stream, m, table, static_cast<const double *>(aggr),
+                               static_cast<const double *>(lanes), len, static_cast<int>(nblk));
+        }
         PESQ_CHECK_LAUNCH("iir output");
     }
     return PESQ_OK;
