@@ -791,10 +791,7 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
 // ---------------------------------------------------------------------------
 
 template <typename real>
-#ifndef PESQ_STFT_BWD_OCC
-#define PESQ_STFT_BWD_OCC 4
-#endif
-__global__ void __launch_bounds__(kWave *kBwdFrames, PESQ_STFT_BWD_OCC) stft_bwd_kernel(PipeArgs a) {
+__global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs a) {
     __shared__ cplx<real> fftbuf[kBwdFrames][kHalf];
     __shared__ float contrib[kBwdFrames][kNfft];
     __shared__ double gpart[kBwdFrames][kBands];
@@ -845,8 +842,8 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, PESQ_STFT_BWD_OCC) stft_bwd
     const double scale = region<double>(a.ws, L.rowconst)[int64_t(row) * 4 + 2];
     cplx<real> *buf = fftbuf[wave];
     if (live) {
-        Twiddles tw;
-        tw.load(t.tw256, t.tw512, lane);
+        // twiddles read per pass (fewer live registers: five wavefronts per SIMD)
+        const LazyTwiddles tw{reload(t.tw256), reload(t.tw512), lane};
         float win[8];
         int bin_band[4];
 #pragma unroll
@@ -1090,13 +1087,18 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_plain_bwd_kernel(StftA
 // host entry points
 // ---------------------------------------------------------------------------
 
-// FFT arithmetic of the STFT kernels.  float64 costs no measurable time on
-// gfx950 (both kernels are latency bound, float64 FMA issues at the float32
+// FFT arithmetic of the forward STFT kernels and the stand-alone operator.
+// float64 costs no measurable time there (float64 FMA issues at the float32
 // rate with packed float32 disabled) and cuts the spectral rounding error.
 #ifndef PESQ_STFT_REAL
 #define PESQ_STFT_REAL double
 #endif
 using StftReal = PESQ_STFT_REAL;
+// The backward's FFTs (spectrum recomputed, adjoint) run in float32: fewer
+// registers (five wavefronts per SIMD instead of four; 20.3 instead of 22.9 us
+// at BASELINE c2) for a gradient error of about 2e-6 of its peak instead of
+// 5e-7 (the forward Bark spectra, and so the distances, stay float64).
+using StftBwdReal = float;
 
 // Chain launches: up to about two workgroups per CU of the 256 CU MI355X the
 // kernels are latency bound and run one frame (backward) or two (forward) per
@@ -1271,7 +1273,7 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
         PESQ_CHECK_LAUNCH("pipeline chain backward");
     }
     if (stages & 2u) {
-        hipLaunchKernelGGL(stft_bwd_kernel<StftReal>,
+        hipLaunchKernelGGL(stft_bwd_kernel<StftBwdReal>,
                            dim3(static_cast<unsigned>(L.nrg * L.nhoptile)),
                            dim3(kWave * kBwdFrames), 0, stream, a);
         PESQ_CHECK_LAUNCH("pipeline stft backward");
