@@ -221,7 +221,7 @@ STAGES = {
     "fwd_stft": ("fwd", 0x4, ["stft_fwd_kernel<double,false>"]),
     "fwd_chain": ("fwd", 0x18, ["chain_fwd_kernel<8>", "chain_final_kernel"]),
     "bwd_chain": ("bwd", 0x1, ["chain_bwd_kernel<16>"]),
-    "bwd_stft": ("bwd", 0x2, ["stft_bwd_kernel<double>"]),
+    "bwd_stft": ("bwd", 0x2, ["stft_bwd_kernel<float>"]),
     "bwd_scans": ("bwd", 0xC, ["iir_aggregate_kernel<5,1,PipeBwdMode,true>", "iir_prefix_kernel<6>",
                                "iir_output_kernel<5,1,PipeBwdMode,true>"]),
 }
