@@ -23,7 +23,9 @@
 //              laid out [row][block][section][lane][2];
 //   prefix:    per (row, section) an exclusive scan of the block aggregates,
 //              written over them (aggr[b] becomes the state at the start of
-//              block b), one wavefront per sequence;
+//              block b), one wavefront per sequence; small grids of short rows
+//              skip it and the output pass reduces the aggregates before its
+//              block instead (block_start_*);
 //   output:    lane start state = lanes[lane] + A^(kChunk lane) aggr[block];
 //              run from it; per sample y = c0 x + y_0 + y_1 + ... in this order.
 // The time axis can be reversed (adjoint filter) by the Mode policy.
@@ -201,8 +203,8 @@ __device__ __forceinline__ void dpp_level(const double *const (&pw)[NS > 0 ? NS 
     }
 }
 
-template <int S0, int NS>
-__device__ __forceinline__ void scan_wave_dpp(const IirTable &t, Bank<NS> &z, int lane) {
+template <int S0, int NS, class Powers>
+__device__ __forceinline__ void scan_wave_dpp(const Powers &t, Bank<NS> &z, int lane) {
     const double *pw[NS > 0 ? NS : 1];
 #pragma unroll
     for (int k = 0; k < NS; ++k) pw[k] = t.pw[0][S0 + k];
@@ -226,6 +228,83 @@ __device__ __forceinline__ void scan_wave_dpp(const IirTable &t, Bank<NS> &z, in
     dpp_level<0x143, 0xC, S0, NS>(pw, z);  // row_bcast:31
 }
 
+// Small grids (those that keep lane states) of rows of up to
+// kFusedPrefixBlocks blocks skip the prefix pass: every output wavefront
+// derives its block's start state from the block aggregates itself
+// (block_start_load, block_start_reduce).  Large grids keep the separate
+// prefix kernel, whose work is not repeated per block.
+#ifndef PESQ_FUSED_PREFIX_BLOCKS
+#define PESQ_FUSED_PREFIX_BLOCKS 128
+#endif
+constexpr int kFusedPrefixBlocks = PESQ_FUSED_PREFIX_BLOCKS;
+static_assert(kFusedPrefixBlocks <= 2 * kWave, "two blocks per lane");
+
+// Start state of block `blk` of a row from the zero start end states e_j of
+// the blocks before it (row_aggr, laid out [section][block][2]):
+//     p = sum_{j < blk} M^(blk - 1 - j) e_j,  M = A^kSpan per section.
+// Lane i holds blocks j0 = blk - 128 + 2 i and j0 + 1 (0 before the row
+// start) and combines them as M e_j0 + e_j0+1; the DPP scan steps with the
+// uniform powers M^(2 2^l) then reduce the lanes exactly onto lane 63 (row
+// shifts 1, 2, 4, 8 leave each row's weighted sum in its last lane,
+// row_bcast:15 adds row 2 to lane 63 with M^32 and row_bcast:31 lanes 0..31
+// with M^64; the other lanes hold partial sums).  The loads are issued first
+// so that they overlap the kernel's other loads.
+template <int NS>
+__device__ __forceinline__ void block_start_load(const double *row_aggr, int nblk, int blk,
+                                                 int lane, Bank<NS> &e0, Bank<NS> &e1) {
+    const int j0 = blk - 2 * kWave + 2 * lane;
+    const int c0 = j0 >= 0 ? j0 : 0, c1 = j0 + 1 >= 0 ? j0 + 1 : 0;
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const double *sec = row_aggr + int64_t(k) * nblk * 2;
+        const double2 a = *reinterpret_cast<const double2 *>(sec + 2 * c0);
+        const double2 b = *reinterpret_cast<const double2 *>(sec + 2 * c1);
+        e0.u[k] = j0 >= 0 ? a.x : 0.0;
+        e0.v[k] = j0 >= 0 ? a.y : 0.0;
+        e1.u[k] = j0 + 1 >= 0 ? b.x : 0.0;
+        e1.v[k] = j0 + 1 >= 0 ? b.y : 0.0;
+    }
+}
+
+template <int NS, class Powers>
+__device__ __forceinline__ void block_start_reduce(const Powers &t, Bank<NS> &z,
+                                                   const Bank<NS> &e1) {
+    const double *pw[NS];
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock][k];
+    // z = M e_j0 + e_j0+1
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const double *m = pw[k];
+        const double u = z.u[k], v = z.v[k];
+        z.u[k] = fma(m[0], u, fma(m[1], v, e1.u[k]));
+        z.v[k] = fma(m[2], u, fma(m[3], v, e1.v[k]));
+    }
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock + 1][k];
+    dpp_level<0x111, 0xF, 0, NS>(pw, z);  // row_shr:1
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock + 2][k];
+    dpp_level<0x112, 0xF, 0, NS>(pw, z);  // row_shr:2
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock + 3][k];
+    dpp_level<0x114, 0xF, 0, NS>(pw, z);  // row_shr:4
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock + 4][k];
+    dpp_level<0x118, 0xF, 0, NS>(pw, z);  // row_shr:8
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock + 5][k];
+    dpp_level<0x142, 0xA, 0, NS>(pw, z);  // row_bcast:15
+#pragma unroll
+    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock + 6][k];
+    dpp_level<0x143, 0xC, 0, NS>(pw, z);  // row_bcast:31
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        z.u[k] = read_lane(z.u[k], kWave - 1);
+        z.v[k] = read_lane(z.v[k], kWave - 1);
+    }
+}
+
 template <int NA, int NB>
 struct BankPair {
     Bank<NA> a;
@@ -240,7 +319,8 @@ struct BankPair {
         if constexpr (NB > 0) scan_wave<NA, NB>(t, level0, b, lane);
     }
     // the in-wave chunk scan (level0 = 0) with DPP moves
-    __device__ __forceinline__ void scan_chunks(const IirTable &t, int lane) {
+    template <class Powers>
+    __device__ __forceinline__ void scan_chunks(const Powers &t, int lane) {
         if constexpr (NA > 0) scan_wave_dpp<0, NA>(t, a, lane);
         if constexpr (NB > 0) scan_wave_dpp<NA, NB>(t, b, lane);
     }
@@ -524,12 +604,13 @@ __global__ void __launch_bounds__(kWave *kPrefixWaves)
     }
 }
 
-template <int NA, int NB, class Mode, bool kLaneStates>
+template <int NA, int NB, class Mode, bool kLaneStates, bool kFusedPrefix>
 __global__ void __launch_bounds__(kWave)
     iir_output_kernel(Mode m, const IirTable *__restrict__ table,
                       const double *__restrict__ aggr, const double *__restrict__ lanes,
                       int64_t len, int nblk) {
     constexpr int NS = NA + NB;
+    static_assert(kLaneStates || !kFusedPrefix, "the fused prefix is for small grids");
     const int row = blockIdx.x / nblk;
     const int blk = blockIdx.x - row * nblk;
     const int lane = threadIdx.x;
@@ -539,11 +620,16 @@ __global__ void __launch_bounds__(kWave)
     // states, the lane start states, the row constants and the raw inputs
     const double *row_aggr = aggr + int64_t(row) * NS * nblk * 2;
     BankPair<NA, NB> p;
+    Bank<NS> e0, e1;  // kFusedPrefix: the block aggregates this block starts from
+    if constexpr (kFusedPrefix) {
+        block_start_load<NS>(row_aggr, nblk, blk, lane, e0, e1);
+    } else {
 #pragma unroll
-    for (int k = 0; k < NS; ++k) {
-        const double *src = row_aggr + (int64_t(k) * nblk + blk) * 2;
-        p.u(k) = src[0];
-        p.v(k) = src[1];
+        for (int k = 0; k < NS; ++k) {
+            const double *src = row_aggr + (int64_t(k) * nblk + blk) * 2;
+            p.u(k) = src[0];
+            p.v(k) = src[1];
+        }
     }
     BankPair<NA, NB> s;
     if constexpr (kLaneStates) {
@@ -561,6 +647,14 @@ __global__ void __launch_bounds__(kWave)
     typename Mode::In in[kChunk][Mode::kInputs];
     load_chunk(m, row, j0, len, in);
     const IirTable &t2 = *table;
+    if constexpr (kFusedPrefix) {
+        block_start_reduce<NS>(t2, e0, e1);
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+            p.u(k) = e0.u[k];
+            p.v(k) = e0.v[k];
+        }
+    }
     if constexpr (!kLaneStates) {
         // the in-block start states again: zero state run, scan, shift by a lane
         Coeffs<0, NA, Mode::kB2> za;
@@ -627,6 +721,7 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
     const unsigned grid = static_cast<unsigned>(rows * nblk);
     if (grid == 0) return PESQ_OK;
     const bool lane_states = grid <= kLaneStateWaves;
+    const bool fused = lane_states && nblk <= kFusedPrefixBlocks;
     if (aggregate) {
         if (lane_states) {
             hipLaunchKernelGGL((iir_aggregate_kernel<NA, NB, Mode, true>), dim3(grid), dim3(kWave),
@@ -637,22 +732,28 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
                                static_cast<int>(nblk));
         }
         PESQ_CHECK_LAUNCH("iir aggregate");
-        const int64_t nseq = rows * NS;
-        hipLaunchKernelGGL(iir_prefix_kernel<NS>,
-                           dim3(static_cast<unsigned>(cdiv(nseq, kPrefixWaves))),
-                           dim3(kWave * kPrefixWaves), 0, stream, table, aggr,
-                           static_cast<int>(nblk), nseq);
-        PESQ_CHECK_LAUNCH("iir prefix");
+        if (!fused) {
+            const int64_t nseq = rows * NS;
+            hipLaunchKernelGGL(iir_prefix_kernel<NS>,
+                               dim3(static_cast<unsigned>(cdiv(nseq, kPrefixWaves))),
+                               dim3(kWave * kPrefixWaves), 0, stream, table, aggr,
+                               static_cast<int>(nblk), nseq);
+            PESQ_CHECK_LAUNCH("iir prefix");
+        }
     }
     if (output) {
-        if (lane_states) {
-            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true>), dim3(grid), dim3(kWave), 0,
-                               stream, m, table, static_cast<const double *>(aggr),
-                               static_cast<const double *>(lanes), len, static_cast<int>(nblk));
+        const double *ca = aggr;
+        const double *cl = lanes;
+        const int nb = static_cast<int>(nblk);
+        if (fused) {
+            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, true>), dim3(grid),
+                               dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
+        } else if (lane_states) {
+            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, false>), dim3(grid),
+                               dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
         } else {
-            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, false>), dim3(grid), dim3(kWave),
-                               0, stream, m, table, static_cast<const double *>(aggr),
-                               static_cast<const double *>(lanes), len, static_cast<int>(nblk));
+            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, false, false>), dim3(grid),
+                               dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
         }
         PESQ_CHECK_LAUNCH("iir output");
     }
