@@ -213,9 +213,12 @@ constexpr int kStftWaves = 8;
 // kLean: the variant for grids of several workgroups per CU, which keeps
 // fewer values live (no next-frame prefetch, twiddles read again per frame,
 // a rolled band sum) so that more wavefronts fit per SIMD.
-template <typename real, bool kLean>
-__global__ void __launch_bounds__(kWave *kStftWaves, kLean ? 4 : 1) stft_fwd_kernel(PipeArgs a) {
-    __shared__ cplx<real> fftbuf[kStftWaves][kHalf];
+template <typename real, bool kLean, int kWaves = kStftWaves>
+__global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(PipeArgs a) {
+    constexpr int kSideWaves = kWaves / 2;            // wavefronts per side
+    constexpr int kPerWave = 2 * kTile / kWaves;      // frames per wavefront
+    static_assert(kSideWaves * kPerWave == kTile, "a tile per side");
+    __shared__ cplx<real> fftbuf[kWaves][kHalf];
     __shared__ float barks[2][kTile][kBands];
     __shared__ float keepflag[kTile];
 
@@ -226,12 +229,12 @@ __global__ void __launch_bounds__(kWave *kStftWaves, kLean ? 4 : 1) stft_fwd_ker
     const int t0 = tile * kTile;
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
-    const int side = wave / 4;                   // 0 = reference, 1 = degraded
+    const int side = wave / kSideWaves;          // 0 = reference, 1 = degraded
     const int row = side * L.batch + item;
 
     // samples of this wavefront's first frame, requested before anything else
     const float *p = region<float>(a.ws, L.p) + int64_t(row) * L.len;
-    const int64_t f_first = t0 + (wave & 3) * 4;
+    const int64_t f_first = t0 + (wave % kSideWaves) * kPerWave;
     float cur[8];
     load_frame(p, (f_first < L.frames ? f_first : L.frames - 1) * kHop, L.len, lane, cur);
 
@@ -242,7 +245,7 @@ __global__ void __launch_bounds__(kWave *kStftWaves, kLean ? 4 : 1) stft_fwd_ker
     e = wave_sum(e);
     const double power = e / static_cast<double>(L.len + 5120) / 1.04684;
     const double scale = sqrt(1e7 / power);
-    if (tile == 0 && (wave & 3) == 0 && lane == 0) {
+    if (tile == 0 && wave % kSideWaves == 0 && lane == 0) {
         double *rc = region<double>(a.ws, L.rowconst) + int64_t(row) * 4;
         rc[0] = 1.0;
         rc[1] = e;
@@ -275,8 +278,8 @@ __global__ void __launch_bounds__(kWave *kStftWaves, kLean ? 4 : 1) stft_fwd_ker
     const double corr = lane < kBands ? t.corr[lane] : 0.0;
     const double th100 = lane < kBands ? 100.0 * t.threshs[lane] : 0.0;
 
-    for (int q = 0; q < 4; ++q) {
-        const int local = (wave & 3) * 4 + q;
+    for (int q = 0; q < kPerWave; ++q) {
+        const int local = (wave % kSideWaves) * kPerWave + q;
         const int64_t frame = t0 + local;
         if (frame >= L.frames) break;
         // the next frame's samples load while this one is transformed
@@ -517,39 +520,48 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
 
 constexpr int kFinalThreads = 256;
 
-__device__ __forceinline__ double block_sum(double v, double *scratch) {
-    const int wave = threadIdx.x / kWave;
-    v = wave_sum(v);
-    if ((threadIdx.x % kWave) == 0) scratch[wave] = v;
-    __syncthreads();
-    double total = 0.0;
-    for (int i = 0; i < int(blockDim.x / kWave); ++i) total += scratch[i];
-    __syncthreads();
-    return total;
-}
-
+// both frame arrays (symmetric, asymmetric) in the same pass over the PSQM
+// windows, so that their loads, powers and block sums overlap; each sum is
+// per wave (wave_sum), then over the waves in order
 __global__ void __launch_bounds__(kFinalThreads) chain_final_kernel(PipeArgs a) {
-    __shared__ double scratch[kFinalThreads / kWave];
+    constexpr int kFinalWaves = kFinalThreads / kWave;
+    __shared__ double scratch[2][kFinalWaves];
     const PipeLayout &L = a.L;
     const int item = blockIdx.x;
-    double d[2];
-    for (int which = 0; which < 2; ++which) {
-        const double *s = frame_array(a, which == 0 ? kSymm : kAsymm) + int64_t(item) * L.frames;
-        double *psqm = region<double>(a.ws, L.psqm) + (int64_t(which) * L.batch + item) * L.nwin;
-        double acc = 0.0;
-        for (int64_t l = threadIdx.x; l < L.nwin; l += blockDim.x) {
-            double m6 = 0.0;
-            for (int j = 0; j < kWin; ++j) {
-                const double v = s[l * kStride + j];
-                const double v2 = v * v;
-                m6 += v2 * v2 * v2;
-            }
-            const double pl = pow(m6 / kWin, 1.0 / 6.0);
-            psqm[l] = pl;
-            acc += pl * pl;
+    const double *s0 = frame_array(a, kSymm) + int64_t(item) * L.frames;
+    const double *s1 = frame_array(a, kAsymm) + int64_t(item) * L.frames;
+    double *psqm0 = region<double>(a.ws, L.psqm) + int64_t(item) * L.nwin;
+    double *psqm1 = psqm0 + L.batch * L.nwin;
+    double acc0 = 0.0, acc1 = 0.0;
+    for (int64_t l = threadIdx.x; l < L.nwin; l += blockDim.x) {
+        double m0 = 0.0, m1 = 0.0;
+        for (int j = 0; j < kWin; ++j) {
+            const double v0 = s0[l * kStride + j], v1 = s1[l * kStride + j];
+            const double q0 = v0 * v0, q1 = v1 * v1;
+            m0 += q0 * q0 * q0;
+            m1 += q1 * q1 * q1;
         }
-        d[which] = sqrt(block_sum(acc, scratch) / static_cast<double>(L.nwin));
+        const double pl0 = pow(m0 / kWin, 1.0 / 6.0), pl1 = pow(m1 / kWin, 1.0 / 6.0);
+        psqm0[l] = pl0;
+        psqm1[l] = pl1;
+        acc0 += pl0 * pl0;
+        acc1 += pl1 * pl1;
     }
+    acc0 = wave_sum(acc0);
+    acc1 = wave_sum(acc1);
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x % kWave) == 0) {
+        scratch[0][wave] = acc0;
+        scratch[1][wave] = acc1;
+    }
+    __syncthreads();
+    double d[2] = {0.0, 0.0};
+    for (int i = 0; i < kFinalWaves; ++i) {
+        d[0] += scratch[0][i];
+        d[1] += scratch[1][i];
+    }
+    d[0] = sqrt(d[0] / static_cast<double>(L.nwin));
+    d[1] = sqrt(d[1] / static_cast<double>(L.nwin));
     if (threadIdx.x == 0) {
         double *dist = region<double>(a.ws, L.dist) + int64_t(item) * 2;
         dist[0] = d[0];
