@@ -44,6 +44,28 @@ def test_forward_matches_float64(orig, new, length):
     assert _close(got, want)
 
 
+@pytest.mark.parametrize("orig", [32000, 48000, 64000, 96000])
+@pytest.mark.parametrize("length", [1, 37, 6001, 50001])
+def test_integer_decimation(orig, length):
+    """Decimation by 2, 3, 4 and 6 to 16 kHz: the single phase plans, whose kernels
+    keep a register window of the staged samples (forward) and of the upstream
+    gradient (adjoint); lengths below, at and across the workgroup tiles."""
+
+    mod = HipResample(orig, 16000).cuda()
+    x = torch.randn(2, length, generator=torch.Generator().manual_seed(orig + length))
+    got = mod(x.cuda())
+    want = O.resample(x.double(), orig, 16000)
+    assert got.shape == want.shape
+    assert _close(got, want)
+    xg = x.cuda().requires_grad_(True)
+    y = mod(xg)
+    g = torch.randn(y.shape, generator=torch.Generator().manual_seed(length))
+    (gx,) = torch.autograd.grad(y, xg, grad_outputs=g.cuda())
+    xo = x.double().requires_grad_(True)
+    (gw,) = torch.autograd.grad(O.resample(xo, orig, 16000), xo, grad_outputs=g.double())
+    assert _close(gx, gw)
+
+
 @pytest.mark.parametrize("orig,new", RATES)
 def test_backward_is_the_adjoint(orig, new):
     mod = HipResample(orig, new).cuda()

@@ -90,6 +90,82 @@ __global__ void __launch_bounds__(kResampleThreads)
 // phase ascending), zero padded terms add exact zeros.
 // ---------------------------------------------------------------------------
 
+// Staging of a row segment into LDS.  stage_row4 copies samples lo .. lo +
+// span - 1 of a row of n (sample s at s + s / kPad for kPad > 0, else at s),
+// zero outside the row, with 16 byte loads: thread t of a batch takes the
+// four staged samples 4 (t + 256 k) .. + 3, and issues all kBatch4 loads of a
+// batch before any of their LDS writes, so that a batch costs one memory round
+// trip (a plain loop waits for every load before its write).  The load starts
+// at the clamped sample st = clamp(lo + s, 0, n - 4) (a row of n >= 4), so it
+// stays inside the row; at a row edge the lane picks its samples out of the
+// loaded four by their shift from st and masks those outside the row.  No
+// load depends on a condition (which would let the compiler move it under a
+// branch and wait for it there), and the destination holds
+// staged_floats4<kPad, kBatch4>(span) floats: span rounded up to whole
+// batches.  kPad is a multiple of 4, so the four samples of a thread stay
+// contiguous in the padded layout.
+constexpr int kStageBatch = 8;  // staged samples per thread and batch of the tiled kernels
+
+__host__ __device__ constexpr int64_t staged_floats(int64_t span, int pad,
+                                                    int batch = kStageBatch) {
+    const int64_t round = int64_t(kResampleThreads) * batch;
+    const int64_t r = (span + round - 1) / round * round;
+    return pad > 0 ? r + r / pad + 1 : r;
+}
+
+template <int kPad, int kBatch4>
+__host__ __device__ constexpr int64_t staged_floats4(int64_t span) {
+    const int64_t round = int64_t(kResampleThreads) * 4 * kBatch4;
+    const int64_t r = (span + round - 1) / round * round;
+    return kPad > 0 ? r + r / kPad + 1 : r;
+}
+
+template <int kPad, int kBatch4>
+__device__ __forceinline__ void stage_row4(float *__restrict__ dst, const float *__restrict__ src,
+                                           int64_t lo, int64_t n, int span) {
+    static_assert(kPad % 4 == 0, "four samples stay contiguous");
+    constexpr int kRound = kResampleThreads * 4 * kBatch4;
+    if (n < 4) {  // rows of fewer than 4 samples: the plain copy
+        for (int s = threadIdx.x; s < staged_floats4<0, kBatch4>(span); s += kResampleThreads) {
+            const int64_t i = lo + s;
+            dst[kPad > 0 ? s + s / kPad : s] = (i >= 0 && i < n) ? src[i] : 0.0f;
+        }
+        return;
+    }
+    for (int s0 = 0; s0 < span; s0 += kRound) {
+        // all loads of the batch first, then the edge selection, then the writes
+        float q[kBatch4][4];
+        int64_t g0[kBatch4];
+        int d[kBatch4];  // shift of the load from the first sample: 0 inside the row
+#pragma unroll
+        for (int k = 0; k < kBatch4; ++k) {
+            g0[k] = lo + s0 + 4 * (k * kResampleThreads + static_cast<int>(threadIdx.x));
+            const int64_t st = g0[k] < 0 ? 0 : (g0[k] > n - 4 ? n - 4 : g0[k]);
+            d[k] = static_cast<int>(g0[k] - st);
+            __builtin_memcpy(q[k], src + st, sizeof(q[k]));
+        }
+        float v[kBatch4][4];
+#pragma unroll
+        for (int k = 0; k < kBatch4; ++k) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = e + d[k];
+                const float val =
+                    j <= 0 ? q[k][0] : (j == 1 ? q[k][1] : (j == 2 ? q[k][2] : q[k][3]));
+                const uint32_t keep = (g0[k] + e >= 0 && g0[k] + e < n) ? 0xFFFFFFFFu : 0u;
+                v[k][e] = __uint_as_float(__float_as_uint(val) & keep);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kBatch4; ++k) {
+            const unsigned s = s0 + 4 * (k * kResampleThreads + threadIdx.x);
+            float *o = dst + (kPad > 0 ? s + s / kPad : s);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = v[k][e];
+        }
+    }
+}
+
 constexpr int kTileQ = 4;
 constexpr int kTileOut = kResampleThreads * kTileQ;
 constexpr int kMaxSpan = 8192;   // staged samples per workgroup (32 KiB)
@@ -107,16 +183,13 @@ __global__ void __launch_bounds__(kResampleThreads)
                        int64_t blocks_per_row) {
     extern __shared__ float lds[];
     float *xs = lds;
-    float *tl = lds + span;
+    float *tl = lds + staged_floats(span, 0);
     const int64_t row = blockIdx.x / blocks_per_row;
     const int64_t m0 = (blockIdx.x - row * blocks_per_row) * kTileOut;
     const int64_t l_first = m0 / nstep;
     const int64_t in_lo = l_first * orig + off_min;
     const float *xr = x + row * n_in;
-    for (int s = threadIdx.x; s < span; s += kResampleThreads) {
-        const int64_t i = in_lo + s;
-        xs[s] = (i >= 0 && i < n_in) ? xr[i] : 0.0f;
-    }
+    stage_row4<0, kStageBatch / 4>(xs, xr, in_lo, n_in, span);
     if constexpr (kSource == kTapsLds) {
         for (int s = threadIdx.x; s < ntaps * nstep; s += kResampleThreads) tl[s] = taps[s];
     }
@@ -159,6 +232,113 @@ __global__ void __launch_bounds__(kResampleThreads)
     }
 }
 
+// Single phase forward (new_step 1, decimation by kOrig) with a register
+// window: thread u computes the kR consecutive outputs m0 + kR u + r.  With
+// the taps taken in chunks t = kOrig c + d, output r reads the staged sample
+// b + kOrig (r + c) + d (b = kR kOrig u: the phase's first tap is the first
+// staged sample), so the rows
+// X[j][d] = xs[b + kOrig j + d] form a window that slides by one row per
+// chunk: every staged sample is read and converted to double once and used by
+// up to kR outputs (the plain kernel reads and converts it for each of them).
+// The sum of each output runs over the taps in ascending order from 0, the
+// same operations as resample_fwd_tiled<kTapsUniform>.
+constexpr int kWinOut = 8;  // outputs per thread
+// staging batch of resample_fwd_window (float4 loads per thread): 1024
+// (2 orig + 1) samples, the window of 2048 outputs and up to 1024 / orig taps
+__host__ __device__ constexpr int fwd_window_batch4(int orig) { return 2 * orig + 1; }
+constexpr int kMaxWindowLds = 65536;  // bytes of LDS a window kernel may stage
+
+template <int kOrig>
+__global__ void __launch_bounds__(kResampleThreads)
+    resample_fwd_window(const float *__restrict__ x, float *__restrict__ y, int64_t n_in,
+                        int64_t n_out, const double *__restrict__ taps64, int ntaps, int off_min,
+                        int span, int64_t blocks_per_row) {
+    constexpr int kR = kWinOut;
+    constexpr int kTile = kResampleThreads * kR;
+    constexpr int kStride = kR * kOrig;  // staged samples between the windows of two lanes
+    extern __shared__ float lds[];
+    // staged sample s at s + s / kStride: one word of padding per lane stride
+    // makes the lane stride kStride + 1 words, odd, so a wavefront's reads of
+    // one window row fall in distinct banks
+    float *xs = lds;
+    const int64_t row = blockIdx.x / blocks_per_row;
+    const int64_t m0 = (blockIdx.x - row * blocks_per_row) * kTile;
+    const int64_t in_lo = m0 * kOrig + off_min;
+    const float *xr = x + row * n_in;
+    stage_row4<kStride, fwd_window_batch4(kOrig)>(xs, xr, in_lo, n_in, span);
+    __syncthreads();
+    // staged sample kStride u + o of lane u sits at xl[o + o / kStride]; a
+    // group of kR chunks advances the window by kStride samples, so the reads
+    // of a group take compile time offsets from a base that moves by
+    // kStride + 1 words per group
+    const float *xl = xs + (kStride + 1) * static_cast<int>(threadIdx.x);
+    double win[kR][kOrig];  // row j of the window in slot j mod kR
+#pragma unroll
+    for (int j = 0; j < kR - 1; ++j) {
+#pragma unroll
+        for (int d = 0; d < kOrig; ++d) {
+            const int o = kOrig * j + d;
+            win[j][d] = static_cast<double>(xl[o + o / kStride]);
+        }
+    }
+    double acc[kR];
+#pragma unroll
+    for (int r = 0; r < kR; ++r) acc[r] = 0.0;
+    // chunk g kR + cc of a group at base xg (rows g kR ...), taps tg[kOrig cc + d];
+    // kTail: the last group, whose taps may end inside it (rem of them left)
+    auto group = [&](const float *xg, const double *tg, auto tail, int rem) {
+        constexpr bool kTail = decltype(tail)::value;
+#pragma unroll
+        for (int cc = 0; cc < kR; ++cc) {
+            if (kTail && kOrig * cc >= rem) break;
+            // row g kR + cc + kR - 1 enters the window
+#pragma unroll
+            for (int d = 0; d < kOrig; ++d) {
+                const int o = kOrig * (cc + kR - 1) + d;
+                win[(cc + kR - 1) % kR][d] = static_cast<double>(xg[o + o / kStride]);
+            }
+#pragma unroll
+            for (int d = 0; d < kOrig; ++d) {
+                if (kTail && kOrig * cc + d >= rem) break;
+                const double w = tg[kOrig * cc + d];
+#pragma unroll
+                for (int r = 0; r < kR; ++r) acc[r] = fma(w, win[(cc + r) % kR][d], acc[r]);
+            }
+        }
+    };
+    const int full = ntaps / kStride;  // groups whose taps all exist
+    const float *xg = xl;
+    const double *tg = taps64;
+    for (int g = 0; g < full; ++g, xg += kStride + 1, tg += kStride) {
+        group(xg, tg, std::false_type{}, kStride);
+    }
+    if (ntaps > full * kStride) group(xg, tg, std::true_type{}, ntaps - full * kStride);
+    float *yr = y + row * n_out;
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+        const int64_t m = m0 + int64_t(kR) * threadIdx.x + r;
+        if (m < n_out) yr[m] = static_cast<float>(acc[r]);
+    }
+}
+
+// staged samples of resample_fwd_window (the last window row read ends at
+// orig (256 kR + nchunk - 1)), and its LDS bytes with the padding
+static int64_t window_span(int orig, int ntaps) {
+    const int64_t nchunk = (ntaps + orig - 1) / orig;
+    return int64_t(orig) * (int64_t(kResampleThreads) * kWinOut + nchunk - 1);
+}
+static int64_t window_lds(int64_t span, int orig) {
+    int64_t f = 0;
+    switch (orig) {
+        case 2: f = staged_floats4<kWinOut * 2, fwd_window_batch4(2)>(span); break;
+        case 3: f = staged_floats4<kWinOut * 3, fwd_window_batch4(3)>(span); break;
+        case 4: f = staged_floats4<kWinOut * 4, fwd_window_batch4(4)>(span); break;
+        case 6: f = staged_floats4<kWinOut * 6, fwd_window_batch4(6)>(span); break;
+        default: f = int64_t(1) << 40;  // no window kernel
+    }
+    return f * int64_t(sizeof(float));
+}
+
 // Adjoint of a single phase rate pair (new_step 1, integer decimation):
 // thread u of the workgroup takes the orig consecutive inputs
 // i = i0 + orig (u + 256 q) + c; input c of every thread uses the taps
@@ -173,16 +353,13 @@ __global__ void __launch_bounds__(kResampleThreads)
                          int sweeps, int span, int64_t blocks_per_row) {
     extern __shared__ float lds[];
     float *gs = lds;
-    float *out = lds + span;
+    float *out = lds + staged_floats(span, 0);
     const int per_block = kResampleThreads * kUniQ * orig;
     const int64_t row_id = blockIdx.x / blocks_per_row;
     const int64_t i0 = (blockIdx.x - row_id * blocks_per_row) * per_block;
     const int64_t l_lo = (i0 + width) / orig - (sweeps - 1);
     const float *gr = gy + row_id * n_out;
-    for (int s = threadIdx.x; s < span; s += kResampleThreads) {
-        const int64_t m = l_lo + s;
-        gs[s] = (m >= 0 && m < n_out) ? gr[m] : 0.0f;
-    }
+    stage_row4<0, kStageBatch / 4>(gs, gr, l_lo, n_out, span);
     __syncthreads();
     for (int c = 0; c < orig; ++c) {
         const int rho = (c + width) % orig;
@@ -212,6 +389,90 @@ __global__ void __launch_bounds__(kResampleThreads)
     }
 }
 
+// Adjoint of a single phase rate pair (new_step 1, decimation by kOrig) with
+// a register window.  Input i with i + width = kOrig l + rho receives
+//     gx[i] = sum_{s < sweeps} row[rho + kOrig s] gy[l - s].
+// Thread u takes the kV consecutive l = l_u + v (v < kV) and all kOrig phases
+// of each: the kV kOrig consecutive inputs from kOrig l_u - width.  They read
+// gy[l_u + v - s], a window of kV values that slides by one per step s: each
+// staged gy sample is converted to double once and feeds kV kOrig sums.  The
+// sums run over s in ascending order from 0, as in resample_bwd_uniform; the
+// results go through LDS to be written with unit stride.
+// output positions l per thread: odd, so that the lane strides of the
+// staged gradient (kWinIn words) and of the results (kWinIn orig words) are
+// odd and a wavefront's LDS accesses fall in distinct banks without padding
+constexpr int kWinIn = 7;
+constexpr int kBwdWindowBatch4 = 2;  // staging: float4 loads per thread, 2048 samples
+
+template <int kOrig>
+__global__ void __launch_bounds__(kResampleThreads)
+    resample_bwd_window(const float *__restrict__ gy, float *__restrict__ gx, int64_t n_in,
+                        int64_t n_out, const double *__restrict__ row, int width, int sweeps,
+                        int64_t l_min, int span, int64_t blocks_per_row) {
+    constexpr int kV = kWinIn;
+    constexpr int kPerBlock = kResampleThreads * kV;  // l per workgroup
+    constexpr int kOut = kV * kOrig;                  // inputs per thread
+    extern __shared__ float lds[];
+    float *gs = lds;                                                // gy[l_b - sweeps + 1 + s]
+    float *out = lds + staged_floats4<0, kBwdWindowBatch4>(span);  // the block's inputs
+    const int64_t row_id = blockIdx.x / blocks_per_row;
+    const int64_t l_b = l_min + (blockIdx.x - row_id * blocks_per_row) * kPerBlock;
+    const int64_t g_lo = l_b - sweeps + 1;
+    const float *gr = gy + row_id * n_out;
+    stage_row4<0, kBwdWindowBatch4>(gs, gr, g_lo, n_out, span);
+    __syncthreads();
+    // gy[l_u + p] is staged sample kV u + sweeps - 1 + p, p = v - s
+    const float *gl = gs + kV * static_cast<int>(threadIdx.x) + sweeps - 1;
+    auto grad = [&](int p) { return static_cast<double>(gl[p]); };
+    double win[kV];  // gy[l_u + p] in slot p mod kV
+#pragma unroll
+    for (int p = 1; p < kV; ++p) win[p] = grad(p);
+    double acc[kV][kOrig];
+#pragma unroll
+    for (int v = 0; v < kV; ++v) {
+#pragma unroll
+        for (int r = 0; r < kOrig; ++r) acc[v][r] = 0.0;
+    }
+    for (int s0 = 0; s0 < sweeps; s0 += kV) {
+#pragma unroll
+        for (int ss = 0; ss < kV; ++ss) {
+            const int sw = s0 + ss;
+            if (sw >= sweeps) break;
+            // p = -sw enters the window (v = 0), in the slot of p = kV - sw
+            win[(kV - ss) % kV] = grad(-sw);
+#pragma unroll
+            for (int r = 0; r < kOrig; ++r) {
+                const double w = row[r + kOrig * sw];
+#pragma unroll
+                for (int v = 0; v < kV; ++v) acc[v][r] = fma(w, win[(v - ss + kV) % kV], acc[v][r]);
+            }
+        }
+    }
+    float *ol = out + kOut * static_cast<int>(threadIdx.x);
+#pragma unroll
+    for (int v = 0; v < kV; ++v) {
+#pragma unroll
+        for (int r = 0; r < kOrig; ++r) ol[v * kOrig + r] = static_cast<float>(acc[v][r]);
+    }
+    __syncthreads();
+    // input of result k: kOrig l_b - width + k
+    const int64_t i_b = kOrig * l_b - width;
+    float *gxr = gx + row_id * n_in;
+    for (int k = threadIdx.x; k < kPerBlock * kOrig; k += kResampleThreads) {
+        const int64_t i = i_b + k;
+        if (i >= 0 && i < n_in) gxr[i] = out[k];
+    }
+}
+
+// staged gy samples of resample_bwd_window and its LDS bytes
+static int64_t bwd_window_span(int sweeps) {
+    return int64_t(kResampleThreads) * kWinIn + sweeps - 1;
+}
+static int64_t bwd_window_lds(int64_t span, int orig) {
+    const int64_t results = int64_t(kResampleThreads) * kWinIn * orig;
+    return (staged_floats4<0, kBwdWindowBatch4>(span) + results) * int64_t(sizeof(float));
+}
+
 template <bool kLds>
 __global__ void __launch_bounds__(kResampleThreads)
     resample_bwd_tiled(const float *__restrict__ gy, float *__restrict__ gx, int64_t n_in,
@@ -220,17 +481,14 @@ __global__ void __launch_bounds__(kResampleThreads)
                        int nphases, int sweeps, int ncols, int span, int64_t blocks_per_row) {
     extern __shared__ float lds[];
     float *gs = lds;
-    float *cl = lds + span;
+    float *cl = lds + staged_floats(span, 0);
     int32_t *clo = reinterpret_cast<int32_t *>(cl + nphases * ncols);
     const int64_t row = blockIdx.x / blocks_per_row;
     const int64_t i0 = (blockIdx.x - row * blocks_per_row) * kTileOut;
     const int64_t l_lo = (i0 + width) / orig - (sweeps - 1);
     const int64_t m_lo = l_lo * nstep;  // may be negative: those outputs read as zero
     const float *gr = gy + row * n_out;
-    for (int s = threadIdx.x; s < span; s += kResampleThreads) {
-        const int64_t m = m_lo + s;
-        gs[s] = (m >= 0 && m < n_out) ? gr[m] : 0.0f;
-    }
+    stage_row4<0, kStageBatch / 4>(gs, gr, m_lo, n_out, span);
     if constexpr (kLds) {
         for (int s = threadIdx.x; s < nphases * ncols; s += kResampleThreads) cl[s] = cols[s];
         for (int s = threadIdx.x; s < ncols; s += kResampleThreads) clo[s] = col_lo[s];
@@ -420,8 +678,46 @@ extern "C" int pesq_resample_plan_forward(const float *x, float *y, int64_t rows
     const float *taps = reinterpret_cast<const float *>(base);
     const double *taps64 = reinterpret_cast<const double *>(base + r.off_taps64);
     const int32_t *offs = reinterpret_cast<const int32_t *>(base + r.off_offs);
+    if (r.new_step == 1) {
+        // decimation by 2, 3, 4 or 6 (32, 48, 64, 96 kHz to 16 kHz): the register window
+        const int64_t wspan = window_span(r.orig_step, r.taps);
+        const int64_t wbpr = cdiv(n_out, int64_t(kResampleThreads) * kWinOut);
+        const dim3 wgrid(static_cast<unsigned>(rows * wbpr)), wblock(kResampleThreads);
+        const size_t wbytes = size_t(window_lds(wspan, r.orig_step));
+        bool launched = wbytes <= size_t(kMaxWindowLds);
+        if (launched) {
+            switch (r.orig_step) {
+                case 2:
+                    hipLaunchKernelGGL(resample_fwd_window<2>, wgrid, wblock, wbytes, stream, x, y,
+                                       n_in, n_out, taps64, r.taps, r.off_min,
+                                       static_cast<int>(wspan), wbpr);
+                    break;
+                case 3:
+                    hipLaunchKernelGGL(resample_fwd_window<3>, wgrid, wblock, wbytes, stream, x, y,
+                                       n_in, n_out, taps64, r.taps, r.off_min,
+                                       static_cast<int>(wspan), wbpr);
+                    break;
+                case 4:
+                    hipLaunchKernelGGL(resample_fwd_window<4>, wgrid, wblock, wbytes, stream, x, y,
+                                       n_in, n_out, taps64, r.taps, r.off_min,
+                                       static_cast<int>(wspan), wbpr);
+                    break;
+                case 6:
+                    hipLaunchKernelGGL(resample_fwd_window<6>, wgrid, wblock, wbytes, stream, x, y,
+                                       n_in, n_out, taps64, r.taps, r.off_min,
+                                       static_cast<int>(wspan), wbpr);
+                    break;
+                default:
+                    launched = false;
+            }
+        }
+        if (launched) {
+            PESQ_CHECK_LAUNCH("resample forward (window)");
+            return PESQ_OK;
+        }
+    }
     const dim3 grid(static_cast<unsigned>(rows * bpr)), block(kResampleThreads);
-    const size_t span_bytes = size_t(r.fwd_span) * sizeof(float);
+    const size_t span_bytes = size_t(staged_floats(r.fwd_span, 0)) * sizeof(float);
     if (r.new_step == 1) {
         hipLaunchKernelGGL(resample_fwd_tiled<kTapsUniform>, grid, block, span_bytes, stream, x,
                            y, n_in, n_out, taps, taps64, offs, r.orig_step, r.new_step, r.taps,
@@ -457,10 +753,49 @@ extern "C" int pesq_resample_plan_backward(const float *grad_y, float *grad_x, i
     PESQ_CHECK_ARG(rows * bpr < (int64_t(1) << 31), "too many rows x blocks for one launch");
     const unsigned char *base = static_cast<const unsigned char *>(plan);
     if (r.new_step == 1) {
+        // decimation by 2, 3, 4 or 6: the register window
+        const int64_t wspan = bwd_window_span(r.sweeps);
+        const int64_t wlds = bwd_window_lds(wspan, r.orig_step);
+        const int64_t l_min = r.width / r.orig_step;
+        const int64_t l_max = (n_in - 1 + r.width) / r.orig_step;
+        const int64_t wnb = cdiv(l_max - l_min + 1, int64_t(kResampleThreads) * kWinIn);
+        const double *row = reinterpret_cast<const double *>(base + r.off_row64);
+        const dim3 wgrid(static_cast<unsigned>(rows * wnb)), wblock(kResampleThreads);
+        bool launched = wlds <= kMaxWindowLds && rows * wnb < (int64_t(1) << 31);
+        if (launched) {
+            switch (r.orig_step) {
+                case 2:
+                    hipLaunchKernelGGL(resample_bwd_window<2>, wgrid, wblock, size_t(wlds), stream,
+                                       grad_y, grad_x, n_in, n_out, row, r.width, r.sweeps, l_min,
+                                       static_cast<int>(wspan), wnb);
+                    break;
+                case 3:
+                    hipLaunchKernelGGL(resample_bwd_window<3>, wgrid, wblock, size_t(wlds), stream,
+                                       grad_y, grad_x, n_in, n_out, row, r.width, r.sweeps, l_min,
+                                       static_cast<int>(wspan), wnb);
+                    break;
+                case 4:
+                    hipLaunchKernelGGL(resample_bwd_window<4>, wgrid, wblock, size_t(wlds), stream,
+                                       grad_y, grad_x, n_in, n_out, row, r.width, r.sweeps, l_min,
+                                       static_cast<int>(wspan), wnb);
+                    break;
+                case 6:
+                    hipLaunchKernelGGL(resample_bwd_window<6>, wgrid, wblock, size_t(wlds), stream,
+                                       grad_y, grad_x, n_in, n_out, row, r.width, r.sweeps, l_min,
+                                       static_cast<int>(wspan), wnb);
+                    break;
+                default:
+                    launched = false;
+            }
+        }
+        if (launched) {
+            PESQ_CHECK_LAUNCH("resample backward (window)");
+            return PESQ_OK;
+        }
         const int64_t per_block = int64_t(kResampleThreads) * kUniQ * r.orig_step;
         const int64_t nb = cdiv(n_in, per_block);
         PESQ_CHECK_ARG(rows * nb < (int64_t(1) << 31), "too many rows x blocks for one launch");
-        const size_t lds = size_t(r.bwd_span + per_block) * sizeof(float);
+        const size_t lds = size_t(staged_floats(r.bwd_span, 0) + per_block) * sizeof(float);
         hipLaunchKernelGGL(resample_bwd_uniform, dim3(static_cast<unsigned>(rows * nb)),
                            dim3(kResampleThreads), lds, stream, grad_y, grad_x, n_in, n_out,
                            reinterpret_cast<const double *>(base + r.off_row64), r.orig_step,
@@ -471,7 +806,7 @@ extern "C" int pesq_resample_plan_backward(const float *grad_y, float *grad_x, i
     const float *cols = reinterpret_cast<const float *>(base + r.off_cols);
     const int32_t *col_lo = reinterpret_cast<const int32_t *>(base + r.off_col_lo);
     const dim3 grid(static_cast<unsigned>(rows * bpr)), block(kResampleThreads);
-    const size_t span_bytes = size_t(r.bwd_span) * sizeof(float);
+    const size_t span_bytes = size_t(staged_floats(r.bwd_span, 0)) * sizeof(float);
     const int64_t table = (int64_t(r.phases) + 1) * r.columns;
     if (table <= kMaxTable) {
         hipLaunchKernelGGL(resample_bwd_tiled<true>, grid, block,
