@@ -313,7 +313,7 @@ int pesq_stft_backward(const float *g_bark, const float *x, int64_t rows, int64_
 /* perceptual chain (TritonPesqChain, torch_pesq/triton_ops/chain.py:1024-1126) */
 /* ----------------------------------------------------------------------- */
 
-/* Pack the chain constants of `nbands` bands (1 .. 64) into `out` (host
+/* Pack the chain constants of `nbands` bands (1 .. 128) into `out` (host
  * memory, pesq_model_table_bytes() bytes): hearing thresholds (> 0), loudness
  * exponents, band widths in Bark, their total over bands 1.. and sl.  The
  * constructor of TritonPesqChain (chain.py:1057-1078).  A table from
@@ -325,7 +325,7 @@ int pesq_chain_forward_workspace(int64_t batch, int64_t frames, int nbands, size
 int pesq_chain_backward_workspace(int64_t batch, int64_t frames, int nbands, size_t *bytes);
 
 /* (d_symm, d_asymm)[batch] of two Bark spectrograms [batch, frames, nbands]
- * (nbands 1 .. 64, as packed in model_table); needs at least 20 frames.
+ * (nbands 1 .. 128, as packed in model_table); needs at least 20 frames.
  * Replaces the 7 forward kernels of _ChainFunction.forward (chain.py:768-940). */
 int pesq_chain_forward(const float *ref_bark, const float *deg_bark, int64_t batch,
                        int64_t frames, int nbands, const void *model_table, float *d_symm,

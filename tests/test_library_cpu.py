@@ -241,7 +241,9 @@ def test_chain_table_pack_validates():
     wd = np.full(17, 0.5)
     ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
     assert lib.pesq_chain_table_pack(17, ptr(th), ptr(ex), ptr(wd), 8.0, 0.18, buf) == 0
-    assert lib.pesq_chain_table_pack(65, ptr(np.ones(65)), ptr(np.ones(65)), ptr(np.ones(65)),
+    assert lib.pesq_chain_table_pack(128, ptr(np.ones(128)), ptr(np.ones(128)), ptr(np.ones(128)),
+                                     8.0, 0.18, buf) == 0
+    assert lib.pesq_chain_table_pack(129, ptr(np.ones(129)), ptr(np.ones(129)), ptr(np.ones(129)),
                                      8.0, 0.18, buf) != 0
     assert b"bands" in lib.pesq_last_error()
     th[3] = 0.0

@@ -269,12 +269,13 @@ def test_chain_batch_independence_and_errors(chain):
         chain(ref, deg)
 
 
-@pytest.mark.parametrize("nband", [17, 33, 64])
+@pytest.mark.parametrize("nband", [17, 33, 64, 65, 100, 128])
 def test_chain_other_band_counts(nband):
     """Band counts other than 49 (``test_triton_chain.py:668-717``): random
     thresholds, exponents and widths, against the float64 restatement with the
-    same tables, forward and gradients.  The kernels take one band per lane,
-    so 64 is the largest count (65 raises)."""
+    same tables, forward and gradients.  The kernels take one band per lane up
+    to 64 bands and two (band lane + 64) up to 128, the largest count (129
+    raises)."""
 
     gen = torch.Generator().manual_seed(nband)
     threshs = (10 ** (torch.rand(nband, generator=gen) * 8 - 1)).double()
@@ -303,6 +304,6 @@ def test_chain_other_band_counts(nband):
         chain(ref[:, :, :-1].contiguous().cuda(), deg[:, :, :-1].contiguous().cuda())
 
 
-def test_chain_rejects_more_than_64_bands():
-    with pytest.raises(ValueError, match="at most 64"):
-        HipPesqChain(torch.ones(65), torch.full((65,), 0.2), torch.ones(65), 64.0)
+def test_chain_rejects_more_than_128_bands():
+    with pytest.raises(ValueError, match="at most 128"):
+        HipPesqChain(torch.ones(129), torch.full((129,), 0.2), torch.ones(129), 128.0)

@@ -166,12 +166,12 @@ __device__ __forceinline__ double *band_array(const PipeArgs &a, int which) {
     return region<double>(a.ws, a.L.band) + int64_t(which) * a.L.batch * a.L.nb;
 }
 
-// Band `lane` of the per tile band partials base[tile][nb], summed over tiles
+// Band `band` of the per tile band partials base[tile][nb], summed over tiles
 // part, part + parts, part + 2 parts, ... (in that order); 0 when there are none.
 __device__ __forceinline__ double tile_partial(const double *base, int64_t ntile, int part,
-                                               int parts, int lane, int nb) {
+                                               int parts, int band, int nb) {
     const int n = ntile > part ? static_cast<int>((ntile - 1 - part) / parts) + 1 : 0;
-    return n > 0 ? strided_sum(base + int64_t(part) * nb + lane, n, int64_t(parts) * nb) : 0.0;
+    return n > 0 ? strided_sum(base + int64_t(part) * nb + band, n, int64_t(parts) * nb) : 0.0;
 }
 
 // Zwicker loudness sl (2 th)^e ((0.5 + 0.5 x / th)^e - 1) above the threshold,
@@ -365,14 +365,14 @@ struct BandConsts {
     double th, inv2th, e, ls, w;
 };
 
-__device__ __forceinline__ BandConsts band_consts(const ModelTable &t, int lane, int nb) {
+__device__ __forceinline__ BandConsts band_consts(const ModelTable &t, int band, int nb) {
     BandConsts c{1.0, 0.5, 1.0, 0.0, 0.0};
-    if (lane < nb) {
-        c.th = t.threshs[lane];
+    if (band < nb) {
+        c.th = t.threshs[band];
         c.inv2th = 0.5 / c.th;
-        c.e = t.exps[lane];
-        c.ls = t.loud_scale[lane];
-        c.w = t.width[lane];
+        c.e = t.exps[band];
+        c.ls = t.loud_scale[band];
+        c.w = t.width[band];
     }
     return c;
 }
@@ -385,14 +385,14 @@ __device__ __forceinline__ BandConsts band_consts(const ModelTable &t, int lane,
 // any kWaves, so the results do not depend on the choice.
 constexpr int kChainSlices = 16;  // fixed split of the band partial sums
 
-template <int kWaves>
+template <int kWaves, int kBPL>
 __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
     constexpr int kPer = kTile / kWaves;  // frames per wavefront
-    __shared__ double part[2][kChainSlices][kMaxChainBands];
+    __shared__ double part[2][kChainSlices][kWave * kBPL];
 
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
-    const int nb = L.nb;  // bands, one per lane
+    const int nb = L.nb;  // bands: band lane + kWave k is slot k of a lane
     const int item = blockIdx.x / L.ntile;
     const int tile = blockIdx.x - item * L.ntile;
     const int t0 = tile * kTile;
@@ -403,23 +403,28 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
 
     // Bark values of frames f0 - 1 .. f0 + kPer - 1, loaded up front (indices
     // clamped into the array; out of range frames and bands are masked later)
-    float R[kPer + 1], G[kPer + 1];
+    float R[kBPL][kPer + 1], G[kBPL][kPer + 1];
     {
-        const int band = lane < nb ? lane : nb - 1;
         const float *bref = a.bark_ref + int64_t(item) * L.frames * nb;
         const float *bdeg = a.bark_deg + int64_t(item) * L.frames * nb;
 #pragma unroll
-        for (int q = 0; q <= kPer; ++q) {
-            int64_t frame = f0 - 1 + q;
-            frame = frame < 0 ? 0 : (frame >= L.frames ? L.frames - 1 : frame);
-            R[q] = bref[frame * nb + band];
-            G[q] = bdeg[frame * nb + band];
+        for (int k = 0; k < kBPL; ++k) {
+            const int band = lane + kWave * k < nb ? lane + kWave * k : nb - 1;
+#pragma unroll
+            for (int q = 0; q <= kPer; ++q) {
+                int64_t frame = f0 - 1 + q;
+                frame = frame < 0 ? 0 : (frame >= L.frames ? L.frames - 1 : frame);
+                R[k][q] = bref[frame * nb + band];
+                G[k][q] = bdeg[frame * nb + band];
+            }
         }
     }
 
     // band constants and the uniform reciprocals, requested before the barrier
     // (which would hold back loads issued after it)
-    const BandConsts c = band_consts(t, lane, nb);
+    BandConsts c[kBPL];
+#pragma unroll
+    for (int k = 0; k < kBPL; ++k) c[k] = band_consts(t, lane + kWave * k, nb);
     const double W = t.total_width;
     const double inv_sqrt_w = 1.0 / sqrt(W);
     const double inv_w = 1.0 / W;
@@ -428,45 +433,67 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
     // partials of tiles v, v + kChainSlices, ...; the slices are then added in
     // order, the same order in every workgroup (wavefront w takes slices w,
     // w + kWaves, ...)
-    if (lane < nb) {
+    {
         const double *pr = region<double>(a.ws, L.bandref) + int64_t(item) * L.ntile * nb;
         const double *pd = region<double>(a.ws, L.banddeg) + int64_t(item) * L.ntile * nb;
 #pragma unroll
-        for (int v = wave; v < kChainSlices; v += kWaves) {
-            part[0][v][lane] = tile_partial(pr, L.ntile, v, kChainSlices, lane, nb);
-            part[1][v][lane] = tile_partial(pd, L.ntile, v, kChainSlices, lane, nb);
+        for (int k = 0; k < kBPL; ++k) {
+            const int band = lane + kWave * k;
+            if (band < nb) {
+#pragma unroll
+                for (int v = wave; v < kChainSlices; v += kWaves) {
+                    part[0][v][band] = tile_partial(pr, L.ntile, v, kChainSlices, band, nb);
+                    part[1][v][band] = tile_partial(pd, L.ntile, v, kChainSlices, band, nb);
+                }
+            }
         }
     }
     __syncthreads();
 
-    const bool live = lane < nb;
-    double r = 0.0;
-    if (live) {
-        double sr = 0.0, sd = 0.0;
-        for (int v = 0; v < kChainSlices; ++v) {
-            sr += part[0][v][lane];
-            sd += part[1][v][lane];
-        }
-        const double mref = sr / frames_f;
-        const double mdeg = sd / frames_f;
-        const double ratio = (mdeg + 1000.0) / (mref + 1000.0);
-        r = fmin(fmax(ratio, 0.01), 100.0);
-        if (tile == 0 && wave == 0) {
-            band_array(a, kR)[item * nb + lane] = r;
-            band_array(a, kRatio)[item * nb + lane] = ratio;
-            band_array(a, kMref)[item * nb + lane] = mref;
+    bool live[kBPL];
+    double r[kBPL];
+#pragma unroll
+    for (int k = 0; k < kBPL; ++k) {
+        const int band = lane + kWave * k;
+        live[k] = band < nb;
+        r[k] = 0.0;
+        if (live[k]) {
+            double sr = 0.0, sd = 0.0;
+            for (int v = 0; v < kChainSlices; ++v) {
+                sr += part[0][v][band];
+                sd += part[1][v][band];
+            }
+            const double mref = sr / frames_f;
+            const double mdeg = sd / frames_f;
+            const double ratio = (mdeg + 1000.0) / (mref + 1000.0);
+            r[k] = fmin(fmax(ratio, 0.01), 100.0);
+            if (tile == 0 && wave == 0) {
+                band_array(a, kR)[item * nb + band] = r[k];
+                band_array(a, kRatio)[item * nb + band] = ratio;
+                band_array(a, kMref)[item * nb + band] = mref;
+            }
         }
     }
     // per frame totals of the audible energies; slot q is frame f0 - 1 + q
+    // (a lane adds its bands, then the lanes are summed)
     double taer[kPer + 1], tad[kPer + 1];
 #pragma unroll
     for (int q = 0; q <= kPer; ++q) {
         const int64_t frame = f0 - 1 + q;
-        const bool ok = live && frame >= 0 && frame < L.frames;
-        const double er = r * static_cast<double>(R[q]);
-        const double g = G[q];
-        taer[q] = wave_sum(ok && er > c.th ? er : 0.0);
-        tad[q] = wave_sum(ok && g > c.th ? g : 0.0);
+        const bool fok = frame >= 0 && frame < L.frames;
+        double ar = 0.0, ad = 0.0;
+#pragma unroll
+        for (int k = 0; k < kBPL; ++k) {
+            const bool ok = live[k] && fok;
+            const double er = r[k] * static_cast<double>(R[k][q]);
+            const double g = G[k][q];
+            const double xr = ok && er > c[k].th ? er : 0.0;
+            const double xd = ok && g > c[k].th ? g : 0.0;
+            ar = k == 0 ? xr : ar + xr;  // a lane's first band starts the sum
+            ad = k == 0 ? xd : ad + xd;
+        }
+        taer[q] = wave_sum(ar);
+        tad[q] = wave_sum(ad);
     }
 
 #pragma unroll
@@ -481,21 +508,28 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
         const double fpr = fmin(fmax(fpr1, 3e-4), 5.0);
 
         double v2 = 0.0, ya = 0.0;
-        if (live) {
-            const double er = r * static_cast<double>(R[q + 1]);
-            const double ed = fpr * static_cast<double>(G[q + 1]);
-            const double lr = loudness(er, c.th, c.inv2th, c.e, c.ls);
-            const double ld = loudness(ed, c.th, c.inv2th, c.e, c.ls);
-            const double u = ld - lr;
-            const double z = fabs(u) - 0.25 * fmin(ld, lr);
-            const double dist = sgn(u) * fmax(z, 0.0);
-            const double asc_raw = asymmetry(ed, 1.0 / (er + 50.0));
-            const double asc = asc_raw < 3.0 ? 0.0 : fmin(asc_raw, 12.0);
-            if (lane >= 1) {
-                const double v = c.w * dist * inv_sqrt_w;
-                v2 = v * v;
-                ya = fabs(c.w * (dist * asc) * inv_w);
+#pragma unroll
+        for (int k = 0; k < kBPL; ++k) {
+            double xv = 0.0, xa = 0.0;
+            if (live[k]) {
+                const BandConsts &ck = c[k];
+                const double er = r[k] * static_cast<double>(R[k][q + 1]);
+                const double ed = fpr * static_cast<double>(G[k][q + 1]);
+                const double lr = loudness(er, ck.th, ck.inv2th, ck.e, ck.ls);
+                const double ld = loudness(ed, ck.th, ck.inv2th, ck.e, ck.ls);
+                const double u = ld - lr;
+                const double z = fabs(u) - 0.25 * fmin(ld, lr);
+                const double dist = sgn(u) * fmax(z, 0.0);
+                const double asc_raw = asymmetry(ed, 1.0 / (er + 50.0));
+                const double asc = asc_raw < 3.0 ? 0.0 : fmin(asc_raw, 12.0);
+                if (lane + kWave * k >= 1) {
+                    const double v = ck.w * dist * inv_sqrt_w;
+                    xv = v * v;
+                    xa = fabs(ck.w * (dist * asc) * inv_w);
+                }
             }
+            v2 = k == 0 ? xv : v2 + xv;
+            ya = k == 0 ? xa : ya + xa;
         }
         const double symm_raw = W * sqrt(wave_sum(v2));
         const double asymm_raw = W * wave_sum(ya);
@@ -602,40 +636,49 @@ __device__ __forceinline__ double psqm_adjoint(const PipeLayout &L, const double
     return acc;
 }
 
-template <int kWaves>
-__global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
+// the 4 wavefront single band variant (large grids) is held to 128 VGPRs, four
+// workgroups per CU
+template <int kWaves, int kBPL>
+__global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 1)
+    chain_bwd_kernel(PipeArgs a) {
     constexpr int kPer = kTile / kWaves;
     constexpr int kSlots = kTile + 1;  // the tile's frames and the next one
-    __shared__ double rs[kMaxChainBands];
+    constexpr int kLaneBands = kWave * kBPL;
+    __shared__ double rs[kLaneBands];
     __shared__ double fr[kFrameArrays][kSlots];
     __shared__ double pl[2][kPsqmSlots];
     __shared__ double gfpr[kSlots], gh[kSlots];
-    __shared__ double part[kTile][kMaxChainBands];  // per frame band partials
+    __shared__ double part[kTile][kLaneBands];  // per frame band partials
 
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
-    const int nb = L.nb;  // bands, one per lane
+    const int nb = L.nb;  // bands: band lane + kWave k is slot k of a lane
     const int item = blockIdx.x / L.ntile;
     const int tile = blockIdx.x - item * L.ntile;
     const int t0 = tile * kTile;
     const int wave = threadIdx.x / kWave;
     const int lane = threadIdx.x % kWave;
-    const bool live = lane < nb;
+    bool live[kBPL];
+#pragma unroll
+    for (int k = 0; k < kBPL; ++k) live[k] = lane + kWave * k < nb;
     const int64_t fo = int64_t(item) * L.frames;
     const int64_t lbase = t0 / kStride - 1;
 
     // Bark values of this wavefront's frames (slot q = local frame wave kPer + q)
-    float R[kPer + 1], G[kPer + 1];
+    float R[kBPL][kPer + 1], G[kBPL][kPer + 1];
     {
-        const int band = live ? lane : nb - 1;
         const float *bref = a.bark_ref + int64_t(item) * L.frames * nb;
         const float *bdeg = a.bark_deg + int64_t(item) * L.frames * nb;
 #pragma unroll
-        for (int q = 0; q <= kPer; ++q) {
-            const int64_t frame = t0 + wave * kPer + q;
-            const int64_t fc = frame < L.frames ? frame : L.frames - 1;
-            R[q] = bref[fc * nb + band];
-            G[q] = bdeg[fc * nb + band];
+        for (int k = 0; k < kBPL; ++k) {
+            const int band = live[k] ? lane + kWave * k : nb - 1;
+#pragma unroll
+            for (int q = 0; q <= kPer; ++q) {
+                const int64_t frame = t0 + wave * kPer + q;
+                const int64_t fc = frame < L.frames ? frame : L.frames - 1;
+                R[k][q] = bref[fc * nb + band];
+                G[k][q] = bdeg[fc * nb + band];
+            }
         }
     }
 
@@ -652,9 +695,16 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
         l = l < 0 ? 0 : (l >= L.nwin ? L.nwin - 1 : l);
         pl[side][i] = region<double>(a.ws, L.psqm)[(int64_t(side) * L.batch + item) * L.nwin + l];
     }
-    if (wave == 0 && live) rs[lane] = band_array(a, kR)[item * nb + lane];
+    if (wave == 0) {
+#pragma unroll
+        for (int k = 0; k < kBPL; ++k) {
+            if (live[k]) rs[lane + kWave * k] = band_array(a, kR)[item * nb + lane + kWave * k];
+        }
+    }
     // band constants, requested before the barrier (which would hold them back)
-    const BandConsts c = band_consts(t, lane, nb);
+    BandConsts c[kBPL];
+#pragma unroll
+    for (int k = 0; k < kBPL; ++k) c[k] = band_consts(t, lane + kWave * k, nb);
     const double W = t.total_width;
 
     // upstream gradients of the two distances, MOS and loss folded in
@@ -677,16 +727,19 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
     }
     __syncthreads();
 
-    const double r = live ? rs[lane] : 0.0;
+    double r[kBPL];
+#pragma unroll
+    for (int k = 0; k < kBPL; ++k) r[k] = live[k] ? rs[lane + kWave * k] : 0.0;
 
     // phase 1: adjoint of the per frame distances down to equ_ref / equ_deg
-    double g_er[kPer + 1], g_ed[kPer + 1];
+    double g_er[kBPL][kPer + 1], g_ed[kBPL][kPer + 1];
     const int nmine = wave == kWaves - 1 ? kPer + 1 : kPer;
 #pragma unroll
     for (int q = 0; q <= kPer; ++q) {
         const int local = wave * kPer + q;
         const int64_t frame = t0 + local;
-        g_er[q] = g_ed[q] = 0.0;
+#pragma unroll
+        for (int k = 0; k < kBPL; ++k) g_er[k][q] = g_ed[k][q] = 0.0;
         if (q >= nmine || frame >= L.frames) continue;
 
         const double s_sy = fr[kSymm][local];
@@ -706,46 +759,52 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
         const double inv_raw_s = raw_s > 0.0 ? 1.0 / raw_s : 0.0;
         const double fpr = fmin(fmax(fr[kFpr1][local], 3e-4), 5.0);
 
-        double my_er = 0.0, my_ed = 0.0, gf = 0.0;
-        if (live) {
-            const double Rq = R[q], Gq = G[q];
-            const double er = r * Rq, ed = fpr * Gq;
-            double lr, ld, slope_r, slope_d;
-            loudness_and_slope(er, c.th, c.inv2th, c.e, c.ls, lr, slope_r);
-            loudness_and_slope(ed, c.th, c.inv2th, c.e, c.ls, ld, slope_d);
-            const double u = ld - lr;
-            const double z = fabs(u) - 0.25 * fmin(ld, lr);
-            const double su = sgn(u);
-            const double dst = su * fmax(z, 0.0);
-            const double inv_er50 = 1.0 / (er + 50.0), inv_ed50 = 1.0 / (ed + 50.0);
-            const double asc_raw = asymmetry(ed, inv_er50);
-            const double asc = asc_raw < 3.0 ? 0.0 : fmin(asc_raw, 12.0);
+        double gf = 0.0;
+#pragma unroll
+        for (int k = 0; k < kBPL; ++k) {
+            double my_er = 0.0, my_ed = 0.0, xg = 0.0;
+            if (live[k]) {
+                const BandConsts &ck = c[k];
+                const double Rq = R[k][q], Gq = G[k][q];
+                const double er = r[k] * Rq, ed = fpr * Gq;
+                double lr, ld, slope_r, slope_d;
+                loudness_and_slope(er, ck.th, ck.inv2th, ck.e, ck.ls, lr, slope_r);
+                loudness_and_slope(ed, ck.th, ck.inv2th, ck.e, ck.ls, ld, slope_d);
+                const double u = ld - lr;
+                const double z = fabs(u) - 0.25 * fmin(ld, lr);
+                const double su = sgn(u);
+                const double dst = su * fmax(z, 0.0);
+                const double inv_er50 = 1.0 / (er + 50.0), inv_ed50 = 1.0 / (ed + 50.0);
+                const double asc_raw = asymmetry(ed, inv_er50);
+                const double asc = asc_raw < 3.0 ? 0.0 : fmin(asc_raw, 12.0);
 
-            double g_dist = 0.0, g_asc = 0.0;
-            if (lane >= 1) {
-                if (raw_s > 0.0) g_dist = g_rs * W * c.w * c.w * dst * inv_raw_s;
-                const double gy = g_ra * c.w * sgn(dst * asc);
-                g_dist += gy * asc;
-                g_asc = gy * dst;
+                double g_dist = 0.0, g_asc = 0.0;
+                if (lane + kWave * k >= 1) {
+                    if (raw_s > 0.0) g_dist = g_rs * W * ck.w * ck.w * dst * inv_raw_s;
+                    const double gy = g_ra * ck.w * sgn(dst * asc);
+                    g_dist += gy * asc;
+                    g_asc = gy * dst;
+                }
+                const bool inzone = z >= 0.0;
+                const double g_u = inzone ? g_dist * su * su : 0.0;
+                const double g_min = inzone ? -0.25 * g_dist * su : 0.0;
+                const double wd = ld < lr ? 1.0 : (ld == lr ? 0.5 : 0.0);
+                const double wr = lr < ld ? 1.0 : (ld == lr ? 0.5 : 0.0);
+                const double g_ld = g_u + g_min * wd;
+                const double g_lr = -g_u + g_min * wr;
+                my_er = g_lr * slope_r;
+                my_ed = g_ld * slope_d;
+                if (asc_raw >= 3.0 && asc_raw <= 12.0) {
+                    my_ed += g_asc * 1.2 * asc_raw * inv_ed50;
+                    my_er -= g_asc * 1.2 * asc_raw * inv_er50;
+                }
+                xg = my_ed * Gq;
             }
-            const bool inzone = z >= 0.0;
-            const double g_u = inzone ? g_dist * su * su : 0.0;
-            const double g_min = inzone ? -0.25 * g_dist * su : 0.0;
-            const double wd = ld < lr ? 1.0 : (ld == lr ? 0.5 : 0.0);
-            const double wr = lr < ld ? 1.0 : (ld == lr ? 0.5 : 0.0);
-            const double g_ld = g_u + g_min * wd;
-            const double g_lr = -g_u + g_min * wr;
-            my_er = g_lr * slope_r;
-            my_ed = g_ld * slope_d;
-            if (asc_raw >= 3.0 && asc_raw <= 12.0) {
-                my_ed += g_asc * 1.2 * asc_raw * inv_ed50;
-                my_er -= g_asc * 1.2 * asc_raw * inv_er50;
-            }
-            gf = my_ed * Gq;
+            g_er[k][q] = my_er;
+            g_ed[k][q] = my_ed;
+            gf = k == 0 ? xg : gf + xg;
         }
         gf = wave_sum(gf);
-        g_er[q] = my_er;
-        g_ed[q] = my_ed;
         if (lane == 0) {
             gfpr[local] = gf;
             gh[local] = g_hh;
@@ -757,7 +816,10 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
     // band partials of d/dr are kept per frame and added in frame order
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
-        if (live) part[wave * kPer + q][lane] = 0.0;
+#pragma unroll
+        for (int k = 0; k < kBPL; ++k) {
+            if (live[k]) part[wave * kPer + q][lane + kWave * k] = 0.0;
+        }
     }
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
@@ -780,21 +842,29 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_bwd_kernel(PipeArgs a) {
         const double g_taer = g0 * inv_tad + gh[local] * 0.04 * h / (taer + 1e5);
         const double g_tad = -g0 * fpr0 * inv_tad;
         const double fpr = fmin(fmax(f1, 3e-4), 5.0);
-        if (live) {
-            const double Rq = R[q], Gq = G[q];
-            double ger = g_er[q];
-            if (r * Rq > c.th) ger += g_taer;
-            const double ged = g_ed[q] * fpr + (Gq > c.th ? g_tad : 0.0);
-            a.gbark_ref[(int64_t(item) * L.frames + frame) * nb + lane] = static_cast<float>(ger * r);
-            a.gbark_deg[(int64_t(item) * L.frames + frame) * nb + lane] = static_cast<float>(ged);
-            part[local][lane] = ger * Rq;
+#pragma unroll
+        for (int k = 0; k < kBPL; ++k) {
+            if (!live[k]) continue;
+            const int band = lane + kWave * k;
+            const double Rq = R[k][q], Gq = G[k][q];
+            double ger = g_er[k][q];
+            if (r[k] * Rq > c[k].th) ger += g_taer;
+            const double ged = g_ed[k][q] * fpr + (Gq > c[k].th ? g_tad : 0.0);
+            a.gbark_ref[(int64_t(item) * L.frames + frame) * nb + band] = static_cast<float>(ger * r[k]);
+            a.gbark_deg[(int64_t(item) * L.frames + frame) * nb + band] = static_cast<float>(ged);
+            part[local][band] = ger * Rq;
         }
     }
     __syncthreads();
-    if (wave == 0 && live) {
-        double s = 0.0;
-        for (int f = 0; f < kTile; ++f) s += part[f][lane];
-        region<double>(a.bw, L.grpart)[(int64_t(item) * L.ntile + tile) * nb + lane] = s;
+    if (wave == 0) {
+#pragma unroll
+        for (int k = 0; k < kBPL; ++k) {
+            if (!live[k]) continue;
+            const int band = lane + kWave * k;
+            double s = 0.0;
+            for (int f = 0; f < kTile; ++f) s += part[f][band];
+            region<double>(a.bw, L.grpart)[(int64_t(item) * L.ntile + tile) * nb + band] = s;
+        }
     }
 }
 
@@ -923,6 +993,7 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
 // spectra, and the mean band power scatter of the backward
 // ---------------------------------------------------------------------------
 
+template <int kBPL>
 __global__ void __launch_bounds__(kWave) chain_partials_kernel(PipeArgs a) {
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
@@ -931,28 +1002,48 @@ __global__ void __launch_bounds__(kWave) chain_partials_kernel(PipeArgs a) {
     const int tile = blockIdx.x - item * L.ntile;
     const int t0 = tile * kTile;
     const int lane = threadIdx.x;
-    const bool live = lane < nb;
-    const double th100 = live ? 100.0 * t.threshs[lane] : 0.0;
+    bool live[kBPL];
+    double th100[kBPL], pr[kBPL], pd[kBPL];
+#pragma unroll
+    for (int k = 0; k < kBPL; ++k) {
+        live[k] = lane + kWave * k < nb;
+        th100[k] = live[k] ? 100.0 * t.threshs[lane + kWave * k] : 0.0;
+        pr[k] = pd[k] = 0.0;
+    }
     const float *bref = a.bark_ref + int64_t(item) * L.frames * nb;
     const float *bdeg = a.bark_deg + int64_t(item) * L.frames * nb;
-    double pr = 0.0, pd = 0.0;
     for (int local = 0; local < kTile; ++local) {
         const int64_t frame = t0 + local;
         if (frame >= L.frames) break;
-        const double r = live ? static_cast<double>(bref[frame * nb + lane]) : 0.0;
-        const double d = live ? static_cast<double>(bdeg[frame * nb + lane]) : 0.0;
-        const double total = wave_sum(live && r > th100 ? r : 0.0);
+        double rv[kBPL], dv[kBPL];
+        double aud = 0.0;
+#pragma unroll
+        for (int k = 0; k < kBPL; ++k) {
+            const int64_t o = frame * nb + lane + kWave * k;
+            rv[k] = live[k] ? static_cast<double>(bref[o]) : 0.0;
+            dv[k] = live[k] ? static_cast<double>(bdeg[o]) : 0.0;
+            const double x = live[k] && rv[k] > th100[k] ? rv[k] : 0.0;
+            aud = k == 0 ? x : aud + x;
+        }
+        const double total = wave_sum(aud);
         const bool keep = total >= 1e7;
         if (lane == 0) region<float>(a.ws, L.keep)[int64_t(item) * L.frames + frame] = keep ? 1.0f : 0.0f;
-        if (keep && r > th100) pr += r;
-        if (keep && d > th100) pd += d;
+#pragma unroll
+        for (int k = 0; k < kBPL; ++k) {
+            if (keep && rv[k] > th100[k]) pr[k] += rv[k];
+            if (keep && dv[k] > th100[k]) pd[k] += dv[k];
+        }
     }
-    if (live) {
-        region<double>(a.ws, L.bandref)[(int64_t(item) * L.ntile + tile) * nb + lane] = pr;
-        region<double>(a.ws, L.banddeg)[(int64_t(item) * L.ntile + tile) * nb + lane] = pd;
+#pragma unroll
+    for (int k = 0; k < kBPL; ++k) {
+        if (!live[k]) continue;
+        const int64_t o = (int64_t(item) * L.ntile + tile) * nb + lane + kWave * k;
+        region<double>(a.ws, L.bandref)[o] = pr[k];
+        region<double>(a.ws, L.banddeg)[o] = pd[k];
     }
 }
 
+template <int kBPL>
 __global__ void __launch_bounds__(kWave) chain_meanpow_kernel(PipeArgs a) {
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
@@ -961,29 +1052,33 @@ __global__ void __launch_bounds__(kWave) chain_meanpow_kernel(PipeArgs a) {
     const int tile = blockIdx.x - item * L.ntile;
     const int t0 = tile * kTile;
     const int lane = threadIdx.x;
-    if (lane >= nb) return;
     const double *gp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * nb;
-    double g = 0.0;  // the summation order of stft_bwd_kernel
-    for (int w = 0; w < kBwdFrames; ++w) g += tile_partial(gp, L.ntile, w, kBwdFrames, lane, nb);
-    const double ratio = band_array(a, kRatio)[item * nb + lane];
-    const double mref = band_array(a, kMref)[item * nb + lane];
-    const double gr = (ratio >= 0.01 && ratio <= 100.0) ? g : 0.0;
-    const double inv = 1.0 / (mref + 1000.0);
-    const double frames_f = static_cast<double>(L.frames);
-    const double gm_ref = -gr * ratio * inv / frames_f;
-    const double gm_deg = gr * inv / frames_f;
-    const double th100 = 100.0 * t.threshs[lane];
     const float *keep = region<float>(a.ws, L.keep) + int64_t(item) * L.frames;
-    for (int local = 0; local < kTile; ++local) {
-        const int64_t frame = t0 + local;
-        if (frame >= L.frames) break;
-        if (keep[frame] == 0.0f) continue;
-        const int64_t o = (int64_t(item) * L.frames + frame) * nb + lane;
-        if (static_cast<double>(a.bark_ref[o]) > th100) {
-            a.gbark_ref[o] = static_cast<float>(static_cast<double>(a.gbark_ref[o]) + gm_ref);
-        }
-        if (static_cast<double>(a.bark_deg[o]) > th100) {
-            a.gbark_deg[o] = static_cast<float>(static_cast<double>(a.gbark_deg[o]) + gm_deg);
+    const double frames_f = static_cast<double>(L.frames);
+#pragma unroll
+    for (int k = 0; k < kBPL; ++k) {
+        const int band = lane + kWave * k;
+        if (band >= nb) continue;
+        double g = 0.0;  // the summation order of stft_bwd_kernel
+        for (int w = 0; w < kBwdFrames; ++w) g += tile_partial(gp, L.ntile, w, kBwdFrames, band, nb);
+        const double ratio = band_array(a, kRatio)[item * nb + band];
+        const double mref = band_array(a, kMref)[item * nb + band];
+        const double gr = (ratio >= 0.01 && ratio <= 100.0) ? g : 0.0;
+        const double inv = 1.0 / (mref + 1000.0);
+        const double gm_ref = -gr * ratio * inv / frames_f;
+        const double gm_deg = gr * inv / frames_f;
+        const double th100 = 100.0 * t.threshs[band];
+        for (int local = 0; local < kTile; ++local) {
+            const int64_t frame = t0 + local;
+            if (frame >= L.frames) break;
+            if (keep[frame] == 0.0f) continue;
+            const int64_t o = (int64_t(item) * L.frames + frame) * nb + band;
+            if (static_cast<double>(a.bark_ref[o]) > th100) {
+                a.gbark_ref[o] = static_cast<float>(static_cast<double>(a.gbark_ref[o]) + gm_ref);
+            }
+            if (static_cast<double>(a.bark_deg[o]) > th100) {
+                a.gbark_deg[o] = static_cast<float>(static_cast<double>(a.gbark_deg[o]) + gm_deg);
+            }
         }
     }
 }
@@ -1118,19 +1213,26 @@ using StftBwdReal = float;
 // BASELINE c2 and c5 respectively).  The results are the same either way.
 constexpr unsigned kChainWideGrid = 512;
 
+// Up to 64 bands a lane holds one band; 65 .. 128 bands take two per lane
+// (band lane + 64), with 4 wavefronts per workgroup for the larger register
+// footprint.
 static void launch_chain_fwd(const PipeArgs &a, unsigned grid, hipStream_t stream) {
-    if (grid <= kChainWideGrid) {
-        hipLaunchKernelGGL(chain_fwd_kernel<8>, dim3(grid), dim3(kWave * 8), 0, stream, a);
+    if (a.L.nb > kWave) {
+        hipLaunchKernelGGL((chain_fwd_kernel<4, 2>), dim3(grid), dim3(kWave * 4), 0, stream, a);
+    } else if (grid <= kChainWideGrid) {
+        hipLaunchKernelGGL((chain_fwd_kernel<8, 1>), dim3(grid), dim3(kWave * 8), 0, stream, a);
     } else {
-        hipLaunchKernelGGL(chain_fwd_kernel<4>, dim3(grid), dim3(kWave * 4), 0, stream, a);
+        hipLaunchKernelGGL((chain_fwd_kernel<4, 1>), dim3(grid), dim3(kWave * 4), 0, stream, a);
     }
 }
 
 static void launch_chain_bwd(const PipeArgs &a, unsigned grid, hipStream_t stream) {
-    if (grid <= kChainWideGrid) {
-        hipLaunchKernelGGL(chain_bwd_kernel<16>, dim3(grid), dim3(kWave * 16), 0, stream, a);
+    if (a.L.nb > kWave) {
+        hipLaunchKernelGGL((chain_bwd_kernel<4, 2>), dim3(grid), dim3(kWave * 4), 0, stream, a);
+    } else if (grid <= kChainWideGrid) {
+        hipLaunchKernelGGL((chain_bwd_kernel<16, 1>), dim3(grid), dim3(kWave * 16), 0, stream, a);
     } else {
-        hipLaunchKernelGGL(chain_bwd_kernel<4>, dim3(grid), dim3(kWave * 4), 0, stream, a);
+        hipLaunchKernelGGL((chain_bwd_kernel<4, 1>), dim3(grid), dim3(kWave * 4), 0, stream, a);
     }
 }
 
@@ -1369,7 +1471,11 @@ extern "C" int pesq_chain_forward(const float *ref_bark, const float *deg_bark, 
     a.d_symm = d_symm;
     a.d_asymm = d_asymm;
     const unsigned grid = static_cast<unsigned>(batch * a.L.ntile);
-    hipLaunchKernelGGL(chain_partials_kernel, dim3(grid), dim3(kWave), 0, stream, a);
+    if (a.L.nb > kWave) {
+        hipLaunchKernelGGL(chain_partials_kernel<2>, dim3(grid), dim3(kWave), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(chain_partials_kernel<1>, dim3(grid), dim3(kWave), 0, stream, a);
+    }
     PESQ_CHECK_LAUNCH("chain partials");
     launch_chain_fwd(a, grid, stream);
     PESQ_CHECK_LAUNCH("chain");
@@ -1399,7 +1505,11 @@ extern "C" int pesq_chain_backward(const float *g_symm, const float *g_asymm, co
     const unsigned grid = static_cast<unsigned>(batch * a.L.ntile);
     launch_chain_bwd(a, grid, stream);
     PESQ_CHECK_LAUNCH("chain backward");
-    hipLaunchKernelGGL(chain_meanpow_kernel, dim3(grid), dim3(kWave), 0, stream, a);
+    if (a.L.nb > kWave) {
+        hipLaunchKernelGGL(chain_meanpow_kernel<2>, dim3(grid), dim3(kWave), 0, stream, a);
+    } else {
+        hipLaunchKernelGGL(chain_meanpow_kernel<1>, dim3(grid), dim3(kWave), 0, stream, a);
+    }
     PESQ_CHECK_LAUNCH("chain mean power backward");
     return PESQ_OK;
 }

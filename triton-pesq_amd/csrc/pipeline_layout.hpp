@@ -25,7 +25,7 @@ struct PipeLayout {
     int64_t nblk = 0, ntile = 0, nhoptile = 0, nwin = 0;
     int64_t row0 = 0, nrg = 0;  // stacked rows that receive gradients
     int grad_mask = 0;
-    int nb = kBands;            // Bark bands (the stand-alone chain takes 1 .. 64)
+    int nb = kBands;            // Bark bands (the stand-alone chain takes 1 .. 128)
 
     // forward workspace
     size_t aggr = 0, energy = 0, p = 0, f = 0, rowconst = 0, bark = 0, keep = 0;

@@ -8,7 +8,7 @@
 
 namespace pesq {
 
-constexpr int kMaxChainBands = kWave;  // one band per lane
+constexpr int kMaxChainBands = 2 * kWave;  // at most two bands per lane
 
 struct ModelTable {
     IirTable iir;                 // A = level alignment band pass, B = pre-emphasis
@@ -19,7 +19,7 @@ struct ModelTable {
     int32_t band_end[kBands];     // one past the last bin of band i
     int32_t bin_band[kHalf];      // band owning bin f, -1 if none (bin 0 is -1)
     double corr[kBands];          // power density correction per band
-    // per band chain constants (the stand-alone chain takes up to 64 bands)
+    // per band chain constants (the stand-alone chain takes up to 128 bands)
     double threshs[kMaxChainBands];     // hearing thresholds
     double exps[kMaxChainBands];        // Zwicker exponents
     double loud_scale[kMaxChainBands];  // sl (2 th)^e

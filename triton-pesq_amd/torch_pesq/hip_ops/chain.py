@@ -16,7 +16,7 @@ from ._common import check_input
 __all__ = ["HipPesqChain"]
 
 #: bands of the stand-alone chain, one per lane of a wavefront
-_MAX_BANDS = 64
+_MAX_BANDS = 128
 
 
 def _pack_chain(threshs, exps, widths, total_width, sl) -> torch.Tensor:
@@ -105,7 +105,7 @@ class HipPesqChain(torch.nn.Module):
             raise ValueError("Hearing thresholds have to be strictly positive.")
         if threshs.numel() > _MAX_BANDS:
             raise ValueError(
-                f"The HIP chain takes at most {_MAX_BANDS} bands (one per lane of a "
+                f"The HIP chain takes at most {_MAX_BANDS} bands (two per lane of a "
                 f"wavefront), got {threshs.numel()}."
             )
         self.total_width, self.sl = float(total_width), float(sl)
