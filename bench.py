@@ -219,8 +219,8 @@ STAGES = {
     "fwd_scans": ("fwd", 0x3, ["iir_aggregate_kernel<5,1,PipeFwdMode,true>",
                                "iir_output_kernel<5,1,PipeFwdMode,true,true>"]),
     "fwd_stft": ("fwd", 0x4, ["stft_fwd_kernel<double,false,8>"]),
-    "fwd_chain": ("fwd", 0x18, ["chain_fwd_kernel<8>", "chain_final_kernel"]),
-    "bwd_chain": ("bwd", 0x1, ["chain_bwd_kernel<16>"]),
+    "fwd_chain": ("fwd", 0x18, ["chain_fwd_kernel<8,1>", "chain_final_kernel"]),
+    "bwd_chain": ("bwd", 0x1, ["chain_bwd_kernel<16,1>"]),
     "bwd_stft": ("bwd", 0x2, ["stft_bwd_kernel<float>"]),
     "bwd_scans": ("bwd", 0xC, ["iir_aggregate_kernel<5,1,PipeBwdMode,true>",
                                "iir_output_kernel<5,1,PipeBwdMode,true,true>"]),
