@@ -436,13 +436,13 @@ def diagnose(config: int, steps: int, warmup: int) -> dict:
         deg16 = model.resampler(deg.detach()) if fs != 16000 else deg.detach()
     if fs != 16000:
         # one resampler launch each way over the rows the step resamples
-        from torch_pesq.hip_ops.resample import _ResampleAdjoint, _ResampleFunction
+        from torch_pesq.hip_ops.resample import resample_launch
 
         rs = model.resampler
         n_out = ref16.shape[1]
         g = torch.ones_like(deg16)
-        fwd_ms = timed(lambda: _ResampleFunction.forward(_Ctx(), ref, rs, n_out), steps)[1]
-        bwd_ms = timed(lambda: _ResampleAdjoint.forward(_Ctx(), g, rs, ref.shape[1]), steps)[1]
+        fwd_ms = timed(lambda: resample_launch(ref, n_out, rs, True), steps)[1]
+        bwd_ms = timed(lambda: resample_launch(g, ref.shape[1], rs, False), steps)[1]
         src_bytes = ref.numel() * 4
         dst_bytes = ref16.numel() * 4
         out["resample"] = {
@@ -461,10 +461,6 @@ def diagnose(config: int, steps: int, warmup: int) -> dict:
     }
     out["model_bytes_16k"] = total
     return out
-
-
-class _Ctx:
-    """Stand-in autograd context for timing a Function's forward alone."""
 
 
 def main(argv=None):

@@ -39,6 +39,29 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.pesq_abi_version() >= 1
 
 
+def test_torch_extension_loads_and_shares_the_library():
+    ext = _lib.torch_ext()
+    assert callable(ext.pipeline)
+    # the extension resolves libpesq_hip.so by soname to the copy ctypes loaded
+    maps = Path("/proc/self/maps").read_text().splitlines()
+    paths = {line.split()[-1] for line in maps if line.endswith("libpesq_hip.so")}
+    assert paths == {str(_lib.LIB_PATH.resolve())}
+    # host tensors are refused before any library call
+    table = torch.zeros(_lib.library().pesq_model_table_bytes(), dtype=torch.uint8)
+    x = torch.zeros(1, 16000, requires_grad=True)
+    with pytest.raises(RuntimeError, match="must be GPU tensors"):
+        ext.pipeline(x, x.detach(), table, 1.0)
+
+    from torch_pesq.hip_ops.resample import HipResample
+
+    rs = HipResample(48000, 16000)
+    assert rs.plan_bytes.numel() == ctypes.sizeof(_lib.ResamplePlanInfo)
+    assert not rs.plan_bytes.is_cuda
+    tables = (rs.kernel, rs.tap_lo, rs.tap_hi, rs.phase_lo, rs.phase_hi, rs.plan, rs.plan_bytes)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        ext.resample(torch.zeros(2, 4800), 1600, *tables, rs.orig_step, rs.new_step, rs.width)
+
+
 def test_product_tables_match_golden():
     for key in (
         "nr_of_hz_bands_per_bark_band_16k",

@@ -298,3 +298,21 @@ def test_error_conventions(model):
     with pytest.raises(ValueError):
         short = torch.from_numpy(ref[:, :5000]).cuda()
         model(short, short)
+
+
+def test_create_graph_and_double_backward(model):
+    """The backward is differentiable once (Python's ``@once_differentiable``)."""
+    ref, deg = speech_like_pair(1, 16000, seed=15, noise=0.1)
+    r = torch.from_numpy(ref).cuda()
+    d = torch.from_numpy(deg).cuda().requires_grad_(True)
+    loss = model(r, d)
+    (plain,) = torch.autograd.grad(loss, d, retain_graph=True)
+    # create_graph with constant upstream gradients: same values, nothing to differentiate
+    (g,) = torch.autograd.grad(loss, d, create_graph=True, retain_graph=True)
+    assert torch.equal(g, plain) and not g.requires_grad
+    # upstream gradients that require grad: a backward through the result raises
+    w = torch.ones_like(loss, requires_grad=True)
+    (g,) = torch.autograd.grad(loss, d, grad_outputs=w, create_graph=True)
+    assert torch.equal(g.detach(), plain) and g.requires_grad
+    with pytest.raises(RuntimeError, match="differentiate twice"):
+        g.sum().backward()

@@ -17,6 +17,7 @@ __all__ = [
     "ResamplePlanInfo",
     "ModelConstants",
     "library",
+    "torch_ext",
     "check",
     "stream_handle",
     "MAX_SECTIONS",
@@ -197,6 +198,34 @@ def library():
             fn.argtypes = argtypes
         _LIB = lib
     return _LIB
+
+
+_EXT = None
+
+
+def torch_ext():
+    """The PyTorch extension module ``_pesq_torch`` (autograd nodes in C++).
+
+    It links ``libpesq_hip.so`` by its soname, so loading :func:`library`
+    first makes both use the same copy of the library.
+    """
+
+    global _EXT
+    if _EXT is None:
+        library()
+        path = LIB_PATH.with_name("_pesq_torch.so")
+        if not path.exists():
+            raise RuntimeError(
+                f"The PESQ PyTorch extension is not built ({path} is missing). Run "
+                "`python triton-pesq_amd/build.py` (or `__graft_entry__.build()`)."
+            )
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("torch_pesq._pesq_torch", path)
+        module = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(module)
+        _EXT = module
+    return _EXT
 
 
 def check(status: int, what: str = "") -> None:

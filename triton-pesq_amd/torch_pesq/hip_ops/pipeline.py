@@ -1,4 +1,4 @@
-"""Fused PESQ pipeline as one autograd function.
+"""Host calls of the fused PESQ pipeline.
 
 Forward: ``pesq_pipeline_forward`` (five kernels) evaluates, for 16 kHz rows,
 everything ``PesqLossTriton.raw`` + ``mos`` + ``forward`` compute in the
@@ -7,8 +7,11 @@ normalisation, level alignment, pre-emphasis, STFT, Bark, the perceptual chain
 and the MOS epilogue.  Backward: ``pesq_pipeline_backward`` (four kernels).
 
 The forward workspace carries the state the backward reads (the filtered and
-pre-emphasised signals, Bark spectra, chain intermediates); it is saved on the
-autograd context.
+pre-emphasised signals, Bark spectra, chain intermediates).  The autograd node
+that saves it between the two calls is C++ (``csrc/torch_autograd.cpp``,
+reached through ``_lib.torch_ext().pipeline``), so that the backward runs no
+Python on autograd's worker thread; the functions here make the same two calls
+from Python for measurement and the stage tests.
 """
 
 import ctypes
@@ -20,7 +23,6 @@ from .. import _lib
 from .iir import parallel_sections, sections_struct
 
 __all__ = [
-    "PipelineFunction",
     "pack_model_table",
     "pipeline_forward",
     "pipeline_backward",
@@ -161,29 +163,3 @@ def pipeline_backward(grads, workspace, table, batch, length, factor, grad_mask)
             "pesq_pipeline_backward",
         )
     return g_ref, g_deg
-
-
-class PipelineFunction(torch.autograd.Function):
-    """``(ref, deg) -> (d_symm, d_asymm, mos, loss)`` for 16 kHz rows."""
-
-    @staticmethod
-    def forward(ctx, ref, deg, table, factor):
-        grad_mask = (_lib.GRAD_REF if ctx.needs_input_grad[0] else 0) | (
-            _lib.GRAD_DEG if ctx.needs_input_grad[1] else 0
-        )
-        out, workspace = pipeline_forward(ref, deg, table, factor, grad_mask)
-        ctx.set_materialize_grads(False)
-        ctx.save_for_backward(workspace, table)
-        ctx.meta = (ref.shape[0], ref.shape[1], grad_mask, float(factor))
-        return out[0], out[1], out[2], out[3]
-
-    @staticmethod
-    @torch.autograd.function.once_differentiable
-    def backward(ctx, g_symm, g_asymm, g_mos, g_loss):
-        batch, length, grad_mask, factor = ctx.meta
-        grads = (g_symm, g_asymm, g_mos, g_loss)
-        if grad_mask == 0 or all(g is None for g in grads):
-            return None, None, None, None
-        workspace, table = ctx.saved_tensors
-        g_ref, g_deg = pipeline_backward(grads, workspace, table, batch, length, factor, grad_mask)
-        return g_ref, g_deg, None, None

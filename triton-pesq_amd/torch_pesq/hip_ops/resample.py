@@ -3,9 +3,10 @@
 Same constructor and attributes as the reference (``kernel``, ``kernel_t``
 is not needed, ``width``, ``orig_step``, ``new_step``).  Forward and adjoint
 are HIP kernels (``csrc/resample.hip``) that evaluate only the non-zero taps
-of each phase; the adjoint is itself differentiable (its derivative is the
-forward), which gives a working double backward like the reference's
-``_ResampleAdjoint`` (``resample.py:381-410``).
+of each phase.  The autograd nodes are C++ (``csrc/torch_autograd.cpp``):
+the adjoint is itself differentiable (its derivative is the forward), which
+gives a working double backward like the reference's ``_ResampleAdjoint``
+(``resample.py:381-410``).
 """
 
 import ctypes
@@ -18,27 +19,27 @@ from .. import _lib
 from ._common import check_input
 from .sinc import resample_length, sinc_resample_kernel
 
-__all__ = ["HipResample"]
+__all__ = ["HipResample", "resample_launch"]
 
 _INDEX_LIMIT = 2**31 - 1
 
 
-def _launch(fn_name, src, n_out_or_in, module, forward: bool):
+def resample_launch(src: torch.Tensor, n_other: int, module: "HipResample", forward: bool):
+    """One forward (``[rows, n_in] -> [rows, n_other]``) or adjoint
+    (``[rows, n_out] -> [rows, n_other]``) launch, outside autograd.
+
+    The same library calls the C++ autograd nodes make; used to time the
+    kernels alone.
+    """
+
     lib = _lib.library()
     rows = src.shape[0]
-    if forward:
-        n_in, n_out = src.shape[1], n_out_or_in
-        out = torch.empty((rows, n_out), dtype=torch.float32, device=src.device)
-        lo, hi = module.tap_lo, module.tap_hi
-    else:
-        n_out, n_in = src.shape[1], n_out_or_in
-        out = torch.empty((rows, n_in), dtype=torch.float32, device=src.device)
-        lo, hi = module.phase_lo, module.phase_hi
+    n_in, n_out = (src.shape[1], n_other) if forward else (n_other, src.shape[1])
+    out = torch.empty((rows, n_other), dtype=torch.float32, device=src.device)
     info = module.plan_info
-    tiled = info.fwd_span > 0 if forward else info.bwd_span > 0
-    if tiled:
-        name = "pesq_resample_plan_forward" if forward else "pesq_resample_plan_backward"
-        with torch.cuda.device(src.device):
+    with torch.cuda.device(src.device):
+        if (info.fwd_span if forward else info.bwd_span) > 0:
+            name = "pesq_resample_plan_forward" if forward else "pesq_resample_plan_backward"
             _lib.check(
                 getattr(lib, name)(
                     _lib.ptr(src), _lib.ptr(out), rows, n_in, n_out, ctypes.byref(info),
@@ -46,54 +47,18 @@ def _launch(fn_name, src, n_out_or_in, module, forward: bool):
                 ),
                 name,
             )
-        return out
-    with torch.cuda.device(src.device):
+            return out
+        name = "pesq_resample_forward" if forward else "pesq_resample_backward"
+        lo, hi = (module.tap_lo, module.tap_hi) if forward else (module.phase_lo, module.phase_hi)
         _lib.check(
-            getattr(lib, fn_name)(
-                _lib.ptr(src),
-                _lib.ptr(out),
-                rows,
-                n_in,
-                n_out,
-                _lib.ptr(module.kernel),
-                _lib.ptr(lo),
-                _lib.ptr(hi),
-                module.orig_step,
-                module.new_step,
-                module.width,
-                module.kernel.shape[1],
-                _lib.stream_handle(src.device),
+            getattr(lib, name)(
+                _lib.ptr(src), _lib.ptr(out), rows, n_in, n_out, _lib.ptr(module.kernel),
+                _lib.ptr(lo), _lib.ptr(hi), module.orig_step, module.new_step, module.width,
+                module.kernel.shape[1], _lib.stream_handle(src.device),
             ),
-            fn_name,
+            name,
         )
     return out
-
-
-class _ResampleAdjoint(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, grad_out, module, n_in):
-        ctx.module, ctx.n_out = module, grad_out.shape[1]
-        return _launch("pesq_resample_backward", grad_out.contiguous(), n_in, module, False)
-
-    @staticmethod
-    def backward(ctx, grad_grad):
-        if not ctx.needs_input_grad[0]:
-            return None, None, None
-        out = _launch("pesq_resample_forward", grad_grad.contiguous(), ctx.n_out, ctx.module, True)
-        return out, None, None
-
-
-class _ResampleFunction(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, waveform, module, n_out):
-        ctx.module, ctx.n_in = module, waveform.shape[1]
-        return _launch("pesq_resample_forward", waveform, n_out, module, True)
-
-    @staticmethod
-    def backward(ctx, grad_out):
-        if not ctx.needs_input_grad[0]:
-            return None, None, None
-        return _ResampleAdjoint.apply(grad_out, ctx.module, ctx.n_in), None, None
 
 
 class HipResample(torch.nn.Module):
@@ -165,6 +130,8 @@ class HipResample(torch.nn.Module):
         _lib.check(lib.pesq_resample_plan(*args, ctypes.byref(info), plan.data_ptr()),
                    "pesq_resample_plan")
         self.plan_info = info
+        # host copy of the geometry for the C++ autograd nodes (stays on the CPU)
+        self.plan_bytes = torch.frombuffer(bytearray(bytes(info)), dtype=torch.uint8)
         self.register_buffer("plan", plan)
 
     def output_length(self, n_samples: int) -> int:
@@ -187,7 +154,10 @@ class HipResample(torch.nn.Module):
         slack = 128 * max(self.orig_step, self.new_step) + self.kernel.shape[1]
         if max(shape[-1], n_out) > _INDEX_LIMIT - slack:
             raise RuntimeError("The signal is too long for the resampler's 32 bit launch grid.")
-        out = _ResampleFunction.apply(packed, self, n_out)
+        out = _lib.torch_ext().resample(
+            packed, n_out, self.kernel, self.tap_lo, self.tap_hi, self.phase_lo, self.phase_hi,
+            self.plan, self.plan_bytes, self.orig_step, self.new_step, self.width,
+        )
         return out.reshape(shape[:-1] + out.shape[-1:])
 
     def extra_repr(self) -> str:

@@ -163,8 +163,8 @@ class PesqLoss(torch.nn.Module):
     # -- pipeline -----------------------------------------------------------
 
     def _run(self, ref: torch.Tensor, deg: torch.Tensor):
+        from . import _lib
         from .hip_ops._common import check_input
-        from .hip_ops.pipeline import PipelineFunction
 
         deg, ref = torch.atleast_2d(deg), torch.atleast_2d(ref)
         if ref.shape != deg.shape:
@@ -205,7 +205,7 @@ class PesqLoss(torch.nn.Module):
                 "The loss treats `factor` as a constant, pass a Python float. A tensor "
                 "that requires a gradient would receive none."
             )
-        return PipelineFunction.apply(ref, deg, self.model_table, float(self.factor))
+        return tuple(_lib.torch_ext().pipeline(ref, deg, self.model_table, float(self.factor)))
 
     def _run_stages(self, ref: torch.Tensor, deg: torch.Tensor):
         """The stage sequence of ``PesqLossTriton.raw`` (``triton_ops/loss.py:104-147``).
