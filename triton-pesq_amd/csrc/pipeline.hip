@@ -162,6 +162,10 @@ __device__ __forceinline__ double *frame_array(const PipeArgs &a, int which) {
     return region<double>(a.ws, a.L.frame) + int64_t(which) * a.L.batch * a.L.frames;
 }
 
+__device__ __forceinline__ double *loud_array(const PipeArgs &a, int which) {
+    return region<double>(a.ws, a.L.loud) + int64_t(which) * a.L.batch * a.L.frames * a.L.nb;
+}
+
 __device__ __forceinline__ double *band_array(const PipeArgs &a, int which) {
     return region<double>(a.ws, a.L.band) + int64_t(which) * a.L.batch * a.L.nb;
 }
@@ -183,23 +187,17 @@ __device__ __forceinline__ double loudness(double x, double th, double inv2th, d
     return ls * expm1(e * log1p((x - th) * inv2th));
 }
 
-// loudness and d loudness / dx, sharing the logarithm
-__device__ __forceinline__ void loudness_and_slope(double x, double th, double inv2th, double e,
-                                                   double ls, double &l, double &slope) {
-    if (!(x > th)) {
-        l = slope = 0.0;
-        return;
-    }
-    const double lg = log1p((x - th) * inv2th);
-    l = ls * expm1(e * lg);
-    slope = ls * e * inv2th * exp((e - 1.0) * lg);
+// d loudness / dx from the loudness l itself: with 1 + u = (x + th) / (2 th),
+// l = ls ((1 + u)^e - 1) gives ls e (1 + u)^(e - 1) / (2 th) = e (l + ls) / (x + th)
+__device__ __forceinline__ double loudness_slope(double x, double l, double th, double e,
+                                                 double ls) {
+    return x > th ? e * (l + ls) / (x + th) : 0.0;
 }
 
-// raw asymmetry factor ((ed + 50) / (er + 50))^1.2, inv_er50 = 1 / (er + 50);
-// forward and backward evaluate the same expression, so their clamp decisions
-// (below 3, above 12) agree
-__device__ __forceinline__ double asymmetry(double ed, double inv_er50) {
-    return exp(1.2 * log((ed + 50.0) * inv_er50));
+// raw asymmetry factor ((ed + 50) / (er + 50))^1.2; the backward reads the
+// forward's values, so the clamp decisions (below 3, above 12) agree
+__device__ __forceinline__ double asymmetry(double ed, double er) {
+    return exp(1.2 * log((ed + 50.0) / (er + 50.0)));
 }
 
 __device__ __forceinline__ double sgn(double v) { return v > 0.0 ? 1.0 : (v < 0.0 ? -1.0 : 0.0); }
@@ -520,8 +518,14 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
                 const double u = ld - lr;
                 const double z = fabs(u) - 0.25 * fmin(ld, lr);
                 const double dist = sgn(u) * fmax(z, 0.0);
-                const double asc_raw = asymmetry(ed, 1.0 / (er + 50.0));
+                const double asc_raw = asymmetry(ed, er);
                 const double asc = asc_raw < 3.0 ? 0.0 : fmin(asc_raw, 12.0);
+                if (L.loud_store) {
+                    const int64_t o = (int64_t(item) * L.frames + frame) * nb + lane + kWave * k;
+                    loud_array(a, kLoudRef)[o] = lr;
+                    loud_array(a, kLoudDeg)[o] = ld;
+                    loud_array(a, kAscRaw)[o] = asc_raw;
+                }
                 if (lane + kWave * k >= 1) {
                     const double v = ck.w * dist * inv_sqrt_w;
                     xv = v * v;
@@ -767,15 +771,17 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
                 const BandConsts &ck = c[k];
                 const double Rq = R[k][q], Gq = G[k][q];
                 const double er = r[k] * Rq, ed = fpr * Gq;
-                double lr, ld, slope_r, slope_d;
-                loudness_and_slope(er, ck.th, ck.inv2th, ck.e, ck.ls, lr, slope_r);
-                loudness_and_slope(ed, ck.th, ck.inv2th, ck.e, ck.ls, ld, slope_d);
+                // the forward's loudnesses and asymmetry factor of this (frame, band)
+                const int64_t o = (fo + frame) * nb + lane + kWave * k;
+                const double lr = loud_array(a, kLoudRef)[o];
+                const double ld = loud_array(a, kLoudDeg)[o];
+                const double asc_raw = loud_array(a, kAscRaw)[o];
+                const double slope_r = loudness_slope(er, lr, ck.th, ck.e, ck.ls);
+                const double slope_d = loudness_slope(ed, ld, ck.th, ck.e, ck.ls);
                 const double u = ld - lr;
                 const double z = fabs(u) - 0.25 * fmin(ld, lr);
                 const double su = sgn(u);
                 const double dst = su * fmax(z, 0.0);
-                const double inv_er50 = 1.0 / (er + 50.0), inv_ed50 = 1.0 / (ed + 50.0);
-                const double asc_raw = asymmetry(ed, inv_er50);
                 const double asc = asc_raw < 3.0 ? 0.0 : fmin(asc_raw, 12.0);
 
                 double g_dist = 0.0, g_asc = 0.0;
@@ -795,8 +801,9 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
                 my_er = g_lr * slope_r;
                 my_ed = g_ld * slope_d;
                 if (asc_raw >= 3.0 && asc_raw <= 12.0) {
-                    my_ed += g_asc * 1.2 * asc_raw * inv_ed50;
-                    my_er -= g_asc * 1.2 * asc_raw * inv_er50;
+                    const double g_log = g_asc * 1.2 * asc_raw;  // d asc / d log(ratio)
+                    my_ed += g_log / (ed + 50.0);
+                    my_er -= g_log / (er + 50.0);
                 }
                 xg = my_ed * Gq;
             }

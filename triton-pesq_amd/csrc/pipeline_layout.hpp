@@ -19,6 +19,9 @@ constexpr int kStride = 10;        // PSQM stride (frames)
 enum FrameArray { kTaer, kTad, kFpr0, kFpr1, kH, kSymmRaw, kAsymmRaw, kSymm, kAsymm, kFrameArrays };
 // per band chain arrays, [batch, bands] each
 enum BandArray { kR, kRatio, kMref, kBandArrays };
+// per (frame, band) values of the forward chain that the backward reads,
+// [batch, frames, bands] each: the two loudnesses and the raw asymmetry factor
+enum LoudArray { kLoudRef, kLoudDeg, kAscRaw, kLoudArrays };
 
 struct PipeLayout {
     int64_t batch = 0, len = 0, rows = 0, frames = 0;
@@ -26,10 +29,12 @@ struct PipeLayout {
     int64_t row0 = 0, nrg = 0;  // stacked rows that receive gradients
     int grad_mask = 0;
     int nb = kBands;            // Bark bands (the stand-alone chain takes 1 .. 128)
+    int loud_store = 0;         // the forward writes the `loud` region (a backward follows)
 
     // forward workspace
     size_t aggr = 0, energy = 0, p = 0, f = 0, rowconst = 0, bark = 0, keep = 0;
-    size_t bandref = 0, banddeg = 0, frame = 0, band = 0, psqm = 0, dist = 0, fwd_bytes = 0;
+    size_t bandref = 0, banddeg = 0, frame = 0, band = 0, psqm = 0, dist = 0, loud = 0;
+    size_t fwd_bytes = 0;
     // backward workspace
     size_t gbark = 0, grpart = 0, gp = 0, spart = 0, aggr_b = 0, bwd_bytes = 0;
 
@@ -72,6 +77,8 @@ struct PipeLayout {
         take(band, size_t(kBandArrays) * batch * nb * sizeof(double));
         take(psqm, size_t(2) * batch * nwin * sizeof(double));
         take(dist, size_t(batch) * 2 * sizeof(double));
+        loud_store = mask != 0;
+        take(loud, loud_store ? size_t(kLoudArrays) * batch * frames * nb * sizeof(double) : 0);
         fwd_bytes = off;
 
         off = 0;
@@ -105,6 +112,8 @@ struct PipeLayout {
         take(band, size_t(kBandArrays) * batch * nb * sizeof(double));
         take(psqm, size_t(2) * batch * nwin * sizeof(double));
         take(dist, size_t(batch) * 2 * sizeof(double));
+        loud_store = 1;
+        take(loud, size_t(kLoudArrays) * batch * frames * nb * sizeof(double));
         fwd_bytes = off;
         off = 0;
         take(grpart, size_t(batch) * ntile * nb * sizeof(double));
@@ -121,7 +130,7 @@ struct PipeLayout {
             {"p", p, f},                {"f", f, rowconst},         {"rowconst", rowconst, bark},
             {"bark", bark, keep},       {"keep", keep, bandref},    {"bandref", bandref, banddeg},
             {"banddeg", banddeg, frame}, {"frame", frame, band},    {"band", band, psqm},
-            {"psqm", psqm, dist},       {"dist", dist, fwd_bytes},
+            {"psqm", psqm, dist},       {"dist", dist, loud},       {"loud", loud, fwd_bytes},
         };
         for (const Entry &e : table) {
             if (std::strcmp(e.name, name) == 0) {
