@@ -219,6 +219,11 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
     __shared__ cplx<real> fftbuf[kWaves][kHalf];
     __shared__ float barks[2][kTile][kBands];
     __shared__ float keepflag[kTile];
+    // kLean: the twiddle tables (kHalf entries each) and the window, staged
+    // once per workgroup and read per frame (10 KB; two workgroups per CU
+    // still fit)
+    __shared__ double2 lds_tw256[kLean ? kHalf : 1], lds_tw512[kLean ? kHalf : 1];
+    __shared__ float lds_win[kLean ? kNfft : 1];
 
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
@@ -255,11 +260,19 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
     float *bark = region<float>(a.ws, L.bark) + int64_t(row) * L.frames * kBands;
     cplx<real> *buf = fftbuf[wave];
     real *power_buf = reinterpret_cast<real *>(buf);
-    // kLean reads the twiddles per pass; otherwise they stay in registers
+    // kLean reads the twiddles per pass from LDS; otherwise they stay in registers
     using TW = typename std::conditional<kLean, LazyTwiddles, Twiddles>::type;
     TW tw;
     if constexpr (kLean) {
-        tw = TW{t.tw256, t.tw512, lane};
+        for (int i = threadIdx.x; i < kNfft; i += kWave * kWaves) {
+            if (i < kHalf) {
+                lds_tw256[i] = t.tw256[i];
+                lds_tw512[i] = t.tw512[i];
+            }
+            lds_win[i] = t.window[i];
+        }
+        __syncthreads();
+        tw = TW{lds_tw256, lds_tw512, lane};
     } else {
         tw.load(t.tw256, t.tw512, lane);
     }
@@ -287,14 +300,10 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
             load_frame(p, fn * kHop, L.len, lane, nxt);
         } else {
             if (q > 0) load_frame(p, frame * kHop, L.len, lane, cur);
-            // through reload(): the twiddle and window loads stay inside the
-            // frame loop
-            tw = TW{reload(t.tw256), reload(t.tw512), lane};
-            const float *wp = reload(t.window);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                win[2 * r] = wp[2 * (lane + 64 * r)];
-                win[2 * r + 1] = wp[2 * (lane + 64 * r) + 1];
+                win[2 * r] = lds_win[2 * (lane + 64 * r)];
+                win[2 * r + 1] = lds_win[2 * (lane + 64 * r) + 1];
             }
         }
         auto u = [&](int k) -> real {
@@ -886,6 +895,11 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
     __shared__ double gpart[kBwdFrames][kBands];
     __shared__ float gband[kBwdFrames][kBands];
     __shared__ double scratch[kBwdFrames];
+    // the twiddle tables, window and bin-to-band map, staged once per
+    // workgroup (both FFTs of every frame read them)
+    __shared__ double2 lds_tw256[kHalf], lds_tw512[kHalf];
+    __shared__ float lds_win[kNfft];
+    __shared__ int lds_bin_band[kHalf];
 
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
@@ -916,6 +930,14 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
     // and every wavefront adds the partial sums in wavefront order
     const double *grp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
     if (lane < kBands) gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kBwdFrames, lane, kBands);
+    for (int k = threadIdx.x; k < kNfft; k += kWave * kBwdFrames) {
+        if (k < kHalf) {
+            lds_tw256[k] = t.tw256[k];
+            lds_tw512[k] = t.tw512[k];
+            lds_bin_band[k] = t.bin_band[k];
+        }
+        lds_win[k] = t.window[k];
+    }
     __syncthreads();
     double gm = 0.0;
     if (lane < kBands) {
@@ -931,15 +953,16 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
     const double scale = region<double>(a.ws, L.rowconst)[int64_t(row) * 4 + 2];
     cplx<real> *buf = fftbuf[wave];
     if (live) {
-        // twiddles read per pass (fewer live registers: five wavefronts per SIMD)
-        const LazyTwiddles tw{reload(t.tw256), reload(t.tw512), lane};
+        // twiddles read per pass from LDS (fewer live registers: five
+        // wavefronts per SIMD)
+        const LazyTwiddles tw{lds_tw256, lds_tw512, lane};
         float win[8];
         int bin_band[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            win[2 * r] = t.window[2 * (lane + 64 * r)];
-            win[2 * r + 1] = t.window[2 * (lane + 64 * r) + 1];
-            bin_band[r] = t.bin_band[lane + 64 * r];
+            win[2 * r] = lds_win[2 * (lane + 64 * r)];
+            win[2 * r + 1] = lds_win[2 * (lane + 64 * r) + 1];
+            bin_band[r] = lds_bin_band[lane + 64 * r];
         }
         if (lane < kBands) {
             double g = gbk_v;
