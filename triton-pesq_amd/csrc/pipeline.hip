@@ -222,7 +222,7 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
     // kLean: the twiddle tables (kHalf entries each) and the window, staged
     // once per workgroup and read per frame (10 KB; two workgroups per CU
     // still fit)
-    __shared__ double2 lds_tw256[kLean ? kHalf : 1], lds_tw512[kLean ? kHalf : 1];
+    __shared__ double2 lds_pass[kLean ? kPassTwiddles : 1], lds_tw512[kLean ? kHalf : 1];
     __shared__ float lds_win[kLean ? kNfft : 1];
 
     const ModelTable &t = *a.tab;
@@ -261,18 +261,16 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
     cplx<real> *buf = fftbuf[wave];
     real *power_buf = reinterpret_cast<real *>(buf);
     // kLean reads the twiddles per pass from LDS; otherwise they stay in registers
-    using TW = typename std::conditional<kLean, LazyTwiddles, Twiddles>::type;
+    using TW = typename std::conditional<kLean, LdsTwiddles, Twiddles>::type;
     TW tw;
     if constexpr (kLean) {
         for (int i = threadIdx.x; i < kNfft; i += kWave * kWaves) {
-            if (i < kHalf) {
-                lds_tw256[i] = t.tw256[i];
-                lds_tw512[i] = t.tw512[i];
-            }
+            if (i < kPassTwiddles) lds_pass[i] = pass_twiddle_entry(t.tw256, i);
+            if (i < kHalf) lds_tw512[i] = t.tw512[i];
             lds_win[i] = t.window[i];
         }
         __syncthreads();
-        tw = TW{lds_tw256, lds_tw512, lane};
+        tw = TW{lds_pass, lds_tw512, lane};
     } else {
         tw.load(t.tw256, t.tw512, lane);
     }
@@ -897,7 +895,7 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
     __shared__ double scratch[kBwdFrames];
     // the twiddle tables, window and bin-to-band map, staged once per
     // workgroup (both FFTs of every frame read them)
-    __shared__ double2 lds_tw256[kHalf], lds_tw512[kHalf];
+    __shared__ double2 lds_pass[kPassTwiddles], lds_tw512[kHalf];
     __shared__ float lds_win[kNfft];
     __shared__ int lds_bin_band[kHalf];
 
@@ -931,8 +929,8 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
     const double *grp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
     if (lane < kBands) gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kBwdFrames, lane, kBands);
     for (int k = threadIdx.x; k < kNfft; k += kWave * kBwdFrames) {
+        if (k < kPassTwiddles) lds_pass[k] = pass_twiddle_entry(t.tw256, k);
         if (k < kHalf) {
-            lds_tw256[k] = t.tw256[k];
             lds_tw512[k] = t.tw512[k];
             lds_bin_band[k] = t.bin_band[k];
         }
@@ -955,7 +953,7 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
     if (live) {
         // twiddles read per pass from LDS (fewer live registers: five
         // wavefronts per SIMD)
-        const LazyTwiddles tw{lds_tw256, lds_tw512, lane};
+        const LdsTwiddles tw{lds_pass, lds_tw512, lane};
         float win[8];
         int bin_band[4];
 #pragma unroll

@@ -128,6 +128,36 @@ struct LazyTwiddles {
     __device__ __forceinline__ double2 fold_tw(int r) const { return tw512[lane + 64 * r]; }
 };
 
+// The pass twiddles laid out per (pass, r, k) with k = lane mod ns running
+// fastest, for tables staged in LDS: the reads of one pass are unit stride
+// (pass 1 reads 4 entries, a broadcast), so they do not conflict on the banks.
+//   pass[pass_offset(p) + (r - 1) ns + k] = e^{-2 pi i k r / (4 ns)}, ns = 4^p
+//   fold[f]                               = e^{-2 pi i f / 512}
+constexpr int kPassTwiddles = 3 * (4 + 16 + 64);
+__device__ __forceinline__ constexpr int pass_offset(int p) {
+    return p == 1 ? 0 : (p == 2 ? 3 * 4 : 3 * (4 + 16));
+}
+
+// entry i (0 <= i < kPassTwiddles) of the per pass table, from the 256-point table
+__device__ __forceinline__ double2 pass_twiddle_entry(const double2 *tw256, int i) {
+    const int p = i < pass_offset(2) ? 1 : (i < pass_offset(3) ? 2 : 3);
+    const int ns = 1 << (2 * p);
+    const int j = i - pass_offset(p);
+    const int r = j / ns + 1, k = j % ns;
+    return tw256[(k * r * (64 / ns)) & 255];
+}
+
+struct LdsTwiddles {
+    const double2 *pass, *fold;
+    int lane;
+
+    __device__ __forceinline__ double2 pass_tw(int p, int r) const {
+        const int ns = 1 << (2 * p);
+        return pass[pass_offset(p) + (r - 1) * ns + (lane & (ns - 1))];
+    }
+    __device__ __forceinline__ double2 fold_tw(int r) const { return fold[lane + 64 * r]; }
+};
+
 // In: v[r] = z_{lane + 64 r}.  Out: buf[slot(n)] = Z_n, unnormalised.
 template <typename real, bool kInverse, class TW>
 __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, const TW &tw,
