@@ -178,6 +178,39 @@ __device__ __forceinline__ double tile_partial(const double *base, int64_t ntile
     return n > 0 ? strided_sum(base + int64_t(part) * nb + band, n, int64_t(parts) * nb) : 0.0;
 }
 
+// K sums s_k = sum_{i < n_k} p_k[i * stride], each accumulated in the order
+// i = 0, 1, ... (the value of strided_sum), with the loads of all K sums
+// issued together, kRound per sum at a time, so that they share one memory
+// latency per round.  A sum with n_k = 0 is 0 and loads nothing.
+template <int K, int kRound = 2>
+__device__ __forceinline__ void strided_sums(const double *const (&p)[K], const int (&n)[K],
+                                             int64_t stride, double (&out)[K]) {
+    int nmax = 0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        out[k] = 0.0;
+        nmax = n[k] > nmax ? n[k] : nmax;
+    }
+    for (int i0 = 0; i0 < nmax; i0 += kRound) {
+        double v[K][kRound];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+#pragma unroll
+            for (int u = 0; u < kRound; ++u) {
+                const int i = i0 + u < n[k] ? i0 + u : n[k] - 1;  // clamped, value dropped
+                v[k][u] = n[k] > 0 ? p[k][int64_t(i) * stride] : 0.0;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+#pragma unroll
+            for (int u = 0; u < kRound; ++u) {
+                if (i0 + u < n[k]) out[k] += v[k][u];
+            }
+        }
+    }
+}
+
 // Zwicker loudness sl (2 th)^e ((0.5 + 0.5 x / th)^e - 1) above the threshold,
 // written as loud_scale expm1(e log1p((x - th) / (2 th))) so that bands just
 // above their threshold keep full precision (inv2th = 1 / (2 th)).
@@ -441,14 +474,30 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
     {
         const double *pr = region<double>(a.ws, L.bandref) + int64_t(item) * L.ntile * nb;
         const double *pd = region<double>(a.ws, L.banddeg) + int64_t(item) * L.ntile * nb;
+        constexpr int kMine = kChainSlices / kWaves;  // slices per wavefront
+        static_assert(kMine * kWaves == kChainSlices, "slices split evenly over the wavefronts");
 #pragma unroll
         for (int k = 0; k < kBPL; ++k) {
             const int band = lane + kWave * k;
             if (band < nb) {
+                // tile_partial of both arrays for each of the wavefront's slices,
+                // with all their loads in flight together
+                const double *ptr[2 * kMine];
+                int cnt[2 * kMine];
 #pragma unroll
-                for (int v = wave; v < kChainSlices; v += kWaves) {
-                    part[0][v][band] = tile_partial(pr, L.ntile, v, kChainSlices, band, nb);
-                    part[1][v][band] = tile_partial(pd, L.ntile, v, kChainSlices, band, nb);
+                for (int j = 0; j < kMine; ++j) {
+                    const int v = wave + j * kWaves;
+                    const int n = L.ntile > v ? static_cast<int>((L.ntile - 1 - v) / kChainSlices) + 1 : 0;
+                    ptr[2 * j] = pr + int64_t(v) * nb + band;
+                    ptr[2 * j + 1] = pd + int64_t(v) * nb + band;
+                    cnt[2 * j] = cnt[2 * j + 1] = n;
+                }
+                double sums[2 * kMine];
+                strided_sums(ptr, cnt, int64_t(kChainSlices) * nb, sums);
+#pragma unroll
+                for (int j = 0; j < kMine; ++j) {
+                    part[0][wave + j * kWaves][band] = sums[2 * j];
+                    part[1][wave + j * kWaves][band] = sums[2 * j + 1];
                 }
             }
         }
