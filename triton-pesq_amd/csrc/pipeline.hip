@@ -1138,8 +1138,21 @@ __global__ void __launch_bounds__(kWave) chain_meanpow_kernel(PipeArgs a) {
     for (int k = 0; k < kBPL; ++k) {
         const int band = lane + kWave * k;
         if (band >= nb) continue;
-        double g = 0.0;  // the summation order of stft_bwd_kernel
-        for (int w = 0; w < kBwdFrames; ++w) g += tile_partial(gp, L.ntile, w, kBwdFrames, band, nb);
+        // the summation order of stft_bwd_kernel: the partial of each of its
+        // wavefronts (tiles w, w + kBwdFrames, ...), then those in order; the
+        // loads of all of them in flight together
+        const double *ptr[kBwdFrames];
+        int cnt[kBwdFrames];
+#pragma unroll
+        for (int w = 0; w < kBwdFrames; ++w) {
+            ptr[w] = gp + int64_t(w) * nb + band;
+            cnt[w] = L.ntile > w ? static_cast<int>((L.ntile - 1 - w) / kBwdFrames) + 1 : 0;
+        }
+        double parts[kBwdFrames];
+        strided_sums(ptr, cnt, int64_t(kBwdFrames) * nb, parts);
+        double g = 0.0;
+#pragma unroll
+        for (int w = 0; w < kBwdFrames; ++w) g += parts[w];
         const double ratio = band_array(a, kRatio)[item * nb + band];
         const double mref = band_array(a, kMref)[item * nb + band];
         const double gr = (ratio >= 0.01 && ratio <= 100.0) ? g : 0.0;
