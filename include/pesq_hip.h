@@ -179,6 +179,20 @@ int pesq_pipeline_backward_stages(const float *g_symm, const float *g_asymm, con
 int pesq_pipeline_region(int64_t batch, int64_t len, int grad_mask, const char *name,
                          size_t *offset, size_t *bytes);
 
+/* Names of the kernels that pesq_pipeline_forward (backward == 0) or
+ * pesq_pipeline_backward (backward != 0) launches for this shape, in launch
+ * order, separated by ';' (for example "iir_aggregate_kernel<5, 1,
+ * PipeFwdMode, true>;...;chain_final_kernel").  Writes at most `capacity`
+ * bytes including the terminating NUL into `names` (may be NULL) and the
+ * full size including the NUL into *needed (may be NULL).  Host only, no GPU
+ * call.  The kernel variants are chosen by grid size (lane states stored or
+ * recomputed, block prefix fused or launched, frames per wavefront), so tests
+ * use this to show which variants a shape exercises.  No counterpart in the
+ * reference, whose Triton kernels are autotuned rather than chosen by
+ * shape. */
+int pesq_pipeline_kernels(int64_t batch, int64_t len, int grad_mask, int backward, char *names,
+                          size_t capacity, size_t *needed);
+
 /* ----------------------------------------------------------------------- */
 /* IIR filter (TritonIIR, torch_pesq/triton_ops/iir.py:1266-1482)           */
 /* ----------------------------------------------------------------------- */

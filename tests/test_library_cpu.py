@@ -335,3 +335,146 @@ def test_graft_entry_exposes_build_and_smoke():
     import __graft_entry__ as entry
 
     assert callable(entry.build) and callable(entry.smoke)
+
+
+# -- kernel variants per shape (host query, no GPU call) ----------------------
+
+#: (batch, 16 kHz length, grad mask) -> kernels of the forward and the backward
+#: pass.  The variants are chosen by grid size: lane states are stored for
+#: grids of up to 8192 scan wavefronts and recomputed above; the block prefix
+#: is fused into the output pass for rows of up to 128 blocks; the STFT and
+#: chain kernels of grids above 512 workgroups take four frames per wavefront.
+VARIANTS = {
+    # BASELINE c2: 16 rows x 125 blocks, 8 x 32 tiles
+    (8, 128000, 2): (
+        ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, true>",
+         "stft_fwd_kernel<double, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
+        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float>",
+         "iir_aggregate_kernel<5, 1, PipeBwdMode, true>",
+         "iir_output_kernel<5, 1, PipeBwdMode, true, true>"],
+    ),
+    # BASELINE c4: 938 blocks per row (prefix kernel), 4 x 235 = 940 tiles
+    (4, 960000, 2): (
+        ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>", "iir_prefix_kernel<6>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
+         "stft_fwd_kernel<double, true, 8>", "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
+        ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float>",
+         "iir_aggregate_kernel<5, 1, PipeBwdMode, true>", "iir_prefix_kernel<6>",
+         "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
+    ),
+    # BASELINE c5 after the 3:1 resampler: 512 x 63 = 32256 forward scan
+    # wavefronts, 256 x 63 = 16128 backward ones (both above 8192)
+    (256, 64000, 2): (
+        ["iir_aggregate_kernel<5, 1, PipeFwdMode, false>", "iir_prefix_kernel<6>",
+         "iir_output_kernel<5, 1, PipeFwdMode, false, false>",
+         "stft_fwd_kernel<double, true, 8>", "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
+        ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float>",
+         "iir_aggregate_kernel<5, 1, PipeBwdMode, false>", "iir_prefix_kernel<6>",
+         "iir_output_kernel<5, 1, PipeBwdMode, false, false>"],
+    ),
+    # BASELINE c3 after the 441:160 resampler: a small grid like c2
+    (16, 64000, 2): (
+        ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, true>",
+         "stft_fwd_kernel<double, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
+        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float>",
+         "iir_aggregate_kernel<5, 1, PipeBwdMode, true>",
+         "iir_output_kernel<5, 1, PipeBwdMode, true, true>"],
+    ),
+}
+
+
+@pytest.mark.parametrize("shape", sorted(VARIANTS))
+def test_pipeline_kernel_variants_per_shape(shape):
+    fwd, bwd = VARIANTS[shape]
+    assert _lib.pipeline_kernels(*shape, backward=False) == fwd
+    assert _lib.pipeline_kernels(*shape, backward=True) == bwd
+
+
+def test_pipeline_kernel_query_edges():
+    lib = _lib.library()
+    needed = ctypes.c_size_t(0)
+    assert lib.pesq_pipeline_kernels(8, 128000, 2, 0, None, 0, ctypes.byref(needed)) == 0
+    full = ctypes.create_string_buffer(int(needed.value))
+    assert lib.pesq_pipeline_kernels(8, 128000, 2, 0, full, len(full), None) == 0
+    assert len(full.value) + 1 == needed.value
+    # a short buffer gets a truncated, terminated prefix
+    short = ctypes.create_string_buffer(10)
+    assert lib.pesq_pipeline_kernels(8, 128000, 2, 0, short, len(short), None) == 0
+    assert short.value == full.value[:9]
+    # the backward needs a gradient; too few frames are rejected like the pipeline does
+    assert lib.pesq_pipeline_kernels(8, 128000, 0, 1, None, 0, None) == _lib.ERR_ARGUMENT
+    assert lib.pesq_pipeline_kernels(1, 4000, 2, 0, None, 0, None) == _lib.ERR_ARGUMENT
+    # 4 bands more than a lane's worth is not a pipeline shape: the pipeline is 49 bands
+    names = _lib.pipeline_kernels(1, 16000, 1, backward=True)
+    assert names[0] == "chain_bwd_kernel<16, 1>"
+
+
+def test_lane_state_region_only_when_stored():
+    """The scan workspace holds 64 lane states per block only for grids that store them."""
+
+    def fwd_bytes(batch, length):
+        return _lib.size_query(_lib.library().pesq_pipeline_forward_workspace, batch, length, 2)
+
+    # 16 rows x 125 blocks x 6 sections x 2 doubles x (1 aggregate + 64 lane states)
+    assert _region_size(8, 128000, "aggr") == 16 * 125 * 6 * 2 * 65 * 8
+    # c5: 512 rows x 63 blocks, recomputed lane states: aggregates only
+    assert _region_size(256, 64000, "aggr") == 512 * 63 * 6 * 2 * 8
+    assert fwd_bytes(256, 64000) < 600 * 2**20
+
+
+def _region_size(batch, length, name):
+    off = ctypes.c_size_t(0)
+    size = ctypes.c_size_t(0)
+    _lib.check(_lib.library().pesq_pipeline_region(batch, length, 2, name.encode(),
+                                                    ctypes.byref(off), ctypes.byref(size)))
+    return size.value
+
+
+def test_triton_ops_import_paths_resolve_to_the_hip_operators():
+    """The reference's operator modules import unchanged (``torch_pesq.triton_ops.*``)."""
+
+    from torch_pesq import triton_ops
+    from torch_pesq.hip_ops import chain, elementwise, iir, resample, spectral
+    from torch_pesq.hip_ops.loss import PesqLossHip
+    from torch_pesq.triton_ops import _common as t_common
+    from torch_pesq.triton_ops import chain as t_chain
+    from torch_pesq.triton_ops import elementwise as t_elem
+    from torch_pesq.triton_ops import iir as t_iir
+    from torch_pesq.triton_ops import loss as t_loss
+    from torch_pesq.triton_ops import resample as t_resample
+    from torch_pesq.triton_ops import spectral as t_spectral
+
+    assert triton_ops.HAS_TRITON == torch.cuda.is_available()
+    assert t_iir.TritonIIR is iir.HipIIR
+    assert t_iir.CHUNK_CANDIDATES == (64, 128, 256, 512) and t_iir.METHODS == ("scan", "matmul")
+    assert t_resample.TritonResample is resample.HipResample
+    assert t_spectral.TritonStftBark is spectral.HipStftBark
+    assert t_spectral.bark_segments is spectral.bark_segments
+    assert t_chain.TritonPesqChain is chain.HipPesqChain
+    for name in ("peak_normalize", "edge_ramp", "align_scale", "pesq_epilogue"):
+        assert getattr(t_elem, name) is getattr(elementwise, name)
+    assert t_loss.PesqLossTriton is PesqLossHip
+    from torch_pesq import PesqLossTriton
+
+    assert PesqLossTriton is PesqLossHip
+    assert callable(t_common.check_input) and callable(t_common.require_triton)
+    # constructors take the reference's arguments and need no GPU
+    t_iir.TritonIIR([0.2, 0.3], [1.0, -0.5])
+    t_resample.TritonResample(44100, 16000)
+    with pytest.raises(RuntimeError, match="GPU"):
+        t_common.check_input(torch.zeros(3))
+
+
+def test_kernel_trace_normalises_library_names():
+    """The profiler's kernel names and the library's list compare in one spelling."""
+
+    from kernel_trace import library_kernels, normalise
+
+    assert normalise("void pesq::iir_prefix_kernel<6>(pesq::IirTable const*, double*, int, long)") \
+        == "iir_prefix_kernel<6>"
+    mangled = "_ZN4pesq20iir_aggregate_kernelILi5ELi1ENS_11PipeFwdModeELb1EEEvT1_PKNS_8IirTableEPdS6_li"
+    assert normalise(mangled) == "iir_aggregate_kernel<5,1,PipeFwdMode,true>"
+    assert library_kernels(8, 128000, 2, False)[0] == "iir_aggregate_kernel<5,1,PipeFwdMode,true>"
+    assert all(" " not in k for k in library_kernels(4, 960000, 2, True))

@@ -349,3 +349,200 @@ def test_resample_lengths_and_identity():
     out = O.resample(tone, 48000)
     want = torch.sin(2 * math.pi * 1000 * torch.arange(16000, dtype=torch.float64) / 16000)
     assert (out[0, 200:-200] - want[200:-200]).abs().max() < 2e-3
+
+
+# -- resampler: brute force over the continuous kernel ----------------------------
+
+
+def _brute_force_resample(x, orig_freq, new_freq, float32_rounding, lpw=6, rolloff=0.99):
+    """``y[m] = sum_n x[n] h((n / orig - m / new) base) base / orig``, one output at a time.
+
+    ``h(t) = sinc(pi t) cos(pi t / (2 lpw))^2`` on ``|t| <= lpw`` is torchaudio's
+    published Hann windowed sinc; ``base = min(orig, new) rolloff`` with the
+    rates reduced by their gcd; the input is zero outside ``[0, len(x))``.  No
+    filter bank, convolution or reshape: every output walks the input samples
+    its kernel covers.  ``float32_rounding`` applies the two roundings
+    torchaudio's tap table has (the output phase ``-j / new`` formed in
+    float32, the taps stored in float32); without it everything is float64.
+    """
+
+    g = math.gcd(orig_freq, new_freq)
+    orig, new = orig_freq // g, new_freq // g
+    base = min(orig, new) * rolloff
+    y = np.zeros(O.resample_length(len(x), orig_freq, new_freq))
+    for m in range(len(y)):
+        lo = max(math.floor((m / new - lpw / base) * orig) - 1, 0)
+        hi = min(math.ceil((m / new + lpw / base) * orig) + 1, len(x) - 1)
+        n = np.arange(lo, hi + 1)
+        if float32_rounding:
+            j, frame = m % new, m // new
+            t = (float(np.float32(-j / new)) + (n - frame * orig) / orig) * base
+        else:
+            t = (n * new - m * orig) / (orig * new) * base
+        t = np.clip(t, -lpw, lpw)
+        window = np.cos(t * math.pi / lpw / 2) ** 2
+        arg = t * math.pi
+        sinc = np.where(arg == 0, 1.0, np.sin(arg) / np.where(arg == 0, 1.0, arg))
+        taps = sinc * window * (base / orig)
+        if float32_rounding:
+            taps = taps.astype(np.float32).astype(np.float64)
+        y[m] = np.dot(x[n], taps)
+    return y
+
+
+@pytest.mark.parametrize(
+    "orig,new,n",
+    [(44100, 16000, 1500), (22050, 16000, 1000), (48000, 16000, 600), (13, 7, 300), (7, 13, 300)],
+)
+def test_resample_matches_brute_force_over_the_continuous_kernel(orig, new, n):
+    """Pins the phase convention (sign of ``-j / new``), the phase interleave of
+    the output, the ``(width, width + orig)`` padding and the tap support of
+    the oracle's polyphase form: with torchaudio's two float32 roundings the
+    per-output sum agrees to rounding; in plain float64 it agrees to the size
+    of those roundings."""
+
+    x = np.random.default_rng(orig + 3 * new).standard_normal(n)
+    got = O.resample(torch.from_numpy(x)[None], orig, new)[0].numpy()
+    scale = np.abs(got).max()
+    exact = _brute_force_resample(x, orig, new, float32_rounding=True)
+    assert got.shape == exact.shape
+    assert np.abs(got - exact).max() <= 1e-12 * scale
+    plain = _brute_force_resample(x, orig, new, float32_rounding=False)
+    assert np.abs(got - plain).max() <= 2e-5 * scale
+
+
+def _multitone_error(fs, resample):
+    """Largest deviation of resampled pass-band tones from the same tones sampled at 16 kHz."""
+
+    n = fs // 2
+    tones = [(300.0, 0.3, 0.1), (1000.0, 1.0, 1.3), (2200.0, 0.5, 2.0), (3400.0, 0.7, -0.7)]
+    t = np.arange(n) / fs
+    x = sum(a * np.sin(2 * math.pi * f * t + p) for f, a, p in tones)
+    y = resample(torch.from_numpy(x)[None], fs)[0].numpy()
+    m = np.arange(len(y)) / 16000
+    want = sum(a * np.sin(2 * math.pi * f * m + p) for f, a, p in tones)
+    return float(np.abs(y - want)[400:-400].max())
+
+
+@pytest.mark.parametrize("fs", [44100, 22050, 48000, 32000])
+def test_resample_multitone_passband(fs):
+    """Four tones of 0.3 - 3.4 kHz (amplitude sum 2.5) keep amplitude and phase to
+    1e-3 of full scale (the measured pass-band ripple is 1.1e-3 in absolute
+    units); a wrong phase sign or interleave moves samples by a fraction of an
+    input period and errs by 0.1 or more."""
+
+    assert _multitone_error(fs, O.resample) < 2.5e-3
+
+
+def test_resample_multitone_detects_a_wrong_interleave(monkeypatch):
+    """The multitone check fails on a planted mistake: the phases of the filter
+    bank in reverse order (the sign of the phase term flipped, modulo one
+    sample)."""
+
+    real = O.sinc_resample_kernel
+
+    def flipped(*args, **kwargs):
+        kernel, width = real(*args, **kwargs)
+        return kernel.flip(0).contiguous(), width
+
+    monkeypatch.setattr(O, "sinc_resample_kernel", flipped)
+    assert _multitone_error(44100, O.resample) > 0.05
+
+
+# -- chain: clamp known answers ---------------------------------------------------
+
+
+def _single_band(k, ref_level, deg_level, frames=40):
+    """Constant spectra with energy in band ``k`` only (float32 values, as the kernels get them).
+
+    All other bands are exactly zero, so they have no loudness and no
+    disturbance, every frame is the same (the overlapping 6th-power means of a
+    constant are that constant), and both weighted norms reduce to the single
+    term of band ``k``: ``symm = sqrt(W) w_k |d_k| / h`` and
+    ``asymm = w_k |d_k| asc_k / h`` with ``W`` the total band width.
+    """
+
+    ref = torch.zeros(1, frames, 49, dtype=torch.float64)
+    deg = torch.zeros(1, frames, 49, dtype=torch.float64)
+    ref[:, :, k] = ref_level
+    deg[:, :, k] = deg_level
+    return ref.float().double(), deg.float().double()
+
+
+A_LEVEL = 2e7  # one band above 1e7 and above 100 x its threshold: no frame is silent
+
+
+def test_chain_45_cap():
+    """deg = 1e7 ref in band 40: every frame's disturbances exceed 45, both distances are 45."""
+
+    ds, da = O.chain(*_single_band(40, A_LEVEL, 1e7 * A_LEVEL))
+    assert abs(float(ds) - 45.0) < 1e-12 and abs(float(da) - 45.0) < 1e-12
+
+
+@pytest.mark.parametrize("k", [10, 25, 40])
+def test_chain_band_ratio_floor_and_asymmetry_cut(k):
+    """deg = 1e-6 ref: the degraded band is below 100 x threshold (no band mean),
+    so the band ratio 1000 / (A + 1000) clamps at 0.01 and taer = 0.01 A; the
+    equalised degraded band is quieter than the reference, the asymmetry
+    factor is below 3 and is cut, and the asymmetric distance is the 1e-20
+    floor over h = ((0.01 A + 1e5) / 1e7)^0.04.  The symmetric one is not."""
+
+    ref, deg = _single_band(k, A_LEVEL, 1e-6 * A_LEVEL)
+    ds, da = O.chain(ref, deg)
+    h = ((0.01 * float(ref[0, 0, k]) + 1e5) / 1e7) ** 0.04
+    assert abs(float(da) * h / 1e-20 - 1.0) < 1e-12
+    assert 1.0 < float(ds) < 45.0
+
+
+@pytest.mark.parametrize("k", [10, 25])
+@pytest.mark.parametrize("louder", [1.5e6, 3e6])
+def test_chain_upper_clamps_and_asymmetry_factor(k, louder):
+    """deg = q ref with q >= 1.5e6: the band ratio clamps at 100 (equ_ref = 100 A)
+    and the frame ratio (100 A + 5e3) / (q A + 5e3) at 3e-4 (equ_deg = 3e-4 q A),
+    so asc = ((3e-4 q A + 50) / (100 A + 50))^1.2, 6.1 at q = 1.5e6 and 14.0,
+    capped at 12, at q = 3e6; with one band the distances' ratio is
+    asc / sqrt(W), whatever the loudness of the band."""
+
+    ref, deg = _single_band(k, A_LEVEL, louder * A_LEVEL)
+    ds, da = O.chain(ref, deg)
+    c = O.constants()
+    a, b = float(ref[0, 0, k]), float(deg[0, 0, k])
+    asc = min(((3e-4 * b + 50) / (100 * a + 50)) ** 1.2, 12.0)
+    assert (asc == 12.0) == (louder == 3e6)
+    assert float(ds) < 45.0 and float(da) < 45.0
+    assert abs(float(da / ds) / (asc / math.sqrt(float(c["total_width"]))) - 1.0) < 1e-12
+
+
+@pytest.mark.parametrize("k", [10, 25, 40])
+def test_chain_frame_ratio_cap(k):
+    """deg at th_k / 6 in band k: taer = 0.01 A, tad = 0 (below threshold), the frame
+    ratio (0.01 A + 5e3) / 5e3 = 41 clamps at 5, and 5 deg <= th_k has no
+    loudness, exactly like deg = 0: both give the same distances.  Without the
+    clamp (or with one above 6) the degraded band would be audible; at th_k / 3
+    (5 deg > th_k) it is, and the distances differ."""
+
+    th = float(O.constants()["threshs"][k])
+    quiet = O.chain(*_single_band(k, A_LEVEL, th / 6))
+    silent = O.chain(*_single_band(k, A_LEVEL, 0.0))
+    assert float(quiet[0]) == float(silent[0]) and float(quiet[1]) == float(silent[1])
+    audible = O.chain(*_single_band(k, A_LEVEL, th / 3))
+    assert float(audible[0]) != float(silent[0])
+
+
+@pytest.mark.parametrize("deg_scale", [1.0, 100.0])
+def test_chain_exact_threshold_values(deg_scale):
+    """``test_triton_chain.py:725-750``: ref = threshs exactly has no loudness (the
+    ``x > th`` branch is off) and every frame is silent; deg = threshs or 100
+    threshs (frame ratio clamped at 3e-4) has none either, so both distances
+    are the floor 1e-20 / h with h = ((0 + 1e5) / 1e7)^0.04 = 0.83175.  (The
+    float64 thresholds themselves: their float32 roundings lie above some of
+    them, which turns the branch on in those bands.)"""
+
+    th = O.constants()["threshs"].reshape(1, 1, -1)
+    ref = th.expand(2, 62, 49).contiguous()
+    deg = (th * deg_scale).expand(2, 62, 49).contiguous()
+    ds, da = O.chain(ref, deg)
+    h = (1e5 / 1e7) ** 0.04
+    assert abs(h - 0.83175) < 5e-5  # the reference quotes five digits
+    torch.testing.assert_close(ds, torch.full_like(ds, 1e-20 / h), rtol=1e-12, atol=0)
+    torch.testing.assert_close(da, torch.full_like(da, 1e-20 / h), rtol=1e-12, atol=0)

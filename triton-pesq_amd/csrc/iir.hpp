@@ -72,16 +72,41 @@ struct IirTable {
     double lane_pw[kMaxSections][kWave][4];  // A_k^(kChunk lane), lane start powers
 };
 
+// Small grids (those that keep lane states) of rows of up to
+// kFusedPrefixBlocks blocks skip the prefix pass: every output wavefront
+// derives its block's start state from the block aggregates itself
+// (block_start_load, block_start_reduce).  Large grids keep the separate
+// prefix kernel, whose work is not repeated per block.
+#ifndef PESQ_FUSED_PREFIX_BLOCKS
+#define PESQ_FUSED_PREFIX_BLOCKS 128
+#endif
+constexpr int kFusedPrefixBlocks = PESQ_FUSED_PREFIX_BLOCKS;
+static_assert(kFusedPrefixBlocks <= 2 * kWave, "two blocks per lane");
+
+// Launch plan of a scan over `rows` rows of nblk blocks (one wavefront each):
+// whether the aggregate pass stores the lane states, and whether the output
+// pass derives the block start states itself (no prefix launch).  The
+// workspace sizing and the launches both read it.
+struct ScanPlan {
+    bool lane_states;
+    bool fused_prefix;
+};
+__host__ __device__ __forceinline__ ScanPlan scan_plan(int64_t rows, int64_t nblk) {
+    const bool lanes = rows * nblk <= kLaneStateWaves;
+    return {lanes, lanes && nblk <= kFusedPrefixBlocks};
+}
+
 // Scan workspace of `rows` rows of nblk blocks and `ns` sections: the block
-// aggregates [row][section][block][2], then the lane states
-// [row][block][section][lane][2].
+// aggregates [row][section][block][2], then, when the plan stores them, the
+// lane states [row][block][section][lane][2].
 __host__ __device__ __forceinline__ int64_t scan_aggr_doubles(int64_t rows, int64_t nblk,
                                                               int ns = kMaxSections) {
     return rows * nblk * ns * 2;
 }
 __host__ __device__ __forceinline__ int64_t scan_workspace_doubles(int64_t rows, int64_t nblk,
                                                                    int ns = kMaxSections) {
-    return scan_aggr_doubles(rows, nblk, ns) * (1 + kWave);
+    const int64_t lanes = scan_plan(rows, nblk).lane_states ? kWave : 0;
+    return scan_aggr_doubles(rows, nblk, ns) * (1 + lanes);
 }
 
 // --------------------------------------------------------------------------
@@ -230,17 +255,6 @@ __device__ __forceinline__ void scan_wave_dpp(const Powers &t, Bank<NS> &z, int 
     for (int k = 0; k < NS; ++k) pw[k] = t.lane_pw[S0 + k][lane >= 32 ? lane - 31 : 0];
     dpp_level<0x143, 0xC, S0, NS>(pw, z);  // row_bcast:31
 }
-
-// Small grids (those that keep lane states) of rows of up to
-// kFusedPrefixBlocks blocks skip the prefix pass: every output wavefront
-// derives its block's start state from the block aggregates itself
-// (block_start_load, block_start_reduce).  Large grids keep the separate
-// prefix kernel, whose work is not repeated per block.
-#ifndef PESQ_FUSED_PREFIX_BLOCKS
-#define PESQ_FUSED_PREFIX_BLOCKS 128
-#endif
-constexpr int kFusedPrefixBlocks = PESQ_FUSED_PREFIX_BLOCKS;
-static_assert(kFusedPrefixBlocks <= 2 * kWave, "two blocks per lane");
 
 // Start state of block `blk` of a row from the zero start end states e_j of
 // the blocks before it (row_aggr, laid out [section][block][2]):
@@ -723,8 +737,9 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
     double *lanes = ws + scan_aggr_doubles(rows, nblk, NS);
     const unsigned grid = static_cast<unsigned>(rows * nblk);
     if (grid == 0) return PESQ_OK;
-    const bool lane_states = grid <= kLaneStateWaves;
-    const bool fused = lane_states && nblk <= kFusedPrefixBlocks;
+    const ScanPlan plan = scan_plan(rows, nblk);
+    const bool lane_states = plan.lane_states;
+    const bool fused = plan.fused_prefix;
     if (aggregate) {
         if (lane_states) {
             hipLaunchKernelGGL((iir_aggregate_kernel<NA, NB, Mode, true>), dim3(grid), dim3(kWave),

@@ -30,6 +30,8 @@
 // is zero for the same reason: the loss is invariant under s -> c s.)
 #include <cmath>
 
+#include <algorithm>
+#include <string>
 #include <type_traits>
 
 #include "pipeline_layout.hpp"
@@ -37,8 +39,6 @@
 
 namespace pesq {
 
-constexpr int kPowerSections = 5;  // order 10 band pass, parallel form
-constexpr int kPreSections = 1;    // pre-emphasis biquad
 
 // ---------------------------------------------------------------------------
 // IIR modes
@@ -1305,13 +1305,37 @@ using StftBwdReal = float;
 // BASELINE c2 and c5 respectively).  The results are the same either way.
 constexpr unsigned kChainWideGrid = 512;
 
-// Up to 64 bands a lane holds one band; 65 .. 128 bands take two per lane
-// (band lane + 64), with 4 wavefronts per workgroup for the larger register
-// footprint.
+// The kernel variants the pipeline launches for one shape.  Every launch
+// below and pesq_pipeline_kernels read this one plan, so the variants a test
+// asks about are the ones that run.
+struct PipePlan {
+    ScanPlan fwd_scan, bwd_scan;
+    bool stft_lean;      // stft_fwd_kernel<.., true>: grids above kChainWideGrid
+    int chain_fwd_waves, chain_bwd_waves;
+    int chain_bpl;       // bands per lane: 1 up to 64 bands, 2 up to 128
+};
+
+static PipePlan pipe_plan(const PipeLayout &L) {
+    PipePlan P{};
+    P.fwd_scan = scan_plan(L.rows, L.nblk);
+    P.bwd_scan = scan_plan(L.nrg, L.nblk);
+    const int64_t grid = L.batch * L.ntile;
+    const bool wide = grid > kChainWideGrid;
+    P.stft_lean = wide;
+    // Up to 64 bands a lane holds one band; 65 .. 128 bands take two per lane
+    // (band lane + 64), with 4 wavefronts per workgroup for the larger
+    // register footprint.
+    P.chain_bpl = L.nb > kWave ? 2 : 1;
+    P.chain_fwd_waves = P.chain_bpl == 2 || wide ? 4 : 8;
+    P.chain_bwd_waves = P.chain_bpl == 2 || wide ? 4 : 16;
+    return P;
+}
+
 static void launch_chain_fwd(const PipeArgs &a, unsigned grid, hipStream_t stream) {
-    if (a.L.nb > kWave) {
+    const PipePlan P = pipe_plan(a.L);
+    if (P.chain_bpl == 2) {
         hipLaunchKernelGGL((chain_fwd_kernel<4, 2>), dim3(grid), dim3(kWave * 4), 0, stream, a);
-    } else if (grid <= kChainWideGrid) {
+    } else if (P.chain_fwd_waves == 8) {
         hipLaunchKernelGGL((chain_fwd_kernel<8, 1>), dim3(grid), dim3(kWave * 8), 0, stream, a);
     } else {
         hipLaunchKernelGGL((chain_fwd_kernel<4, 1>), dim3(grid), dim3(kWave * 4), 0, stream, a);
@@ -1319,13 +1343,23 @@ static void launch_chain_fwd(const PipeArgs &a, unsigned grid, hipStream_t strea
 }
 
 static void launch_chain_bwd(const PipeArgs &a, unsigned grid, hipStream_t stream) {
-    if (a.L.nb > kWave) {
+    const PipePlan P = pipe_plan(a.L);
+    if (P.chain_bpl == 2) {
         hipLaunchKernelGGL((chain_bwd_kernel<4, 2>), dim3(grid), dim3(kWave * 4), 0, stream, a);
-    } else if (grid <= kChainWideGrid) {
+    } else if (P.chain_bwd_waves == 16) {
         hipLaunchKernelGGL((chain_bwd_kernel<16, 1>), dim3(grid), dim3(kWave * 16), 0, stream, a);
     } else {
         hipLaunchKernelGGL((chain_bwd_kernel<4, 1>), dim3(grid), dim3(kWave * 4), 0, stream, a);
     }
+}
+
+// Names of the kernels of one scan pass, in launch order.
+static void scan_kernel_names(const ScanPlan &S, const char *mode, std::string &out) {
+    const char *lanes = S.lane_states ? "true" : "false";
+    out += std::string("iir_aggregate_kernel<5, 1, ") + mode + ", " + lanes + ">;";
+    if (!S.fused_prefix) out += "iir_prefix_kernel<6>;";
+    out += std::string("iir_output_kernel<5, 1, ") + mode + ", " + lanes + ", " +
+           (S.fused_prefix ? "true" : "false") + ">;";
 }
 
 static int check_sizes(int64_t batch, int64_t len, const PipeLayout &L) {
@@ -1367,6 +1401,40 @@ extern "C" int pesq_pipeline_region(int64_t batch, int64_t len, int grad_mask, c
     L.build(batch, len, grad_mask);
     PESQ_CHECK_ARG(name != nullptr && L.region(name, offset, bytes), "unknown region %s",
                    name ? name : "(null)");
+    return PESQ_OK;
+}
+
+extern "C" int pesq_pipeline_kernels(int64_t batch, int64_t len, int grad_mask, int backward,
+                                     char *names, size_t capacity, size_t *needed) {
+    PipeLayout L;
+    L.build(batch, len, grad_mask);
+    if (int st = check_sizes(batch, len, L)) return st;
+    PESQ_CHECK_ARG((grad_mask & ~3) == 0, "invalid grad_mask %d", grad_mask);
+    PESQ_CHECK_ARG(!backward || grad_mask != 0, "backward needs a non-empty grad_mask");
+    const PipePlan P = pipe_plan(L);
+    const char *real = std::is_same<StftReal, double>::value ? "double" : "float";
+    const char *bwd_real = std::is_same<StftBwdReal, double>::value ? "double" : "float";
+    std::string out;
+    if (!backward) {
+        scan_kernel_names(P.fwd_scan, "PipeFwdMode", out);
+        out += std::string("stft_fwd_kernel<") + real + ", " + (P.stft_lean ? "true" : "false") +
+               ", " + std::to_string(kStftWaves) + ">;";
+        out += "chain_fwd_kernel<" + std::to_string(P.chain_fwd_waves) + ", " +
+               std::to_string(P.chain_bpl) + ">;";
+        out += "chain_final_kernel;";
+    } else {
+        out += "chain_bwd_kernel<" + std::to_string(P.chain_bwd_waves) + ", " +
+               std::to_string(P.chain_bpl) + ">;";
+        out += std::string("stft_bwd_kernel<") + bwd_real + ">;";
+        scan_kernel_names(P.bwd_scan, "PipeBwdMode", out);
+    }
+    out.pop_back();  // the last ';'
+    if (needed != nullptr) *needed = out.size() + 1;
+    if (names != nullptr && capacity > 0) {
+        const size_t n = std::min(out.size(), capacity - 1);
+        std::memcpy(names, out.data(), n);
+        names[n] = '\0';
+    }
     return PESQ_OK;
 }
 
@@ -1416,7 +1484,7 @@ extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, 
     }
     if (stages & 4u) {
         const unsigned grid = static_cast<unsigned>(batch * L.ntile);
-        if (grid <= kChainWideGrid) {
+        if (!pipe_plan(L).stft_lean) {
             hipLaunchKernelGGL((stft_fwd_kernel<StftReal, false>), dim3(grid),
                                dim3(kWave * kStftWaves), 0, stream, a);
         } else {

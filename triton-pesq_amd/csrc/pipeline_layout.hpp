@@ -9,6 +9,9 @@
 
 namespace pesq {
 
+constexpr int kPowerSections = 5;  // order 10 band pass, parallel form
+constexpr int kPreSections = 1;    // pre-emphasis biquad
+constexpr int kPipeSections = kPowerSections + kPreSections;  // scanned in one pass
 constexpr int kTile = 16;          // frames per workgroup of the STFT / chain kernels
 constexpr int kBwdFrames = 8;      // frames per workgroup of the STFT backward
 constexpr int kBwdHops = kBwdFrames - 1;  // output hop blocks per such workgroup
@@ -64,7 +67,7 @@ struct PipeLayout {
             field = off;
             off = align(off + bytes);
         };
-        take(aggr, size_t(scan_workspace_doubles(rows, nblk)) * sizeof(double));
+        take(aggr, size_t(scan_workspace_doubles(rows, nblk, kPipeSections)) * sizeof(double));
         take(energy, size_t(rows) * nblk * sizeof(double));
         take(p, size_t(rows) * len * sizeof(float));
         take(f, size_t(nrg) * len * sizeof(float));
@@ -86,7 +89,7 @@ struct PipeLayout {
         take(grpart, size_t(batch) * ntile * nb * sizeof(double));
         take(gp, size_t(nrg) * len * sizeof(float));
         take(spart, size_t(nrg) * nhoptile * sizeof(double));
-        take(aggr_b, size_t(scan_workspace_doubles(nrg, nblk)) * sizeof(double));
+        take(aggr_b, size_t(scan_workspace_doubles(nrg, nblk, kPipeSections)) * sizeof(double));
         bwd_bytes = off;
     }
 

@@ -20,6 +20,7 @@ __all__ = [
     "torch_ext",
     "check",
     "stream_handle",
+    "pipeline_kernels",
     "MAX_SECTIONS",
     "GRAD_REF",
     "GRAD_DEG",
@@ -31,6 +32,7 @@ NBARKS = 49
 NFFT = 512
 GRAD_REF = 1
 GRAD_DEG = 2
+ERR_ARGUMENT = 1  # PESQ_ERR_ARGUMENT
 
 LIB_PATH = Path(os.environ.get("PESQ_HIP_LIB", Path(__file__).with_name("_lib") / "libpesq_hip.so"))
 
@@ -116,6 +118,8 @@ SIGNATURES = {
     "pesq_pipeline_forward_workspace": (_INT, [_I64, _I64, _INT, _SIZE_P]),
     "pesq_pipeline_backward_workspace": (_INT, [_I64, _I64, _INT, _SIZE_P]),
     "pesq_pipeline_region": (_INT, [_I64, _I64, _INT, ctypes.c_char_p, _SIZE_P, _SIZE_P]),
+    "pesq_pipeline_kernels": (_INT, [_I64, _I64, _INT, _INT, ctypes.c_char_p, ctypes.c_size_t,
+                                     _SIZE_P]),
     "pesq_pipeline_forward": (
         _INT,
         [_P, _P, _I64, _I64, _P, ctypes.c_double, _INT, _P, _P, _P, _P, _P, _P],
@@ -248,6 +252,19 @@ def ptr(tensor) -> ctypes.c_void_p:
     """Device pointer of a tensor, or NULL for ``None``."""
 
     return ctypes.c_void_p(0 if tensor is None else tensor.data_ptr())
+
+
+def pipeline_kernels(batch: int, length: int, grad_mask: int, backward: bool) -> list:
+    """Kernels one pipeline pass launches for a shape, in launch order (host only)."""
+
+    lib = library()
+    needed = ctypes.c_size_t(0)
+    check(lib.pesq_pipeline_kernels(batch, length, grad_mask, int(backward), None, 0,
+                                    ctypes.byref(needed)), "pesq_pipeline_kernels")
+    buf = ctypes.create_string_buffer(int(needed.value))
+    check(lib.pesq_pipeline_kernels(batch, length, grad_mask, int(backward), buf, len(buf), None),
+          "pesq_pipeline_kernels")
+    return buf.value.decode().split(";")
 
 
 def size_query(fn, *args) -> int:

@@ -8,13 +8,7 @@ import torch
 
 from .. import _lib
 
-__all__ = ["check_input", "require_hip", "next_power_of_two"]
-
-
-def next_power_of_two(value: int) -> int:
-    """Smallest power of two which is greater or equal to ``value``."""
-
-    return 1 << max(0, int(value) - 1).bit_length()
+__all__ = ["check_input", "require_hip"]
 
 
 def require_hip() -> None:
