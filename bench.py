@@ -217,17 +217,38 @@ def model_bytes(batch: int, samples: int):
     }, 27 * s + 5 * kb
 
 
-#: fused stage -> (pass, stage bits, kernel names)
+#: fused stage -> (pass, stage bits of the *_stages entry points)
 STAGES = {
-    "fwd_scans": ("fwd", 0x3, ["iir_aggregate_kernel<5,1,PipeFwdMode,true>",
-                               "iir_output_kernel<5,1,PipeFwdMode,true,true>"]),
-    "fwd_stft": ("fwd", 0x4, ["stft_fwd_kernel<double,false,8>"]),
-    "fwd_chain": ("fwd", 0x18, ["chain_fwd_kernel<8,1>", "chain_final_kernel"]),
-    "bwd_chain": ("bwd", 0x1, ["chain_bwd_kernel<16,1>"]),
-    "bwd_stft": ("bwd", 0x2, ["stft_bwd_kernel<float>"]),
-    "bwd_scans": ("bwd", 0xC, ["iir_aggregate_kernel<5,1,PipeBwdMode,true>",
-                               "iir_output_kernel<5,1,PipeBwdMode,true,true>"]),
+    "fwd_scans": ("fwd", 0x3),
+    "fwd_stft": ("fwd", 0x4),
+    "fwd_chain": ("fwd", 0x18),
+    "bwd_chain": ("bwd", 0x1),
+    "bwd_stft": ("bwd", 0x2),
+    "bwd_scans": ("bwd", 0xC),
 }
+
+
+def stage_kernels(batch: int, samples: int, grad_mask: int = 2):
+    """Kernels of each fused stage at a shape, from the library's own plan.
+
+    The variants (lane states stored or recomputed, block prefix fused or
+    launched, frames per wavefront) depend on the grid size; the library
+    names the ones it launches (``pesq_pipeline_kernels``).
+    """
+
+    from torch_pesq import _lib
+
+    fwd = _lib.pipeline_kernels(batch, samples, grad_mask, False)
+    bwd = _lib.pipeline_kernels(batch, samples, grad_mask, True)
+    scan_end = next(i for i, k in enumerate(fwd) if k.startswith("iir_output")) + 1
+    return {
+        "fwd_scans": fwd[:scan_end],
+        "fwd_stft": [k for k in fwd if k.startswith("stft_")],
+        "fwd_chain": [k for k in fwd if k.startswith("chain_")],
+        "bwd_chain": [k for k in bwd if k.startswith("chain_")],
+        "bwd_stft": [k for k in bwd if k.startswith("stft_")],
+        "bwd_scans": [k for k in bwd if k.startswith("iir_")],
+    }
 
 
 def capture_step(model, ref, deg):
@@ -280,7 +301,7 @@ def _stage_times(model, ref, deg, repeats: int = 50):
     run("fwd", 0x1F)
     run("bwd", 0xF)
     times = {}
-    for name, (pass_, bits, _) in STAGES.items():
+    for name, (pass_, bits) in STAGES.items():
         for _ in range(3):
             run(pass_, bits)
         start = torch.cuda.Event(enable_timing=True)
@@ -338,6 +359,23 @@ def cpu_baseline(ref_np, deg_np, gpu_outputs, budget_s: float = 12.0):
         "cpu_port_d_symm": rel(port_ds, ds),
         "cpu_port_d_asymm": rel(port_da, da),
     }
+    # BASELINE c1: PesqLoss(0.5) forward + mos on the CPU, one 1 s item
+    c1_ref, c1_deg, _ = synthetic_config(1)
+    r1, d1 = torch.from_numpy(c1_ref), torch.from_numpy(c1_deg)
+
+    def c1_step():
+        with torch.no_grad():
+            pesq_port.loss(r1, d1, 0.5)
+            pesq_port.mos(r1, d1)
+
+    c1_step()
+    c1_samples, start = [], time.perf_counter()
+    while len(c1_samples) < 5 or (time.perf_counter() - start < 3.0 and len(c1_samples) < 200):
+        t0 = time.perf_counter()
+        c1_step()
+        c1_samples.append(time.perf_counter() - t0)
+    c1_per_step = statistics.median(c1_samples)
+
     cpu_model = platform.processor() or platform.machine()
     try:
         for line in open("/proc/cpuinfo"):
@@ -357,29 +395,65 @@ def cpu_baseline(ref_np, deg_np, gpu_outputs, budget_s: float = 12.0):
             f"restatement of PesqLoss with a C direct-form-I lfilter; host {cpu_model}, "
             f"os.cpu_count()={os.cpu_count()}"
         ),
+        "c1_fwd_mos": {
+            "value": round(1.0 / c1_per_step, 2),
+            "unit": "signals/s",
+            "ms_per_item": round(c1_per_step * 1e3, 3),
+            "sample": f"BASELINE c1 (1 x 16000 @16 kHz) PesqLoss(0.5) forward + mos, no gradient, "
+                      f"median of {len(c1_samples)} calls",
+        },
     }
     return baseline, errors
 
 
-def _profiled_traffic(stage: str):
-    """HBM bytes per launch of a stage from the committed rocprofv3 PMC summary.
+def profiled_traffic(config: int):
+    """HBM bytes per launch of every fused stage from a committed rocprofv3 summary.
 
-    ``profiles/pipeline_c2_hbm_traffic.txt`` holds FETCH_SIZE and WRITE_SIZE per
-    dispatch, calibrated against a plain device copy of known size; ``None``
-    when it is missing.
+    ``profiles/pipeline_c<config>_hbm_traffic.txt`` holds FETCH_SIZE and
+    WRITE_SIZE per dispatch (two ``--pmc`` runs of this script), calibrated
+    against a plain device copy of known size; an empty dict when it is
+    missing.  The counters count the L2's requests to the memory fabric, which
+    the 256 MB MALL may serve: an upper bound of the HBM bytes.
     """
 
-    path = ROOT / "profiles" / "pipeline_c2_hbm_traffic.txt"
+    path = ROOT / "profiles" / f"pipeline_c{config}_hbm_traffic.txt"
     try:
         for line in path.read_text().splitlines():
             if line.startswith("# traffic_json:"):
-                return json.loads(line.split(":", 1)[1])["stage_bytes"].get(stage)
+                return json.loads(line.split(":", 1)[1])["stage_bytes"]
     except (OSError, ValueError, KeyError):
-        return None
-    return None
+        return {}
+    return {}
 
 
-def diagnose(config: int, steps: int, warmup: int) -> dict:
+def stage_report(stage_s, per_stage, traffic, kernels):
+    """Per stage device time, model-bytes roofline and counter-bytes roofline.
+
+    ``frac`` is the canonical model's bytes (every stage of the reference's
+    decomposition reads its inputs and writes its outputs once) over the
+    event time; a fused kernel that never writes the intermediate tensors of
+    the stages it covers can exceed 1 on it.  ``traffic_frac`` is the bytes
+    the kernels moved (counters) over the same time: the physical fraction.
+    """
+
+    out = {}
+    for name in STAGES:
+        t = stage_s[name]
+        entry = {
+            "us": round(t * 1e6, 2),
+            "model_bytes": per_stage[name],
+            "achieved_GBps": round(per_stage[name] / t / 1e9, 1),
+            "frac": round(per_stage[name] / t / HBM_PEAK, 4),
+            "traffic_bytes": traffic.get(name),
+            "traffic_frac": (round(traffic[name] / t / HBM_PEAK, 4)
+                             if traffic.get(name) is not None else None),
+            "kernels": kernels[name],
+        }
+        out[name] = entry
+    return out
+
+
+def diagnose(config: int, steps: int, warmup: int, copy_calibration: bool = False) -> dict:
     """Autograd step, resampler kernels and fused stages of another BASELINE config.
 
     The batch is the config's full shape; its items repeat the first 16
@@ -397,6 +471,8 @@ def diagnose(config: int, steps: int, warmup: int) -> dict:
     ref_np = np.tile(ref_np, (reps, 1))[:count]
     deg_np = np.tile(deg_np, (reps, 1))[:count]
     device = torch.device("cuda:0")
+    if copy_calibration:
+        _copy_calibration(device)
     model = PesqLossTriton(1.0, sample_rate=fs).to(device)
     ref = torch.from_numpy(ref_np).to(device)
     deg = torch.from_numpy(deg_np).to(device).requires_grad_(True)
@@ -451,13 +527,23 @@ def diagnose(config: int, steps: int, warmup: int) -> dict:
         }
     stage_s = _stage_times(model, ref16.contiguous(), deg16.contiguous(), repeats=steps)
     per_stage, total = model_bytes(ref16.shape[0], ref16.shape[1])
-    out["stages"] = {
-        name: {"us": round(stage_s[name] * 1e6, 2),
-               "frac": round(per_stage[name] / stage_s[name] / HBM_PEAK, 4)}
-        for name in STAGES
-    }
+    out["stages"] = stage_report(stage_s, per_stage, profiled_traffic(config),
+                                 stage_kernels(ref16.shape[0], ref16.shape[1]))
     out["model_bytes_16k"] = total
     return out
+
+
+def _copy_calibration(device):
+    """A plain 64 MiB device copy, five launches: the known-size reference for
+    scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters."""
+
+    import torch
+
+    src = torch.ones(16 * 1024 * 1024, device=device)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def main(argv=None):
@@ -492,18 +578,14 @@ def main(argv=None):
     from torch_pesq import PesqLossTriton
 
     if args.config != 2:
-        print(json.dumps(diagnose(args.config, args.steps, args.warmup)))
+        print(json.dumps(diagnose(args.config, args.steps, args.warmup, args.copy_calibration)))
         return 0
 
     ref_np, deg_np, fs = synthetic_config(2)
     batch, samples = ref_np.shape
     device = torch.device("cuda:0")
     if args.copy_calibration:
-        src = torch.ones(16 * 1024 * 1024, device=device)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+        _copy_calibration(device)
     model = PesqLossTriton(1.0, sample_rate=fs).to(device)
     ref = torch.from_numpy(ref_np).to(device)
     deg = torch.from_numpy(deg_np).to(device).requires_grad_(True)
@@ -572,16 +654,9 @@ def main(argv=None):
 
     stage_s = _stage_times(model, ref, deg.detach())
     per_stage, total_bytes = model_bytes(batch, samples)
-    stages = {
-        name: {
-            "us": round(stage_s[name] * 1e6, 2),
-            "model_bytes": per_stage[name],
-            "achieved_GBps": round(per_stage[name] / stage_s[name] / 1e9, 1),
-            "frac": round(per_stage[name] / stage_s[name] / HBM_PEAK, 4),
-            "kernels": STAGES[name][2],
-        }
-        for name in STAGES
-    }
+    kernels = stage_kernels(batch, samples)
+    traffic = profiled_traffic(2)
+    stages = stage_report(stage_s, per_stage, traffic, kernels)
     dominant = max(stage_s, key=stage_s.get)
     achieved = per_stage[dominant] / stage_s[dominant]
     roofline = {
@@ -590,8 +665,9 @@ def main(argv=None):
         "peak": HBM_PEAK / 1e9,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK, 4),
-        "traffic": _profiled_traffic(dominant),
-        "kernel": " + ".join(STAGES[dominant][2]),
+        "traffic": traffic.get(dominant),
+        "traffic_frac": stages[dominant]["traffic_frac"],
+        "kernel": " + ".join(kernels[dominant]),
         "stage": dominant,
         "model_bytes_per_launch": per_stage[dominant],
         "avg_launch_us": round(stage_s[dominant] * 1e6, 2),

@@ -43,14 +43,17 @@ def _run_step(config):
     ref = torch.from_numpy(ref_np).cuda()
     deg = torch.from_numpy(deg_np).cuda().requires_grad_(True)
     weights = torch.linspace(0.5, 1.5, batch, dtype=torch.float64)
+    upstream = weights.float().cuda()
 
     def step():
         out = model._run(ref, deg)
-        (g_deg,) = torch.autograd.grad(out[3], deg, grad_outputs=weights.float().cuda())
-        return [o.detach().double().cpu() for o in out], g_deg.double().cpu()
+        (g_deg,) = torch.autograd.grad(out[3], deg, grad_outputs=upstream)
+        return out, g_deg
 
     step()  # first call: module buffers, allocator
     (outputs, g_deg), kernels = launched_kernels(step)
+    outputs = [o.detach().double().cpu() for o in outputs]
+    g_deg = g_deg.double().cpu()
     print(f"\nconfig {config}: {batch} x {ref_np.shape[1]} @ {fs} Hz, kernels {sorted(kernels)}",
           flush=True)
     return ref_np, deg_np, fs, weights, outputs, g_deg, kernels
