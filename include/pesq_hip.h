@@ -193,6 +193,26 @@ int pesq_pipeline_region(int64_t batch, int64_t len, int grad_mask, const char *
 int pesq_pipeline_kernels(int64_t batch, int64_t len, int grad_mask, int backward, char *names,
                           size_t capacity, size_t *needed);
 
+/* Size of the static device array that serves as the workspace of
+ * pesq_pipeline_forward_noalloc (32 MiB, held by each GPU the library runs on
+ * until the process ends). */
+#define PESQ_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/* pesq_pipeline_forward with grad_mask 0 (distances, MOS and loss, no
+ * backward) that allocates nothing: its workspace is the library's static
+ * device array of PESQ_NOALLOC_SCRATCH_BYTES on the stream's device, so the
+ * caller passes only inputs and outputs.  Shapes whose forward workspace
+ * (pesq_pipeline_forward_workspace with grad_mask 0) exceeds that size are
+ * rejected with PESQ_ERR_ARGUMENT (about 1.5 M samples of batch x len:
+ * 8 x 8 s at 16 kHz needs 21.7 MiB and fits, 16 x 8 s does not).  Calls that overlap on one GPU share the array and
+ * race; calls ordered on one stream do not.  Results are bitwise those of
+ * pesq_pipeline_forward.  No counterpart in the reference: this is for
+ * callers that cannot allocate (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). */
+int pesq_pipeline_forward_noalloc(const float *ref, const float *deg, int64_t batch, int64_t len,
+                                  const void *model_table, double factor, float *d_symm,
+                                  float *d_asymm, float *mos, float *loss, hipStream_t stream);
+
 /* ----------------------------------------------------------------------- */
 /* IIR filter (TritonIIR, torch_pesq/triton_ops/iir.py:1266-1482)           */
 /* ----------------------------------------------------------------------- */

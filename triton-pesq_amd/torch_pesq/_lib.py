@@ -33,6 +33,7 @@ NFFT = 512
 GRAD_REF = 1
 GRAD_DEG = 2
 ERR_ARGUMENT = 1  # PESQ_ERR_ARGUMENT
+NOALLOC_SCRATCH_BYTES = 32 << 20  # PESQ_NOALLOC_SCRATCH_BYTES
 
 LIB_PATH = Path(os.environ.get("PESQ_HIP_LIB", Path(__file__).with_name("_lib") / "libpesq_hip.so"))
 
@@ -118,6 +119,9 @@ SIGNATURES = {
     "pesq_pipeline_forward_workspace": (_INT, [_I64, _I64, _INT, _SIZE_P]),
     "pesq_pipeline_backward_workspace": (_INT, [_I64, _I64, _INT, _SIZE_P]),
     "pesq_pipeline_region": (_INT, [_I64, _I64, _INT, ctypes.c_char_p, _SIZE_P, _SIZE_P]),
+    "pesq_pipeline_forward_noalloc": (
+        _INT, [_P, _P, _I64, _I64, _P, ctypes.c_double, _P, _P, _P, _P, _P],
+    ),
     "pesq_pipeline_kernels": (_INT, [_I64, _I64, _INT, _INT, ctypes.c_char_p, ctypes.c_size_t,
                                      _SIZE_P]),
     "pesq_pipeline_forward": (
