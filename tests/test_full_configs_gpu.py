@@ -105,8 +105,10 @@ def test_config4_full_batch_forward_and_backward():
     _assert_pipeline_variants(kernels, batch, length)
     for name in ("iir_prefix_kernel<6>", "iir_output_kernel<5,1,PipeBwdMode,true,false>",
                  "iir_output_kernel<5,1,PipeFwdMode,true,false>", "chain_bwd_kernel<4,1>",
-                 "chain_fwd_kernel<4,1>", "stft_fwd_kernel<double,true,8>"):
+                 "chain_fwd_kernel<4,1>"):
         assert name in kernels, name
+    # the STFT variant for large grids (its arithmetic type is the library's choice)
+    assert any(k.startswith("stft_fwd_kernel<") and k.endswith(",true,8>") for k in kernels)
     saturated = _compare_with_oracle(ref_np, deg_np, fs, weights, outputs, g_deg, range(batch))
     # 0 dB pink noise then clipping: the asymmetric distance sits at its clamp,
     # the symmetric one does not, so the comparison above still measures the chain

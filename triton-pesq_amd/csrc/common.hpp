@@ -67,6 +67,32 @@ __device__ __forceinline__ double row_shr(double v) {
     return __hiloint2double(hi, lo);
 }
 
+// 64-bit DPP move with control kCtrl into the rows of kRowMask (0 elsewhere
+// and where the source lane does not exist)
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ double dpp_move64(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), kCtrl, kRowMask, 0xF, true);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), kCtrl, kRowMask, 0xF, true);
+    return __hiloint2double(hi, lo);
+}
+
+// Inclusive prefix sum over the 64 lanes: Kogge-Stone within each row of 16
+// lanes (row shifts 1, 2, 4, 8), then the last lane of rows 0 and 2 is added
+// to rows 1 and 3 (row_bcast:15) and lane 31 to rows 2 and 3 (row_bcast:31).
+// A fixed association order: bitwise deterministic.  All lanes active.
+__device__ __forceinline__ double wave_inclusive_scan(double v) {
+    v += row_shr<1>(v);
+    v += row_shr<2>(v);
+    v += row_shr<4>(v);
+    v += row_shr<8>(v);
+    v += dpp_move64<0x142, 0xA>(v);
+    v += dpp_move64<0x143, 0xC>(v);
+    return v;
+}
+
+// v of the previous lane (0 in lane 0): DPP wave_shr:1
+__device__ __forceinline__ double wave_shift_up(double v) { return dpp_move64<0x138, 0xF>(v); }
+
 __device__ __forceinline__ double read_lane(double v, int lane) {
     return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), lane),
                             __builtin_amdgcn_readlane(__double2loint(v), lane));

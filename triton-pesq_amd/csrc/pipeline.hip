@@ -211,13 +211,42 @@ __device__ __forceinline__ void strided_sums(const double *const (&p)[K], const 
     }
 }
 
+// Logarithms for the chain, to about 1e-13 relative: a float32 estimate y0
+// (hardware log) refined by one float64 Newton step on the exponential,
+// y1 = y0 - f(y0) / f'(y0), whose error is about half the square of the
+// estimate's (1e-7 relative).  The step costs one float64 exp or expm1 (24
+// float64 operations), a third of the library's float64 log (113); the
+// correction term needs only float32 relative accuracy, so its division is a
+// float32 reciprocal.
+
+// log(1 + u) for u > 0 (u < 3e38).  The estimate is Kahan's
+// log1p(u) = log(w) u / (w - 1), w = 1 + u in float32 (u itself when w
+// rounds to 1), accurate to a few float32 units for every u; the step is
+// y <- y - (expm1(y) - u) / (1 + expm1(y)).
+__device__ __forceinline__ double log1p_refined(double u) {
+    const float uf = static_cast<float>(u);
+    const float w = 1.0f + uf;
+    const float y0 = w == 1.0f ? uf : __logf(w) * (uf / (w - 1.0f));
+    const double y = static_cast<double>(y0);
+    const double m = expm1(y);
+    return y - (m - u) * static_cast<double>(1.0f / static_cast<float>(1.0 + m));
+}
+
+// log(num / den) for num, den > 0 with a float32-range quotient; the step is
+// y <- y + (num exp(-y) - den) / den.
+__device__ __forceinline__ double log_ratio_refined(double num, double den) {
+    const double y = static_cast<double>(
+        __logf(static_cast<float>(num) / static_cast<float>(den)));
+    return y + (num * exp(-y) - den) * static_cast<double>(1.0f / static_cast<float>(den));
+}
+
 // Zwicker loudness sl (2 th)^e ((0.5 + 0.5 x / th)^e - 1) above the threshold,
 // written as loud_scale expm1(e log1p((x - th) / (2 th))) so that bands just
 // above their threshold keep full precision (inv2th = 1 / (2 th)).
 __device__ __forceinline__ double loudness(double x, double th, double inv2th, double e,
                                            double ls) {
     if (!(x > th)) return 0.0;
-    return ls * expm1(e * log1p((x - th) * inv2th));
+    return ls * expm1(e * log1p_refined((x - th) * inv2th));
 }
 
 // d loudness / dx from the loudness l itself: with 1 + u = (x + th) / (2 th),
@@ -230,7 +259,7 @@ __device__ __forceinline__ double loudness_slope(double x, double l, double th, 
 // raw asymmetry factor ((ed + 50) / (er + 50))^1.2; the backward reads the
 // forward's values, so the clamp decisions (below 3, above 12) agree
 __device__ __forceinline__ double asymmetry(double ed, double er) {
-    return exp(1.2 * log((ed + 50.0) / (er + 50.0)));
+    return exp(1.2 * log_ratio_refined(ed + 50.0, er + 50.0));
 }
 
 __device__ __forceinline__ double sgn(double v) { return v > 0.0 ? 1.0 : (v < 0.0 ? -1.0 : 0.0); }
@@ -255,7 +284,8 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
     // kLean: the twiddle tables (kHalf entries each) and the window, staged
     // once per workgroup and read per frame (10 KB; two workgroups per CU
     // still fit)
-    __shared__ double2 lds_pass[kLean ? kPassTwiddles : 1], lds_tw512[kLean ? kHalf : 1];
+    using T2 = typename Vec2<real>::type;
+    __shared__ T2 lds_pass[kLean ? kPassTwiddles : 1], lds_tw512[kLean ? kHalf : 1];
     __shared__ float lds_win[kLean ? kNfft : 1];
 
     const ModelTable &t = *a.tab;
@@ -294,12 +324,12 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
     cplx<real> *buf = fftbuf[wave];
     real *power_buf = reinterpret_cast<real *>(buf);
     // kLean reads the twiddles per pass from LDS; otherwise they stay in registers
-    using TW = typename std::conditional<kLean, LdsTwiddles, Twiddles>::type;
+    using TW = typename std::conditional<kLean, LdsTwiddles<real>, Twiddles<real>>::type;
     TW tw;
     if constexpr (kLean) {
         for (int i = threadIdx.x; i < kNfft; i += kWave * kWaves) {
-            if (i < kPassTwiddles) lds_pass[i] = pass_twiddle_entry(t.tw256, i);
-            if (i < kHalf) lds_tw512[i] = t.tw512[i];
+            if (i < kPassTwiddles) lds_pass[i] = to_vec2<real>(pass_twiddle_entry(t.tw256, i));
+            if (i < kHalf) lds_tw512[i] = to_vec2<real>(t.tw512[i]);
             lds_win[i] = t.window[i];
         }
         __syncthreads();
@@ -354,14 +384,9 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
             power_buf[fbin] = fbin == 0 ? real(0) : (x[r].re * x[r].re + x[r].im * x[r].im) * scale2;
         }
         wave_lds_fence();
+        const double acc = band_power(power_buf, lane, band_lo, band_hi);
         double val = 0.0;
         if (lane < kBands) {
-            double acc = 0.0;
-            if constexpr (kLean) {
-                for (int f = band_lo; f < band_hi; ++f) acc += static_cast<double>(power_buf[f]);
-            } else {
-                acc = band_sum(power_buf, band_lo, band_hi);
-            }
             const float v = static_cast<float>(acc * corr);
             bark[frame * kBands + lane] = v;
             barks[side][local][lane] = v;
@@ -550,12 +575,19 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
         tad[q] = wave_sum(ad);
     }
 
+    // h = ((taer + 1e5) / 1e7)^0.04 of the wavefront's frames, frame q in lane
+    // q (the totals are the same in every lane), read back per frame
+    double t_lane = taer[1];
+#pragma unroll
+    for (int q = 1; q < kPer; ++q) t_lane = lane == q ? taer[q + 1] : t_lane;
+    const double h_lane = exp(0.04 * log((t_lane + 1e5) / 1e7));
+
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
         const int64_t frame = f0 + q;
         if (frame >= L.frames) break;
         const double fpr0 = (taer[q + 1] + 5e3) / (tad[q + 1] + 5e3);
-        const double h = exp(0.04 * log((taer[q + 1] + 1e5) / 1e7));
+        const double h = read_lane(h_lane, q);
         const double inv_h = 1.0 / h;
         const double fpr1 =
             frame > 0 ? fpr0 * 0.8 + ((taer[q] + 5e3) / (tad[q] + 5e3)) * 0.2 : fpr0;
@@ -946,7 +978,8 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
     __shared__ double scratch[kBwdFrames];
     // the twiddle tables, window and bin-to-band map, staged once per
     // workgroup (both FFTs of every frame read them)
-    __shared__ double2 lds_pass[kPassTwiddles], lds_tw512[kHalf];
+    using T2 = typename Vec2<real>::type;
+    __shared__ T2 lds_pass[kPassTwiddles], lds_tw512[kHalf];
     __shared__ float lds_win[kNfft];
     __shared__ int lds_bin_band[kHalf];
 
@@ -980,9 +1013,9 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
     const double *grp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
     if (lane < kBands) gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kBwdFrames, lane, kBands);
     for (int k = threadIdx.x; k < kNfft; k += kWave * kBwdFrames) {
-        if (k < kPassTwiddles) lds_pass[k] = pass_twiddle_entry(t.tw256, k);
+        if (k < kPassTwiddles) lds_pass[k] = to_vec2<real>(pass_twiddle_entry(t.tw256, k));
         if (k < kHalf) {
-            lds_tw512[k] = t.tw512[k];
+            lds_tw512[k] = to_vec2<real>(t.tw512[k]);
             lds_bin_band[k] = t.bin_band[k];
         }
         lds_win[k] = t.window[k];
@@ -1004,7 +1037,7 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
     if (live) {
         // twiddles read per pass from LDS (fewer live registers: five
         // wavefronts per SIMD)
-        const LdsTwiddles tw{lds_pass, lds_tw512, lane};
+        const LdsTwiddles<real> tw{lds_pass, lds_tw512, lane};
         float win[8];
         int bin_band[4];
 #pragma unroll
@@ -1209,7 +1242,7 @@ __global__ void __launch_bounds__(kWave *kPlainWaves) stft_plain_fwd_kernel(Stft
     };
     cplx<real> *buf = fftbuf[wave];
     cplx<real> spec[4];
-    Twiddles tw;
+    Twiddles<real> tw;
     tw.load(t.tw256, t.tw512, lane);
     frame_spectrum<real>(u, spec, buf, tw, lane);
     real *power = reinterpret_cast<real *>(buf);
@@ -1251,7 +1284,7 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_plain_bwd_kernel(StftA
             return static_cast<real>(load_or_zero(x, n, a.len)) * static_cast<real>(t.window[k]);
         };
         cplx<real> spec[4], v[4];
-        Twiddles tw;
+        Twiddles<real> tw;
         tw.load(t.tw256, t.tw512, lane);
         frame_spectrum<real>(u, spec, fftbuf[wave], tw, lane);
 #pragma unroll
@@ -1286,17 +1319,31 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_plain_bwd_kernel(StftA
 // host entry points
 // ---------------------------------------------------------------------------
 
-// FFT arithmetic of the forward STFT kernels and the stand-alone operator.
-// float64 costs no measurable time there (float64 FMA issues at the float32
-// rate with packed float32 disabled) and cuts the spectral rounding error.
+// FFT arithmetic of the stand-alone STFT operator: float64.
 #ifndef PESQ_STFT_REAL
 #define PESQ_STFT_REAL double
 #endif
 using StftReal = PESQ_STFT_REAL;
+// FFT arithmetic of the fused forward STFT of small grids (latency bound) and
+// of large grids (throughput bound): float32 passes, twiddles and bins, with
+// the band sums in float64.  The kernels are bound by LDS traffic and issue,
+// and float32 halves the LDS bytes of every pass and the registers (five
+// wavefronts per SIMD at large grids instead of four): 98 instead of 142 us at
+// BASELINE c5, 11.2 instead of 14.4 us at c2.  The distances then differ from
+// float64 by up to 2.5e-6 at c5 and 4e-7 at c2 (5e-7 and 7e-8 with float64
+// passes), within the 1e-5 bound.
+#ifndef PESQ_STFT_FUSED_REAL
+#define PESQ_STFT_FUSED_REAL float
+#endif
+#ifndef PESQ_STFT_LEAN_REAL
+#define PESQ_STFT_LEAN_REAL float
+#endif
+using StftFusedReal = PESQ_STFT_FUSED_REAL;
+using StftLeanReal = PESQ_STFT_LEAN_REAL;
 // The backward's FFTs (spectrum recomputed, adjoint) run in float32: fewer
 // registers (five wavefronts per SIMD instead of four; 20.3 instead of 22.9 us
 // at BASELINE c2) for a gradient error of about 2e-6 of its peak instead of
-// 5e-7 (the forward Bark spectra, and so the distances, stay float64).
+// 5e-7.
 using StftBwdReal = float;
 
 // Chain launches: up to about two workgroups per CU of the 256 CU MI355X the
@@ -1412,7 +1459,9 @@ extern "C" int pesq_pipeline_kernels(int64_t batch, int64_t len, int grad_mask, 
     PESQ_CHECK_ARG((grad_mask & ~3) == 0, "invalid grad_mask %d", grad_mask);
     PESQ_CHECK_ARG(!backward || grad_mask != 0, "backward needs a non-empty grad_mask");
     const PipePlan P = pipe_plan(L);
-    const char *real = std::is_same<StftReal, double>::value ? "double" : "float";
+    const bool lean_double = std::is_same<StftLeanReal, double>::value;
+    const bool fused_double = std::is_same<StftFusedReal, double>::value;
+    const char *real = (P.stft_lean ? lean_double : fused_double) ? "double" : "float";
     const char *bwd_real = std::is_same<StftBwdReal, double>::value ? "double" : "float";
     std::string out;
     if (!backward) {
@@ -1485,10 +1534,10 @@ extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, 
     if (stages & 4u) {
         const unsigned grid = static_cast<unsigned>(batch * L.ntile);
         if (!pipe_plan(L).stft_lean) {
-            hipLaunchKernelGGL((stft_fwd_kernel<StftReal, false>), dim3(grid),
+            hipLaunchKernelGGL((stft_fwd_kernel<StftFusedReal, false>), dim3(grid),
                                dim3(kWave * kStftWaves), 0, stream, a);
         } else {
-            hipLaunchKernelGGL((stft_fwd_kernel<StftReal, true>), dim3(grid),
+            hipLaunchKernelGGL((stft_fwd_kernel<StftLeanReal, true>), dim3(grid),
                                dim3(kWave * kStftWaves), 0, stream, a);
         }
         PESQ_CHECK_LAUNCH("pipeline stft");

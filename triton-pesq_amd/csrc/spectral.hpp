@@ -34,22 +34,6 @@ __device__ __forceinline__ void load_frame(const float *x, int64_t start, int64_
     }
 }
 
-// sum of p[lo .. hi - 1] in index order (hi - lo <= kMaxBandBins), the reads
-// issued together
-template <typename real>
-__device__ __forceinline__ double band_sum(const real *p, int lo, int hi) {
-    double v[kMaxBandBins];
-#pragma unroll
-    for (int i = 0; i < kMaxBandBins; ++i) {
-        const int f = lo + i;
-        v[i] = static_cast<double>(p[f < kHalf ? f : kHalf - 1]);
-    }
-    double acc = 0.0;
-#pragma unroll
-    for (int i = 0; i < kMaxBandBins; ++i) acc += lo + i < hi ? v[i] : 0.0;
-    return acc;
-}
-
 template <typename real>
 struct cplx {
     real re, im;
@@ -90,14 +74,62 @@ __device__ __forceinline__ void wave_lds_fence() {
     __builtin_amdgcn_wave_barrier();
 }
 
+// Power of the band [lo, hi) of every lane from the 256 bins p[0 .. 255] of
+// the wave's LDS buffer, through a float64 prefix sum: lane l adds bins
+// 4 l .. 4 l + 3 in order, a wave scan turns the lane totals into
+// S_k = sum_{g <= k} p_g, and the band is S_{hi-1} - S_{lo-1}.  Its rounding
+// is a few units of 2^-53 of the frame's total power, far below the float32
+// rounding of the band value.  The prefix sums overwrite the buffer (kHalf
+// doubles, which the frame buffer holds for float and double bins alike).
+template <typename real>
+__device__ __forceinline__ double band_power(real *p, int lane, int lo, int hi) {
+    real b[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = p[4 * lane + j];
+    double s[4];
+    s[0] = static_cast<double>(b[0]);
+#pragma unroll
+    for (int j = 1; j < 4; ++j) s[j] = s[j - 1] + static_cast<double>(b[j]);
+    const double before = wave_shift_up(wave_inclusive_scan(s[3]));
+    wave_lds_fence();
+    double *prefix = reinterpret_cast<double *>(p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) prefix[4 * lane + j] = before + s[j];
+    wave_lds_fence();
+    const double upper = hi > 0 ? prefix[hi - 1] : 0.0;
+    const double lower = lo > 0 ? prefix[lo - 1] : 0.0;
+    wave_lds_fence();
+    return upper - lower;
+}
+
+// Two-component vector of the twiddle tables staged in LDS for an FFT in
+// `real` arithmetic (the tables are stored in the arithmetic's precision).
+template <typename real>
+struct Vec2;
+template <>
+struct Vec2<float> {
+    using type = float2;
+};
+template <>
+struct Vec2<double> {
+    using type = double2;
+};
+
+template <typename real>
+__device__ __forceinline__ typename Vec2<real>::type to_vec2(double2 w) {
+    return {static_cast<real>(w.x), static_cast<real>(w.y)};
+}
+
 // Per lane twiddles of every FFT pass and of the real-FFT fold, loaded once
 // per kernel so that no pass waits on a memory load:
 //   pass[p][r - 1] = e^{-2 pi i k r / (4 ns)}, ns = 4^p (p = 1..3), k = lane mod ns
 //   fold[r]        = e^{-2 pi i f / 512},      f = lane + 64 r
 // (pass 0 has ns = 1 and only unit twiddles).
+template <typename real>
 struct Twiddles {
-    double2 pass[3][3];
-    double2 fold[4];
+    using T2 = typename Vec2<real>::type;
+    T2 pass[3][3];
+    T2 fold[4];
 
     __device__ __forceinline__ void load(const double2 *tw256, const double2 *tw512, int lane) {
 #pragma unroll
@@ -105,13 +137,14 @@ struct Twiddles {
             const int ns = 1 << (2 * p);
             const int k = lane & (ns - 1);
 #pragma unroll
-            for (int r = 1; r < 4; ++r) pass[p - 1][r - 1] = tw256[(k * r * (64 / ns)) & 255];
+            for (int r = 1; r < 4; ++r)
+                pass[p - 1][r - 1] = to_vec2<real>(tw256[(k * r * (64 / ns)) & 255]);
         }
 #pragma unroll
-        for (int r = 0; r < 4; ++r) fold[r] = tw512[lane + 64 * r];
+        for (int r = 0; r < 4; ++r) fold[r] = to_vec2<real>(tw512[lane + 64 * r]);
     }
-    __device__ __forceinline__ double2 pass_tw(int p, int r) const { return pass[p - 1][r - 1]; }
-    __device__ __forceinline__ double2 fold_tw(int r) const { return fold[r]; }
+    __device__ __forceinline__ T2 pass_tw(int p, int r) const { return pass[p - 1][r - 1]; }
+    __device__ __forceinline__ T2 fold_tw(int r) const { return fold[r]; }
 };
 
 // The same twiddles read from the tables when a pass needs them: fewer values
@@ -147,15 +180,17 @@ __device__ __forceinline__ double2 pass_twiddle_entry(const double2 *tw256, int 
     return tw256[(k * r * (64 / ns)) & 255];
 }
 
+template <typename real>
 struct LdsTwiddles {
-    const double2 *pass, *fold;
+    using T2 = typename Vec2<real>::type;
+    const T2 *pass, *fold;
     int lane;
 
-    __device__ __forceinline__ double2 pass_tw(int p, int r) const {
+    __device__ __forceinline__ T2 pass_tw(int p, int r) const {
         const int ns = 1 << (2 * p);
         return pass[pass_offset(p) + (r - 1) * ns + (lane & (ns - 1))];
     }
-    __device__ __forceinline__ double2 fold_tw(int r) const { return fold[lane + 64 * r]; }
+    __device__ __forceinline__ T2 fold_tw(int r) const { return fold[lane + 64 * r]; }
 };
 
 // In: v[r] = z_{lane + 64 r}.  Out: buf[slot(n)] = Z_n, unnormalised.
@@ -171,7 +206,7 @@ __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, cons
             wave_lds_fence();
 #pragma unroll
             for (int r = 1; r < 4; ++r) {
-                const double2 w = tw.pass_tw(pass, r);
+                const auto w = tw.pass_tw(pass, r);
                 const cplx<real> c = {static_cast<real>(w.x),
                                       static_cast<real>(kInverse ? -w.y : w.y)};
                 v[r] = cmul(v[r], c);
@@ -207,7 +242,7 @@ __device__ __forceinline__ void frame_spectrum(Load u, cplx<real> (&x)[4], cplx<
         // E = (Zf + conj Zm) / 2,  O = -i (Zf - conj Zm) / 2
         const cplx<real> e = {(zf.re + zm.re) * real(0.5), (zf.im - zm.im) * real(0.5)};
         const cplx<real> o = {(zf.im + zm.im) * real(0.5), -(zf.re - zm.re) * real(0.5)};
-        const double2 w = tw.fold_tw(r);
+        const auto w = tw.fold_tw(r);
         const cplx<real> c = {static_cast<real>(w.x), static_cast<real>(w.y)};
         const cplx<real> t = cmul(c, o);
         x[r] = {e.re + t.re, e.im + t.im};
@@ -233,7 +268,7 @@ __device__ __forceinline__ void frame_adjoint(const cplx<real> (&vf)[4], real (&
         const cplx<real> b = f == 0 ? cplx<real>{real(0), real(0)} : buf[slot(kHalf - f)];
         const cplx<real> s = {a.re + b.re, a.im - b.im};   // V_f + conj V_{256-f}
         const cplx<real> d = {a.re - b.re, a.im + b.im};   // V_f - conj V_{256-f}
-        const double2 w = tw.fold_tw(r);
+        const auto w = tw.fold_tw(r);
         const cplx<real> c = {static_cast<real>(w.x), static_cast<real>(-w.y)};  // e^{+...}
         const cplx<real> t = cmul(c, d);
         // Z' = s + i t
