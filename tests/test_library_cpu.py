@@ -349,7 +349,7 @@ VARIANTS = {
     (8, 128000, 2): (
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, true>",
-         "stft_fwd_kernel<double, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
+         "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, true>"],
@@ -358,7 +358,7 @@ VARIANTS = {
     (4, 960000, 2): (
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
-         "stft_fwd_kernel<double, true, 8>", "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
+         "stft_fwd_kernel<float, true, 8>", "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
@@ -368,7 +368,7 @@ VARIANTS = {
     (256, 64000, 2): (
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, false>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeFwdMode, false, false>",
-         "stft_fwd_kernel<double, true, 8>", "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
+         "stft_fwd_kernel<float, true, 8>", "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, false>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, false, false>"],
@@ -377,7 +377,7 @@ VARIANTS = {
     (16, 64000, 2): (
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, true>",
-         "stft_fwd_kernel<double, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
+         "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, true>"],
