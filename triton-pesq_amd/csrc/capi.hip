@@ -63,6 +63,19 @@ static int fill_sections(IirTable &t, int first, const pesq_iir_sections &s, dou
             std::memcpy(t.pw[level][q], p, sizeof(p));
             mat_mul(p, p, p);
         }
+        // chunk end state weights: fir[i] = A^(kChunk - 1 - i) beta, beta the
+        // state increment per unit input (y = b0 x + z1 feeds back through a1, a2)
+        {
+            double g[2] = {t.b1[q] - s.a1[k] * t.b0[q], t.b2[q] - s.a2[k] * t.b0[q]};
+            for (int m = 0; m < kChunk; ++m) {
+                t.fir[q][kChunk - 1 - m][0] = g[0];
+                t.fir[q][kChunk - 1 - m][1] = g[1];
+                const double g0 = a[0] * g[0] + a[1] * g[1];
+                const double g1 = a[2] * g[0] + a[3] * g[1];
+                g[0] = g0;
+                g[1] = g1;
+            }
+        }
         // lane start powers A^(kChunk lane): product of the levels of the set bits
         for (int lane = 0; lane < kWave; ++lane) {
             double m[4] = {1.0, 0.0, 0.0, 1.0};

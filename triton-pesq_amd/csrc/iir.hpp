@@ -70,6 +70,10 @@ struct IirTable {
     double a1[kMaxSections], a2[kMaxSections];
     double pw[kLevels][kMaxSections][4];     // A_k^(kChunk 2^j), row major 2x2
     double lane_pw[kMaxSections][kWave][4];  // A_k^(kChunk lane), lane start powers
+    // A_k^(kChunk - 1 - i) beta_k: the weight of the chunk's sample i in the
+    // section's state after the chunk, from a zero state (beta_k: the state
+    // increment per unit input, (b1 - a1 b0, b2 - a2 b0))
+    double fir[kMaxSections][kChunk][2];
 };
 
 // Small grids (those that keep lane states) of rows of up to
@@ -479,19 +483,57 @@ __device__ __forceinline__ void element_inputs(const Mode &m,
     }
 }
 
-// zero state run over the lane's chunk
-template <bool kGeneral, int NA, int NB, class Mode>
-__device__ __forceinline__ void zero_run(const Mode &m, const Coeffs<0, NA, Mode::kB2> &ca,
+// state of NS sections from S0 after the chunk, from a zero state, as the
+// weighted sums of the chunk's inputs x[0 .. kChunk - 1]: kChunk independent
+// fused multiply-adds per state component instead of the recursion's chain
+template <int S0, int NS>
+__device__ __forceinline__ void chunk_end_state(const IirTable &t, const double (&x)[kChunk],
+                                                Bank<NS> &s) {
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        double u = t.fir[S0 + k][0][0] * x[0];
+        double v = t.fir[S0 + k][0][1] * x[0];
+#pragma unroll
+        for (int i = 1; i < kChunk; ++i) {
+            u = fma(t.fir[S0 + k][i][0], x[i], u);
+            v = fma(t.fir[S0 + k][i][1], x[i], v);
+        }
+        s.u[k] = u;
+        s.v[k] = v;
+    }
+}
+
+// zero state run over the lane's chunk: the state after it.  With kWeighted,
+// interior chunks form it as weighted sums of the inputs (chunk_end_state):
+// fewer and independent operations, which large grids (throughput bound)
+// gain from (14 us at BASELINE c5); small grids (latency bound) lose about
+// 1 us to the weights' scalar loads and keep the recursion.  Chunks at a row
+// end always run the recursion, with the ramp weights and bounds of
+// element_inputs.
+template <bool kGeneral, bool kWeighted, int NA, int NB, class Mode>
+__device__ __forceinline__ void zero_run(const Mode &m, const IirTable &t,
+                                         const Coeffs<0, NA, Mode::kB2> &ca,
                                          const Coeffs<NA, NB, Mode::kB2> &cb,
                                          const typename Mode::In (&in)[kChunk][Mode::kInputs],
                                          int64_t j0,
                                          int64_t len, BankPair<NA, NB> &s) {
+    if constexpr (kGeneral || !kWeighted) {
 #pragma unroll
-    for (int i = 0; i < kChunk; ++i) {
-        double w, xa, xb;
-        element_inputs<kGeneral>(m, in[i], j0 + i, len, w, xa, xb);
-        if constexpr (NA > 0) ca.step(s.a, xa);
-        if constexpr (NB > 0) cb.step(s.b, xb);
+        for (int i = 0; i < kChunk; ++i) {
+            double w, xa, xb;
+            element_inputs<kGeneral>(m, in[i], j0 + i, len, w, xa, xb);
+            if constexpr (NA > 0) ca.step(s.a, xa);
+            if constexpr (NB > 0) cb.step(s.b, xb);
+        }
+    } else {
+        double xa[kChunk], xb[kChunk];
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) {
+            double w;
+            element_inputs<false>(m, in[i], j0 + i, len, w, xa[i], xb[i]);
+        }
+        if constexpr (NA > 0) chunk_end_state<0, NA>(t, xa, s.a);
+        if constexpr (NB > 0) chunk_end_state<NA, NB>(t, xb, s.b);
     }
 }
 
@@ -546,9 +588,9 @@ __global__ void __launch_bounds__(kWave)
     BankPair<NA, NB> s;
     s.zero();
     if (general_chunk(j0, len)) {
-        zero_run<true>(m, ca, cb, in, j0, len, s);
+        zero_run<true, !kLaneStates>(m, t, ca, cb, in, j0, len, s);
     } else {
-        zero_run<false>(m, ca, cb, in, j0, len, s);
+        zero_run<false, !kLaneStates>(m, t, ca, cb, in, j0, len, s);
     }
     s.scan_chunks(t, lane);
     if (lane == kWave - 1) {
@@ -680,9 +722,9 @@ __global__ void __launch_bounds__(kWave)
         zb.load(t2, t2.c0b);
         s.zero();
         if (general_chunk(j0, len)) {
-            zero_run<true>(m, za, zb, in, j0, len, s);
+            zero_run<true, true>(m, t2, za, zb, in, j0, len, s);
         } else {
-            zero_run<false>(m, za, zb, in, j0, len, s);
+            zero_run<false, true>(m, t2, za, zb, in, j0, len, s);
         }
         s.scan_chunks(t2, lane);
 #pragma unroll
