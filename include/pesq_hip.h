@@ -266,9 +266,15 @@ int pesq_resample_backward(const float *grad_y, float *grad_x, int64_t rows, int
  * `plan` is not NULL, writes info->bytes bytes of tables (host memory, to be
  * copied to the device).  fwd_span / bwd_span of 0 mean the rate pair's
  * window is too wide for the LDS tile; the untiled entry points above then
- * apply.  Same results as pesq_resample_forward / _backward (the same sums
- * in the same order).  Replaces _resample_fwd_kernel / _resample_bwd_kernel
- * (resample.py:113-243). */
+ * apply.  The forward sums the same terms in the same order as
+ * pesq_resample_forward.  The adjoint of a rate pair with new_step > 1 is
+ * itself a resampler from the new rate to the old one (upsampling by
+ * orig_step and downsampling by new_step, with the bank transposed): input i
+ * receives the contiguous run of outputs whose taps cover it, adj_taps of
+ * them at most, so the plan holds that transposed bank (adj_*) and the
+ * adjoint runs the forward's tiled kernel on it, summing over the outputs in
+ * ascending order (the untiled adjoint adds the same terms sweep by sweep).
+ * Replaces _resample_fwd_kernel / _resample_bwd_kernel (resample.py:113-243). */
 typedef struct pesq_resample_plan_info {
     int32_t orig_step, new_step, width, width_total;
     int32_t taps;             /* longest non-zero tap run of one phase */
@@ -279,6 +285,10 @@ typedef struct pesq_resample_plan_info {
     int32_t fwd_span, bwd_span; /* floats staged per workgroup, 0 = not tiled */
     int64_t bytes;            /* size of the plan tables */
     int64_t off_offs, off_cols, off_col_lo, off_taps64, off_row64; /* table offsets */
+    /* the adjoint as a resampler from new_step to orig_step (new_step > 1):
+     * gx[l orig + j] = sum_{t < adj_taps} adj[t][j] gy[l new_step + adj_offs[j] + t] */
+    int32_t adj_taps, adj_off_min, adj_off_max, adj_span; /* adj_span 0: not used */
+    int64_t off_adj_taps, off_adj_offs;                   /* table offsets */
 } pesq_resample_plan_info;
 
 int pesq_resample_plan(const float *kernel, const int32_t *tap_lo, const int32_t *tap_hi,

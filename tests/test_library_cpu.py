@@ -478,3 +478,37 @@ def test_kernel_trace_normalises_library_names():
     assert normalise(mangled) == "iir_aggregate_kernel<5,1,PipeFwdMode,true>"
     assert library_kernels(8, 128000, 2, False)[0] == "iir_aggregate_kernel<5,1,PipeFwdMode,true>"
     assert all(" " not in k for k in library_kernels(4, 960000, 2, True))
+
+
+@pytest.mark.parametrize("orig,new", [(44100, 16000), (22050, 16000), (8000, 16000), (13, 7), (7, 13)])
+def test_resample_plan_transposed_bank_is_the_adjoint(orig, new):
+    """The plan's adjoint bank (host packing, no GPU): applying it as a resampler
+    from the new rate to the old one, ``gx[l o + j] = sum_t adj[t][j]
+    gy[l n + adj_offs[j] + t]``, gives the float64 adjoint of the oracle's
+    resampler on a random upstream gradient."""
+
+    from oracle import pesq_oracle as O
+    from torch_pesq.hip_ops.resample import HipResample
+
+    mod = HipResample(orig, new)
+    info = mod.plan_info
+    o, n = info.orig_step, info.new_step
+    assert info.adj_span > 0 and info.adj_taps >= 1
+    plan = mod.plan.numpy()
+    adj = plan[info.off_adj_taps:info.off_adj_taps + 4 * info.adj_taps * o].view(np.float32)
+    adj = adj.reshape(info.adj_taps, o).astype(np.float64)
+    offs = plan[info.off_adj_offs:info.off_adj_offs + 4 * o].view(np.int32)
+    length = 2 * 441 + 17
+    x = torch.randn(1, length, dtype=torch.float64, requires_grad=True)
+    y = O.resample(x, orig, new)
+    gy = torch.randn(y.shape, dtype=torch.float64, generator=torch.Generator().manual_seed(1))
+    (want,) = torch.autograd.grad(y, x, grad_outputs=gy)
+    g = gy[0].numpy()
+    got = np.zeros(length)
+    for i in range(length):
+        l, j = divmod(i, o)
+        m = l * n + offs[j] + np.arange(info.adj_taps)
+        ok = (m >= 0) & (m < g.shape[0])
+        got[i] = np.dot(adj[:, j][ok], g[m[ok]])
+    # the oracle's bank is the float32 bank promoted: the same products
+    np.testing.assert_allclose(got, want[0].numpy(), rtol=0, atol=1e-12 * np.abs(g).max())

@@ -106,7 +106,7 @@ static int pack_iir(IirTable &t, const pesq_iir_sections *a, const pesq_iir_sect
 
 using namespace pesq;
 
-extern "C" int pesq_abi_version(void) { return 1; }
+extern "C" int pesq_abi_version(void) { return 2; }
 
 extern "C" const char *pesq_last_error(void) { return g_error; }
 

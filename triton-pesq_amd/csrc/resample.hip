@@ -166,6 +166,27 @@ __device__ __forceinline__ void stage_row4(float *__restrict__ dst, const float 
     }
 }
 
+// Copy of a table of n floats into LDS; every thread issues the loads of a
+// batch of 8 before their stores (indices clamped into the table, values past
+// its end dropped), so that a batch costs one memory round trip instead of 8.
+__device__ __forceinline__ void stage_table(float *__restrict__ dst, const float *__restrict__ src,
+                                            int n) {
+    constexpr int kBatch = 8;
+    for (int s0 = 0; s0 < n; s0 += kResampleThreads * kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int s = s0 + b * kResampleThreads + static_cast<int>(threadIdx.x);
+            v[b] = src[s < n ? s : n - 1];
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+            const int s = s0 + b * kResampleThreads + static_cast<int>(threadIdx.x);
+            if (s < n) dst[s] = v[b];
+        }
+    }
+}
+
 constexpr int kTileQ = 4;
 constexpr int kTileOut = kResampleThreads * kTileQ;
 constexpr int kMaxSpan = 8192;   // staged samples per workgroup (32 KiB)
@@ -190,9 +211,7 @@ __global__ void __launch_bounds__(kResampleThreads)
     const int64_t in_lo = l_first * orig + off_min;
     const float *xr = x + row * n_in;
     stage_row4<0, kStageBatch / 4>(xs, xr, in_lo, n_in, span);
-    if constexpr (kSource == kTapsLds) {
-        for (int s = threadIdx.x; s < ntaps * nstep; s += kResampleThreads) tl[s] = taps[s];
-    }
+    if constexpr (kSource == kTapsLds) stage_table(tl, taps, ntaps * nstep);
     __syncthreads();
     int j[kTileQ], base[kTileQ];
     double acc[kTileQ];
@@ -625,12 +644,48 @@ extern "C" int pesq_resample_plan(const float *kernel, const int32_t *tap_lo,
     }
     r.fwd_span = fwd_span <= kMaxSpan ? static_cast<int32_t>(fwd_span) : 0;
     r.bwd_span = bwd_span <= kMaxSpan ? static_cast<int32_t>(bwd_span) : 0;
+    // The adjoint as a resampler from new_step to orig_step: input i = l orig + j
+    // (i + width = (l + carry) orig + rho, carry and rho from j) receives the
+    // outputs m = (l + carry) nstep + m_rel over the tap columns k = rho + s orig
+    // and their phases, m_rel = col_lo[k] + p - s nstep: one contiguous run of
+    // outputs per j (runs of different sweeps do not overlap, and gaps between
+    // them get zero taps), starting at adj_offs[j] = carry nstep + min m_rel.
+    std::vector<int32_t> adj_lo(orig, 0), adj_n(orig, 0);
+    int adj_taps = 1, adj_off_min = 1 << 30, adj_off_max = -(1 << 30);
+    if (nstep > 1) {
+        for (int j = 0; j < orig; ++j) {
+            const int rho = (j + r.width) % orig, carry = (j + r.width) / orig;
+            int lo = 1 << 30, hi = -(1 << 30);
+            for (int s = 0; s < sweeps; ++s) {
+                const int k = rho + s * orig;
+                if (k >= wtotal || col_n[k] == 0) continue;
+                lo = std::min(lo, col_lo[k] - s * nstep);
+                hi = std::max(hi, col_lo[k] + col_n[k] - 1 - s * nstep);
+            }
+            if (hi < lo) lo = hi = 0;  // no tap reads this input: one zero tap
+            adj_lo[j] = carry * nstep + lo;
+            adj_n[j] = hi - lo + 1;
+            adj_taps = std::max(adj_taps, adj_n[j]);
+            adj_off_min = std::min(adj_off_min, adj_lo[j]);
+            adj_off_max = std::max(adj_off_max, adj_lo[j]);
+        }
+        const int64_t adj_periods = (kTileOut - 1) / orig + 1;
+        const int64_t adj_span = adj_periods * nstep + (adj_off_max - adj_off_min) + adj_taps;
+        r.adj_taps = adj_taps;
+        r.adj_off_min = adj_off_min;
+        r.adj_off_max = adj_off_max;
+        r.adj_span = adj_span <= kMaxSpan && int64_t(adj_taps) * orig <= kMaxTable
+                         ? static_cast<int32_t>(adj_span)
+                         : 0;
+    }
     r.off_offs = align256(int64_t(taps) * nstep * sizeof(float));
     r.off_cols = r.off_offs + align256(int64_t(nstep) * sizeof(int32_t));
     r.off_col_lo = r.off_cols + align256(int64_t(phases) * ncols * sizeof(float));
     r.off_taps64 = r.off_col_lo + align256(int64_t(ncols) * sizeof(int32_t));
     r.off_row64 = r.off_taps64 + align256(int64_t(taps) * sizeof(double));
-    r.bytes = r.off_row64 + align256(int64_t(ncols) * sizeof(double));
+    r.off_adj_taps = r.off_row64 + align256(int64_t(ncols) * sizeof(double));
+    r.off_adj_offs = r.off_adj_taps + align256(int64_t(r.adj_taps) * orig * sizeof(float));
+    r.bytes = r.off_adj_offs + align256(int64_t(orig) * sizeof(int32_t));
     *info = r;
     if (plan == nullptr) return PESQ_OK;
 
@@ -654,6 +709,22 @@ extern "C" int pesq_resample_plan(const float *kernel, const int32_t *tap_lo,
         clo[k] = col_lo[k];
         for (int p = 0; p < col_n[k]; ++p) {
             cols[int64_t(p) * ncols + k] = kernel[int64_t(col_lo[k] + p) * wtotal + k];
+        }
+    }
+    if (r.adj_taps > 0) {
+        float *adj = reinterpret_cast<float *>(base + r.off_adj_taps);
+        int32_t *aoffs = reinterpret_cast<int32_t *>(base + r.off_adj_offs);
+        for (int j = 0; j < orig; ++j) {
+            aoffs[j] = adj_lo[j];
+            const int rho = (j + r.width) % orig, carry = (j + r.width) / orig;
+            for (int s = 0; s < sweeps; ++s) {
+                const int k = rho + s * orig;
+                if (k >= wtotal) continue;
+                for (int p = 0; p < col_n[k]; ++p) {
+                    const int t = carry * nstep + col_lo[k] + p - s * nstep - adj_lo[j];
+                    adj[int64_t(t) * orig + j] = kernel[int64_t(col_lo[k] + p) * wtotal + k];
+                }
+            }
         }
     }
     return PESQ_OK;
@@ -801,6 +872,19 @@ extern "C" int pesq_resample_plan_backward(const float *grad_y, float *grad_x, i
                            reinterpret_cast<const double *>(base + r.off_row64), r.orig_step,
                            r.width, r.sweeps, r.bwd_span, nb);
         PESQ_CHECK_LAUNCH("resample backward (uniform)");
+        return PESQ_OK;
+    }
+    if (r.adj_span > 0) {
+        // the transposed bank: the forward's tiled kernel from new_step to orig_step
+        const float *adj = reinterpret_cast<const float *>(base + r.off_adj_taps);
+        const int32_t *aoffs = reinterpret_cast<const int32_t *>(base + r.off_adj_offs);
+        const int64_t table = int64_t(r.adj_taps) * r.orig_step;
+        const size_t lds = size_t(staged_floats(r.adj_span, 0) + table) * sizeof(float);
+        hipLaunchKernelGGL(resample_fwd_tiled<kTapsLds>, dim3(static_cast<unsigned>(rows * bpr)),
+                           dim3(kResampleThreads), lds, stream, grad_y, grad_x, n_out, n_in, adj,
+                           nullptr, aoffs, r.new_step, r.orig_step, r.adj_taps, r.adj_off_min,
+                           r.adj_span, bpr);
+        PESQ_CHECK_LAUNCH("resample backward (transposed bank)");
         return PESQ_OK;
     }
     const float *cols = reinterpret_cast<const float *>(base + r.off_cols);

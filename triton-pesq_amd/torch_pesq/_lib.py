@@ -62,6 +62,12 @@ class ResamplePlanInfo(ctypes.Structure):
         ("off_col_lo", ctypes.c_int64),
         ("off_taps64", ctypes.c_int64),
         ("off_row64", ctypes.c_int64),
+        ("adj_taps", ctypes.c_int32),
+        ("adj_off_min", ctypes.c_int32),
+        ("adj_off_max", ctypes.c_int32),
+        ("adj_span", ctypes.c_int32),
+        ("off_adj_taps", ctypes.c_int64),
+        ("off_adj_offs", ctypes.c_int64),
     ]
 
 
