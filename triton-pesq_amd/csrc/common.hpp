@@ -12,6 +12,13 @@ namespace pesq {
 
 constexpr int kWave = 64;
 
+// Index of the calling wavefront in its workgroup, as a wave-uniform (scalar)
+// value, so that frame and row indices derived from it stay in scalar
+// registers and branches on them are uniform.
+__device__ __forceinline__ int wave_index() {
+    return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kWave);
+}
+
 // ---------------------------------------------------------------------------
 // status / error string (host side)
 // ---------------------------------------------------------------------------

@@ -341,7 +341,7 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
     const int item = blockIdx.x / L.ntile;
     const int tile = blockIdx.x - item * L.ntile;
     const int t0 = tile * kTile;
-    const int wave = threadIdx.x / kWave;
+    const int wave = wave_index();
     const int lane = threadIdx.x % kWave;
     const int side = wave / kSideWaves;          // 0 = reference, 1 = degraded
     const int row = side * L.batch + item;
@@ -366,7 +366,8 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
         rc[2] = scale;
         rc[3] = 0.0;
     }
-    const real scale2 = static_cast<real>(scale * scale);
+    // the transform returns 2 X: |2 X|^2 scale^2 / 4 (exact scalings)
+    const real scale2 = static_cast<real>(scale * scale) * real(0.25);
 
     float *bark = region<float>(a.ws, L.bark) + int64_t(row) * L.frames * kBands;
     cplx<real> *buf = fftbuf[wave];
@@ -421,7 +422,7 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
             return static_cast<real>(cur[i]) * static_cast<real>(win[i]);
         };
         cplx<real> x[4];
-        frame_spectrum<real>(u, x, buf, tw, lane);
+        frame_spectrum<real, true>(u, x, buf, tw, lane);
         if constexpr (!kLean) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) cur[i] = nxt[i];
@@ -507,7 +508,7 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
     const int item = blockIdx.x / L.ntile;
     const int tile = blockIdx.x - item * L.ntile;
     const int t0 = tile * kTile;
-    const int wave = threadIdx.x / kWave;
+    const int wave = wave_index();
     const int lane = threadIdx.x % kWave;
     const double frames_f = static_cast<double>(L.frames);
     const int64_t f0 = t0 + wave * kPer;  // first frame of this wavefront
@@ -731,7 +732,7 @@ __global__ void __launch_bounds__(kFinalThreads) chain_final_kernel(PipeArgs a) 
     }
     acc0 = wave_sum(acc0);
     acc1 = wave_sum(acc1);
-    const int wave = threadIdx.x / kWave;
+    const int wave = wave_index();
     if ((threadIdx.x % kWave) == 0) {
         scratch[0][wave] = acc0;
         scratch[1][wave] = acc1;
@@ -804,7 +805,7 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
     const int item = blockIdx.x / L.ntile;
     const int tile = blockIdx.x - item * L.ntile;
     const int t0 = tile * kTile;
-    const int wave = threadIdx.x / kWave;
+    const int wave = wave_index();
     const int lane = threadIdx.x % kWave;
     bool live[kBPL];
 #pragma unroll
@@ -1044,7 +1045,7 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
     const int row = L.row0 + i;                  // stacked row
     const int item = row % L.batch;
     const bool is_ref = row < L.batch;
-    const int wave = threadIdx.x / kWave;
+    const int wave = wave_index();
     const int lane = threadIdx.x % kWave;
     const int64_t j0 = int64_t(ht) * kBwdHops;   // first output hop block
 
@@ -1111,9 +1112,9 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
             return static_cast<real>(smp[i]) * static_cast<real>(win[i]);
         };
         cplx<real> x[4];
-        frame_spectrum<real>(u, x, buf, tw, lane);
+        frame_spectrum<real, true>(u, x, buf, tw, lane);
         cplx<real> v[4];
-        const real s = static_cast<real>(scale);
+        const real s = static_cast<real>(scale) * real(0.5);  // x holds 2 X
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int band = bin_band[r];
@@ -1284,7 +1285,7 @@ __global__ void __launch_bounds__(kWave *kPlainWaves) stft_plain_fwd_kernel(Stft
     const ModelTable &t = *a.tab;
     const int64_t row = blockIdx.x / a.ftiles;
     const int64_t ft = blockIdx.x - row * a.ftiles;
-    const int wave = threadIdx.x / kWave;
+    const int wave = wave_index();
     const int lane = threadIdx.x % kWave;
     const int64_t frame = ft * kPlainWaves + wave;
     if (frame >= a.frames) return;
@@ -1321,7 +1322,7 @@ __global__ void __launch_bounds__(kWave *kBwdFrames) stft_plain_bwd_kernel(StftA
     const ModelTable &t = *a.tab;
     const int64_t row = blockIdx.x / a.nhoptile;
     const int64_t ht = blockIdx.x - row * a.nhoptile;
-    const int wave = threadIdx.x / kWave;
+    const int wave = wave_index();
     const int lane = threadIdx.x % kWave;
     const int64_t j0 = ht * kBwdHops;
     const int64_t frame = j0 - 1 + wave;

@@ -132,6 +132,32 @@ __device__ __forceinline__ void stage_row4(float *__restrict__ dst, const float 
         }
         return;
     }
+    const int span4 = (span + 3) & ~3;
+    if (lo >= 0 && lo + span4 <= n) {
+        // the segment lies inside the row (every workgroup but those at the
+        // row ends): no clamps or masks.  Groups past the span load the
+        // span's last group again (the same cache lines, no extra memory
+        // traffic) and are not written.
+        const float *seg = src + lo;
+        for (int s0 = 0; s0 < span; s0 += kRound) {
+            float q[kBatch4][4];
+#pragma unroll
+            for (int k = 0; k < kBatch4; ++k) {
+                const int s = s0 + 4 * (k * kResampleThreads + static_cast<int>(threadIdx.x));
+                __builtin_memcpy(q[k], seg + (s < span4 ? s : span4 - 4), sizeof(q[k]));
+            }
+#pragma unroll
+            for (int k = 0; k < kBatch4; ++k) {
+                const unsigned s = s0 + 4 * (k * kResampleThreads + threadIdx.x);
+                if (s < unsigned(span)) {
+                    float *o = dst + (kPad > 0 ? s + s / kPad : s);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[e] = q[k][e];
+                }
+            }
+        }
+        return;
+    }
     for (int s0 = 0; s0 < span; s0 += kRound) {
         // all loads of the batch first, then the edge selection, then the writes
         float q[kBatch4][4];
@@ -333,10 +359,17 @@ __global__ void __launch_bounds__(kResampleThreads)
     }
     if (ntaps > full * kStride) group(xg, tg, std::true_type{}, ntaps - full * kStride);
     float *yr = y + row * n_out;
+    float res[kR];
 #pragma unroll
-    for (int r = 0; r < kR; ++r) {
-        const int64_t m = m0 + int64_t(kR) * threadIdx.x + r;
-        if (m < n_out) yr[m] = static_cast<float>(acc[r]);
+    for (int r = 0; r < kR; ++r) res[r] = static_cast<float>(acc[r]);
+    const int64_t m = m0 + int64_t(kR) * threadIdx.x;
+    if (m0 + kTile <= n_out) {
+        __builtin_memcpy(yr + m, res, sizeof(res));  // 16 byte stores
+    } else {
+#pragma unroll
+        for (int r = 0; r < kR; ++r) {
+            if (m + r < n_out) yr[m + r] = res[r];
+        }
     }
 }
 
@@ -477,9 +510,21 @@ __global__ void __launch_bounds__(kResampleThreads)
     // input of result k: kOrig l_b - width + k
     const int64_t i_b = kOrig * l_b - width;
     float *gxr = gx + row_id * n_in;
-    for (int k = threadIdx.x; k < kPerBlock * kOrig; k += kResampleThreads) {
-        const int64_t i = i_b + k;
-        if (i >= 0 && i < n_in) gxr[i] = out[k];
+    constexpr int kResults = kPerBlock * kOrig;
+    static_assert(kResults % 4 == 0, "results in groups of four");
+    if (i_b >= 0 && i_b + kResults <= n_in) {
+        // inside the row: 16 byte LDS reads (the result region starts at a
+        // multiple of 4 floats) and 16 byte global stores
+        for (int g = threadIdx.x; g < kResults / 4; g += kResampleThreads) {
+            float v[4];
+            __builtin_memcpy(v, out + 4 * g, sizeof(v));
+            __builtin_memcpy(gxr + i_b + 4 * g, v, sizeof(v));
+        }
+    } else {
+        for (int k = threadIdx.x; k < kResults; k += kResampleThreads) {
+            const int64_t i = i_b + k;
+            if (i >= 0 && i < n_in) gxr[i] = out[k];
+        }
     }
 }
 

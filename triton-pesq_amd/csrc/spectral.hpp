@@ -24,9 +24,17 @@ constexpr int kBands = 49;
 constexpr int kMaxBandBins = 25;  // widest Bark band of the 16 kHz table (bins)
 
 // The 8 samples of a 512 sample frame that lane `lane` folds into its 4 complex
-// inputs: s[2 r + e] = x[start + 2 (lane + 64 r) + e] (zero past len).
+// inputs: s[2 r + e] = x[start + 2 (lane + 64 r) + e] (zero past len).  A frame
+// that ends inside the row (all but the padded last one) loads its pairs
+// without bounds checks.
 __device__ __forceinline__ void load_frame(const float *x, int64_t start, int64_t len, int lane,
                                            float (&s)[8]) {
+    if (start + kNfft <= len) {
+        const float *f = x + start + 2 * lane;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) __builtin_memcpy(&s[2 * r], f + 128 * r, 2 * sizeof(float));
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
 #pragma unroll
@@ -193,8 +201,10 @@ struct LdsTwiddles {
     __device__ __forceinline__ T2 fold_tw(int r) const { return fold[lane + 64 * r]; }
 };
 
-// In: v[r] = z_{lane + 64 r}.  Out: buf[slot(n)] = Z_n, unnormalised.
-template <typename real, bool kInverse, class TW>
+// In: v[r] = z_{lane + 64 r}.  Out: v[r] = Z_{lane + 64 r} and, with
+// kStoreLast, buf[slot(n)] = Z_n (unnormalised; the last pass writes element
+// lane + 64 r from lane `lane`, so the lane keeps its own outputs).
+template <typename real, bool kInverse, bool kStoreLast = true, class TW>
 __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, const TW &tw,
                                        int lane) {
 #pragma unroll
@@ -213,6 +223,7 @@ __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, cons
             }
         }
         dft4<real, kInverse>(v);
+        if (pass == 3 && !kStoreLast) break;
         const int k = lane & (ns - 1);
         const int base = (lane / ns) * ns * 4 + k;
 #pragma unroll
@@ -223,8 +234,10 @@ __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, cons
 
 // Spectrum of one frame: X_f for f = lane + 64 r (r = 0..3), given the frame
 // samples u (already windowed) through the load functor u(k), k < 512.
-// tw holds the per lane twiddles (Twiddles::load).
-template <typename real, class Load, class TW>
+// tw holds the per lane twiddles (Twiddles::load).  kDoubled returns 2 X_f
+// (the fold without its two halvings; scaling by 2 is exact, so a caller that
+// takes a factor 1/2 or 1/4 into its own constants gets the same values).
+template <typename real, bool kDoubled = false, class Load, class TW>
 __device__ __forceinline__ void frame_spectrum(Load u, cplx<real> (&x)[4], cplx<real> *buf,
                                                const TW &tw, int lane) {
     cplx<real> v[4];
@@ -237,11 +250,12 @@ __device__ __forceinline__ void frame_spectrum(Load u, cplx<real> (&x)[4], cplx<
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int f = lane + 64 * r;
-        const cplx<real> zf = buf[slot(f)];
+        const cplx<real> zf = v[r];
         const cplx<real> zm = buf[slot((kHalf - f) & (kHalf - 1))];
         // E = (Zf + conj Zm) / 2,  O = -i (Zf - conj Zm) / 2
-        const cplx<real> e = {(zf.re + zm.re) * real(0.5), (zf.im - zm.im) * real(0.5)};
-        const cplx<real> o = {(zf.im + zm.im) * real(0.5), -(zf.re - zm.re) * real(0.5)};
+        const real h = kDoubled ? real(1) : real(0.5);
+        const cplx<real> e = {(zf.re + zm.re) * h, (zf.im - zm.im) * h};
+        const cplx<real> o = {(zf.im + zm.im) * h, -(zf.re - zm.re) * h};
         const auto w = tw.fold_tw(r);
         const cplx<real> c = {static_cast<real>(w.x), static_cast<real>(w.y)};
         const cplx<real> t = cmul(c, o);
@@ -275,14 +289,13 @@ __device__ __forceinline__ void frame_adjoint(const cplx<real> (&vf)[4], real (&
         v[r] = {s.re - t.im, s.im + t.re};
     }
     wave_lds_fence();
-    fft256<real, true>(v, buf, tw, lane);
+    fft256<real, true, false>(v, buf, tw, lane);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const cplx<real> z = buf[slot(lane + 64 * r)];
-        even[r] = z.re;
-        odd[r] = z.im;
+        even[r] = v[r].re;
+        odd[r] = v[r].im;
     }
-    wave_lds_fence();
+    wave_lds_fence();  // the last pass's reads stay before the caller's next writes
 }
 
 }  // namespace pesq
