@@ -343,14 +343,15 @@ def test_graft_entry_exposes_build_and_smoke():
 #: pass.  The variants are chosen by grid size: lane states are stored for
 #: grids of up to 8192 scan wavefronts and recomputed above; the block prefix
 #: is fused into the output pass for rows of up to 128 blocks; the STFT and
-#: chain kernels of grids above 512 workgroups take four frames per wavefront.
+#: chain kernels of grids above 512 chain tiles take four frames per wavefront
+#: (the STFT backward two).
 VARIANTS = {
     # BASELINE c2: 16 rows x 125 blocks, 8 x 32 tiles
     (8, 128000, 2): (
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, true>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
-        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float>",
+        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, true>"],
     ),
@@ -359,7 +360,7 @@ VARIANTS = {
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
          "stft_fwd_kernel<float, true, 8>", "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
-        ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float>",
+        ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float, 2>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
     ),
@@ -369,7 +370,7 @@ VARIANTS = {
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, false>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeFwdMode, false, false>",
          "stft_fwd_kernel<float, true, 8>", "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
-        ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float>",
+        ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float, 2>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, false>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, false, false>"],
     ),
@@ -378,7 +379,7 @@ VARIANTS = {
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, true>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
-        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float>",
+        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, true>"],
     ),

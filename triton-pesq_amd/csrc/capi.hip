@@ -200,6 +200,13 @@ extern "C" int pesq_model_table_pack(const pesq_model_constants *c, void *out) {
     for (int m = 0; m < kHalf; ++m) {
         t->tw256[m] = make_double2(std::cos(two_pi * m / 256.0), -std::sin(two_pi * m / 256.0));
         t->tw512[m] = make_double2(std::cos(two_pi * m / 512.0), -std::sin(two_pi * m / 512.0));
+        t->tw512_f[m] = make_float2(static_cast<float>(t->tw512[m].x),
+                                    static_cast<float>(t->tw512[m].y));
+    }
+    for (int i = 0; i < kPassTwiddles; ++i) {
+        t->tw_pass[i] = pass_twiddle_entry(t->tw256, i);
+        t->tw_pass_f[i] = make_float2(static_cast<float>(t->tw_pass[i].x),
+                                      static_cast<float>(t->tw_pass[i].y));
     }
     std::memcpy(t->window, c->window, sizeof(t->window));
 

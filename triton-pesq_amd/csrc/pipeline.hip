@@ -394,8 +394,8 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
     TW tw;
     if constexpr (kLean) {
         for (int i = threadIdx.x; i < kNfft; i += kWave * kWaves) {
-            if (i < kPassTwiddles) lds_pass[i] = to_vec2<real>(pass_twiddle_entry(t.tw256, i));
-            if (i < kHalf) lds_tw512[i] = to_vec2<real>(t.tw512[i]);
+            if (i < kPassTwiddles) lds_pass[i] = StagedTwiddles<real>::pass(t)[i];
+            if (i < kHalf) lds_tw512[i] = StagedTwiddles<real>::fold(t)[i];
             lds_win[i] = t.window[i];
         }
         __syncthreads();
@@ -1038,16 +1038,22 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
 }
 
 // ---------------------------------------------------------------------------
-// 7. STFT backward per (grad row, 7 hop blocks)
+// 7. STFT backward per (grad row, kBwdWaves kFPW - 1 hop blocks)
 // ---------------------------------------------------------------------------
 
-template <typename real>
-__global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs a) {
-    __shared__ cplx<real> fftbuf[kBwdFrames][kHalf];
-    __shared__ float contrib[kBwdFrames][kNfft];
-    __shared__ double gpart[kBwdFrames][kBands];
-    __shared__ float gband[kBwdFrames][kBands];
-    __shared__ double scratch[kBwdFrames];
+// kFPW frames per wavefront: wavefront w transforms the workgroup's frames w,
+// w + kBwdWaves, ...  (1 for small grids; 2 for large ones, which halves the
+// per workgroup table staging and band sums per frame and the frames shared
+// by two workgroups).  The sums are taken in the same order either way.
+template <typename real, int kFPW>
+__global__ void __launch_bounds__(kWave *kBwdWaves, 5) stft_bwd_kernel(PipeArgs a) {
+    constexpr int kFrames = kBwdWaves * kFPW;  // frames per workgroup
+    constexpr int kHops = kFrames - 1;         // output hop blocks per workgroup
+    __shared__ cplx<real> fftbuf[kBwdWaves][kHalf];
+    __shared__ float contrib[kFrames][kNfft];
+    __shared__ double gpart[kBwdWaves][kBands];
+    __shared__ float gband[kBwdWaves][kBands];
+    __shared__ double scratch[kBwdWaves];
     // the twiddle tables, window and bin-to-band map, staged once per
     // workgroup (both FFTs of every frame read them)
     using T2 = typename Vec2<real>::type;
@@ -1064,74 +1070,85 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
     const bool is_ref = row < L.batch;
     const int wave = wave_index();
     const int lane = threadIdx.x % kWave;
-    const int64_t j0 = int64_t(ht) * kBwdHops;   // first output hop block
+    const int64_t j0 = int64_t(ht) * kHops;      // first output hop block
 
-    // this wavefront's frame: samples and band data are requested first
-    const int64_t frame = j0 - 1 + wave;
-    const bool live = frame >= 0 && frame < L.frames;
-    const int64_t fc = frame < 0 ? 0 : (frame >= L.frames ? L.frames - 1 : frame);
+    // this wavefront's frames: samples and band data are requested first
     const float *p = region<float>(a.ws, L.p) + int64_t(row) * L.len;
-    float smp[8];
-    load_frame(p, fc * kHop, L.len, lane, smp);
     const int band_l = lane < kBands ? lane : kBands - 1;
-    const int64_t fo = fc * kBands;
-    const float bk_v = region<float>(a.ws, L.bark)[int64_t(row) * L.frames * kBands + fo + band_l];
-    const float gbk_v = region<float>(a.bw, L.gbark)[int64_t(row) * L.frames * kBands + fo + band_l];
-    const float keep = region<float>(a.ws, L.keep)[int64_t(item) * L.frames + fc];
+    float smp[kFPW][8], bk_v[kFPW], gbk_v[kFPW], keep[kFPW];
+#pragma unroll
+    for (int f = 0; f < kFPW; ++f) {
+        const int64_t frame = j0 - 1 + wave + kBwdWaves * f;
+        const int64_t fc = frame < 0 ? 0 : (frame >= L.frames ? L.frames - 1 : frame);
+        load_frame(p, fc * kHop, L.len, lane, smp[f]);
+        const int64_t fo = fc * kBands;
+        bk_v[f] = region<float>(a.ws, L.bark)[int64_t(row) * L.frames * kBands + fo + band_l];
+        gbk_v[f] = region<float>(a.bw, L.gbark)[int64_t(row) * L.frames * kBands + fo + band_l];
+        keep[f] = region<float>(a.ws, L.keep)[int64_t(item) * L.frames + fc];
+    }
 
     // adjoint of the band power ratio and its clamp, then of the mean band
-    // powers: wavefront w sums the band partials of tiles w, w + kBwdFrames, ...
+    // powers: wavefront w sums the band partials of tiles w, w + kBwdWaves, ...
     // and every wavefront adds the partial sums in wavefront order
     const double *grp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
-    if (lane < kBands) gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kBwdFrames, lane, kBands);
-    for (int k = threadIdx.x; k < kNfft; k += kWave * kBwdFrames) {
-        if (k < kPassTwiddles) lds_pass[k] = to_vec2<real>(pass_twiddle_entry(t.tw256, k));
+    if (lane < kBands) gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kBwdWaves, lane, kBands);
+    for (int k = threadIdx.x; k < kNfft; k += kWave * kBwdWaves) {
+        if (k < kPassTwiddles) lds_pass[k] = StagedTwiddles<real>::pass(t)[k];
         if (k < kHalf) {
-            lds_tw512[k] = to_vec2<real>(t.tw512[k]);
+            lds_tw512[k] = StagedTwiddles<real>::fold(t)[k];
             lds_bin_band[k] = t.bin_band[k];
         }
         lds_win[k] = t.window[k];
     }
     __syncthreads();
-    double gm = 0.0;
+    double gm = 0.0, th100 = 0.0, corr = 0.0;
     if (lane < kBands) {
         double g = 0.0;
-        for (int w = 0; w < kBwdFrames; ++w) g += gpart[w][lane];
+        for (int w = 0; w < kBwdWaves; ++w) g += gpart[w][lane];
         const double ratio = band_array(a, kRatio)[item * kBands + lane];
         const double mref = band_array(a, kMref)[item * kBands + lane];
         const double gr = (ratio >= 0.01 && ratio <= 100.0) ? g : 0.0;
         const double inv = 1.0 / (mref + 1000.0);
         gm = (is_ref ? -gr * ratio * inv : gr * inv) / static_cast<double>(L.frames);
+        th100 = 100.0 * t.threshs[lane];
+        corr = t.corr[lane];
     }
 
     const double scale = region<double>(a.ws, L.rowconst)[int64_t(row) * 4 + 2];
+    const real s = static_cast<real>(scale) * real(0.5);  // the transform returns 2 X
     cplx<real> *buf = fftbuf[wave];
-    if (live) {
-        // twiddles read per pass from LDS (fewer live registers: five
-        // wavefronts per SIMD)
-        const LdsTwiddles<real> tw{lds_pass, lds_tw512, lane};
-        float win[8];
-        int bin_band[4];
+    // twiddles read per pass from LDS (fewer live registers: five wavefronts
+    // per SIMD)
+    const LdsTwiddles<real> tw{lds_pass, lds_tw512, lane};
+    float win[8];
+    int bin_band[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            win[2 * r] = lds_win[2 * (lane + 64 * r)];
-            win[2 * r + 1] = lds_win[2 * (lane + 64 * r) + 1];
-            bin_band[r] = lds_bin_band[lane + 64 * r];
+    for (int r = 0; r < 4; ++r) {
+        win[2 * r] = lds_win[2 * (lane + 64 * r)];
+        win[2 * r + 1] = lds_win[2 * (lane + 64 * r) + 1];
+        bin_band[r] = lds_bin_band[lane + 64 * r];
+    }
+#pragma unroll
+    for (int f = 0; f < kFPW; ++f) {
+        const int local = wave + kBwdWaves * f;
+        const int64_t frame = j0 - 1 + local;
+        if (frame < 0 || frame >= L.frames) {
+            for (int k = lane; k < kNfft; k += kWave) contrib[local][k] = 0.0f;
+            continue;
         }
         if (lane < kBands) {
-            double g = gbk_v;
-            if (keep != 0.0f && static_cast<double>(bk_v) > 100.0 * t.threshs[lane]) g += gm;
-            gband[wave][lane] = static_cast<float>(g * t.corr[lane]);
+            double g = gbk_v[f];
+            if (keep[f] != 0.0f && static_cast<double>(bk_v[f]) > th100) g += gm;
+            gband[wave][lane] = static_cast<float>(g * corr);
         }
         wave_lds_fence();
         auto u = [&](int k) -> real {
-            const int i = 2 * (k >> 7) + (k & 1);
-            return static_cast<real>(smp[i]) * static_cast<real>(win[i]);
+            const int idx = 2 * (k >> 7) + (k & 1);
+            return static_cast<real>(smp[f][idx]) * static_cast<real>(win[idx]);
         };
         cplx<real> x[4];
         frame_spectrum<real, true>(u, x, buf, tw, lane);
         cplx<real> v[4];
-        const real s = static_cast<real>(scale) * real(0.5);  // x holds 2 X
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int band = bin_band[r];
@@ -1143,18 +1160,17 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int n = lane + 64 * r;
-            contrib[wave][2 * n] = static_cast<float>(ev[r] * static_cast<real>(win[2 * r]));
-            contrib[wave][2 * n + 1] = static_cast<float>(od[r] * static_cast<real>(win[2 * r + 1]));
+            contrib[local][2 * n] = static_cast<float>(ev[r] * static_cast<real>(win[2 * r]));
+            contrib[local][2 * n + 1] = static_cast<float>(od[r] * static_cast<real>(win[2 * r + 1]));
         }
-    } else {
-        for (int k = lane; k < kNfft; k += kWave) contrib[wave][k] = 0.0f;
+        wave_lds_fence();  // gband and the frame buffer are reused by the next frame
     }
     __syncthreads();
 
     // overlap-add: hop block j0 + q receives frames j0 + q - 1 (second half) and j0 + q
     float *gp_out = region<float>(a.bw, L.gp) + int64_t(i) * L.len;
     double acc = 0.0;
-    for (int k = threadIdx.x; k < kBwdHops * kHop; k += blockDim.x) {
+    for (int k = threadIdx.x; k < kHops * kHop; k += blockDim.x) {
         const int q = k / kHop, m = k % kHop;
         const int64_t n = (j0 + q) * kHop + m;
         if (n >= L.len) continue;
@@ -1166,9 +1182,9 @@ __global__ void __launch_bounds__(kWave *kBwdFrames, 5) stft_bwd_kernel(PipeArgs
     if (lane == 0) scratch[wave] = acc;
     __syncthreads();
     if (threadIdx.x == 0) {
-        double s = 0.0;
-        for (int w = 0; w < kBwdFrames; ++w) s += scratch[w];
-        region<double>(a.bw, L.spart)[int64_t(i) * L.nhoptile + ht] = s;
+        double sum = 0.0;
+        for (int w = 0; w < kBwdWaves; ++w) sum += scratch[w];
+        region<double>(a.bw, L.spart)[int64_t(i) * L.nhoptile + ht] = sum;
     }
 }
 
@@ -1418,18 +1434,18 @@ using StftLeanReal = PESQ_STFT_LEAN_REAL;
 // 5e-7.
 using StftBwdReal = float;
 
-// Chain launches: up to about two workgroups per CU of the 256 CU MI355X the
-// kernels are latency bound and run one frame (backward) or two (forward) per
-// wavefront; larger grids run four frames per wavefront (measured best at
-// BASELINE c2 and c5 respectively).  The results are the same either way.
-constexpr unsigned kChainWideGrid = 512;
+// Chain launches: up to about two workgroups per CU of the 256 CU MI355X
+// (kWideTiles chain tiles) the kernels are latency bound and run one frame
+// (backward) or two (forward) per wavefront; larger grids run four frames per
+// wavefront (measured best at BASELINE c2 and c5 respectively).  The results
+// are the same either way.
 
 // The kernel variants the pipeline launches for one shape.  Every launch
 // below and pesq_pipeline_kernels read this one plan, so the variants a test
 // asks about are the ones that run.
 struct PipePlan {
     ScanPlan fwd_scan, bwd_scan;
-    bool stft_lean;      // stft_fwd_kernel<.., true>: grids above kChainWideGrid
+    bool stft_lean;      // stft_fwd_kernel<.., true>: grids above kWideTiles
     int chain_fwd_waves, chain_bwd_waves;
     int chain_bpl;       // bands per lane: 1 up to 64 bands, 2 up to 128
 };
@@ -1439,7 +1455,7 @@ static PipePlan pipe_plan(const PipeLayout &L) {
     P.fwd_scan = scan_plan(L.rows, L.nblk);
     P.bwd_scan = scan_plan(L.nrg, L.nblk);
     const int64_t grid = L.batch * L.ntile;
-    const bool wide = grid > kChainWideGrid;
+    const bool wide = grid > kWideTiles;
     P.stft_lean = wide;
     // Up to 64 bands a lane holds one band; 65 .. 128 bands take two per lane
     // (band lane + 64), with 4 wavefronts per workgroup for the larger
@@ -1546,7 +1562,7 @@ extern "C" int pesq_pipeline_kernels(int64_t batch, int64_t len, int grad_mask, 
     } else {
         out += "chain_bwd_kernel<" + std::to_string(P.chain_bwd_waves) + ", " +
                std::to_string(P.chain_bpl) + ">;";
-        out += std::string("stft_bwd_kernel<") + bwd_real + ">;";
+        out += std::string("stft_bwd_kernel<") + bwd_real + ", " + std::to_string(L.bwd_fpw) + ">;";
         scan_kernel_names(P.bwd_scan, "PipeBwdMode", out);
     }
     out.pop_back();  // the last ';'
@@ -1668,9 +1684,14 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
         PESQ_CHECK_LAUNCH("pipeline chain backward");
     }
     if (stages & 2u) {
-        hipLaunchKernelGGL(stft_bwd_kernel<StftBwdReal>,
-                           dim3(static_cast<unsigned>(L.nrg * L.nhoptile)),
-                           dim3(kWave * kBwdFrames), 0, stream, a);
+        const dim3 grid(static_cast<unsigned>(L.nrg * L.nhoptile));
+        if (L.bwd_fpw == 2) {
+            hipLaunchKernelGGL((stft_bwd_kernel<StftBwdReal, 2>), grid, dim3(kWave * kBwdWaves), 0,
+                               stream, a);
+        } else {
+            hipLaunchKernelGGL((stft_bwd_kernel<StftBwdReal, 1>), grid, dim3(kWave * kBwdWaves), 0,
+                               stream, a);
+        }
         PESQ_CHECK_LAUNCH("pipeline stft backward");
     }
 

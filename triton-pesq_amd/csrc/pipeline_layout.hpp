@@ -13,8 +13,15 @@ constexpr int kPowerSections = 5;  // order 10 band pass, parallel form
 constexpr int kPreSections = 1;    // pre-emphasis biquad
 constexpr int kPipeSections = kPowerSections + kPreSections;  // scanned in one pass
 constexpr int kTile = 16;          // frames per workgroup of the STFT / chain kernels
-constexpr int kBwdFrames = 8;      // frames per workgroup of the STFT backward
+constexpr int kBwdFrames = 8;      // frames per workgroup of the plain STFT backward
 constexpr int kBwdHops = kBwdFrames - 1;  // output hop blocks per such workgroup
+constexpr int kBwdWaves = 8;       // wavefronts per workgroup of the fused STFT backward
+// Grids of more chain tiles (batch x ntile) than this are throughput bound:
+// the kernels take their wide variants (more frames per wavefront).
+#ifndef PESQ_WIDE_TILES
+#define PESQ_WIDE_TILES 512
+#endif
+constexpr int64_t kWideTiles = PESQ_WIDE_TILES;
 constexpr int kWin = 20;           // PSQM window (frames)
 constexpr int kStride = 10;        // PSQM stride (frames)
 
@@ -33,6 +40,7 @@ struct PipeLayout {
     int grad_mask = 0;
     int nb = kBands;            // Bark bands (the stand-alone chain takes 1 .. 128)
     int loud_store = 0;         // the forward writes the `loud` region (a backward follows)
+    int bwd_fpw = 1;            // frames per wavefront of the fused STFT backward (1 or 2)
 
     // forward workspace
     size_t aggr = 0, energy = 0, p = 0, f = 0, rowconst = 0, bark = 0, keep = 0;
@@ -57,7 +65,8 @@ struct PipeLayout {
         frames = frames_for(n);
         nblk = cdiv(n, kBlockSpan);
         ntile = cdiv(frames, kTile);
-        nhoptile = cdiv(cdiv(n, kHop), kBwdHops);
+        bwd_fpw = b * ntile > kWideTiles ? 2 : 1;
+        nhoptile = cdiv(cdiv(n, kHop), kBwdWaves * bwd_fpw - 1);
         nwin = frames >= kWin ? (frames - kWin) / kStride + 1 : 0;
         row0 = (mask & PESQ_GRAD_REF) ? 0 : b;
         nrg = mask == (PESQ_GRAD_REF | PESQ_GRAD_DEG) ? 2 * b : (mask ? b : 0);

@@ -175,12 +175,12 @@ struct LazyTwiddles {
 //   pass[pass_offset(p) + (r - 1) ns + k] = e^{-2 pi i k r / (4 ns)}, ns = 4^p
 //   fold[f]                               = e^{-2 pi i f / 512}
 constexpr int kPassTwiddles = 3 * (4 + 16 + 64);
-__device__ __forceinline__ constexpr int pass_offset(int p) {
+__host__ __device__ __forceinline__ constexpr int pass_offset(int p) {
     return p == 1 ? 0 : (p == 2 ? 3 * 4 : 3 * (4 + 16));
 }
 
 // entry i (0 <= i < kPassTwiddles) of the per pass table, from the 256-point table
-__device__ __forceinline__ double2 pass_twiddle_entry(const double2 *tw256, int i) {
+__host__ __device__ __forceinline__ double2 pass_twiddle_entry(const double2 *tw256, int i) {
     const int p = i < pass_offset(2) ? 1 : (i < pass_offset(3) ? 2 : 3);
     const int ns = 1 << (2 * p);
     const int j = i - pass_offset(p);

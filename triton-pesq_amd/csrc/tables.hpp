@@ -14,6 +14,12 @@ struct ModelTable {
     IirTable iir;                 // A = level alignment band pass, B = pre-emphasis
     double2 tw256[kHalf];         // e^{-2 pi i m / 256}
     double2 tw512[kHalf];         // e^{-2 pi i f / 512}
+    // the twiddles in the layouts the STFT kernels stage in LDS, in both
+    // arithmetic precisions: per (pass, r, k) (pass_twiddle_entry) and the
+    // fold's tw512 in float32
+    double2 tw_pass[kPassTwiddles];
+    float2 tw_pass_f[kPassTwiddles];
+    float2 tw512_f[kHalf];
     float window[kNfft];          // analysis window, centred in n_fft taps
     int32_t band_start[kBands];   // first bin of band i
     int32_t band_end[kBands];     // one past the last bin of band i
@@ -30,6 +36,20 @@ struct ModelTable {
     int32_t n_fft;
     int32_t hop;
     int32_t pad;
+};
+
+// The staged twiddle tables of ModelTable in the arithmetic's precision.
+template <typename real>
+struct StagedTwiddles;
+template <>
+struct StagedTwiddles<float> {
+    static __device__ __forceinline__ const float2 *pass(const ModelTable &t) { return t.tw_pass_f; }
+    static __device__ __forceinline__ const float2 *fold(const ModelTable &t) { return t.tw512_f; }
+};
+template <>
+struct StagedTwiddles<double> {
+    static __device__ __forceinline__ const double2 *pass(const ModelTable &t) { return t.tw_pass; }
+    static __device__ __forceinline__ const double2 *fold(const ModelTable &t) { return t.tw512; }
 };
 
 }  // namespace pesq
