@@ -97,6 +97,15 @@ __device__ __forceinline__ double wave_inclusive_scan(double v) {
     return v;
 }
 
+// Ordering of LDS accesses within one wavefront: the accesses of a wavefront
+// complete in program order, so when its lanes only exchange data among
+// themselves a compiler level barrier between the write and the read phases
+// is all the ordering needed.
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
 // v of the previous lane (0 in lane 0): DPP wave_shr:1
 __device__ __forceinline__ double wave_shift_up(double v) { return dpp_move64<0x138, 0xF>(v); }
 

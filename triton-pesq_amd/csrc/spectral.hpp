@@ -74,14 +74,6 @@ __device__ __forceinline__ void dft4(cplx<real> (&v)[4]) {
 // all 16 groups and keeps the unit stride reads conflict free.
 __device__ __forceinline__ int slot(int i) { return i ^ (((i >> 4) & 3) * 5); }
 
-// The wavefront's lanes only touch their own LDS buffer; LDS accesses of one
-// wavefront complete in program order, so a compiler level barrier between
-// the read and the write phases of a pass is all the ordering needed.
-__device__ __forceinline__ void wave_lds_fence() {
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-}
-
 // Power of the band [lo, hi) of every lane from the 256 bins p[0 .. 255] of
 // the wave's LDS buffer, through a float64 prefix sum: lane l adds bins
 // 4 l .. 4 l + 3 in order, a wave scan turns the lane totals into
