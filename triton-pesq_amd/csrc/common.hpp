@@ -106,6 +106,40 @@ __device__ __forceinline__ void wave_lds_fence() {
     __builtin_amdgcn_wave_barrier();
 }
 
+// Sums over the 64 lanes of K values per lane, through wave-private LDS
+// (`red`: K rows of kWave + 4 doubles, so that the 16 lanes of an LDS cycle
+// read distinct banks): lane 4 j + q adds value j of lanes q, q + 4, ...,
+// q + 60 in that order and a quad DPP sum gives (p0 + p1) + (p2 + p3).  Sum j
+// is returned in lanes 4 j .. 4 j + 3 (0 in lanes 4 K and above).  About 20
+// VALU operations for all K sums, against some 20 per sum for a DPP tree.
+// All 64 lanes must be active; `red` is free again when this returns.
+template <int K>
+__device__ __forceinline__ double wave_sums_lds(const double (&v)[K], double *red, int lane) {
+    constexpr int kRow = kWave + 4;
+    static_assert(4 * K <= kWave, "four lanes per sum");
+#pragma unroll
+    for (int j = 0; j < K; ++j) red[j * kRow + lane] = v[j];
+    wave_lds_fence();
+    const int j = lane / 4, q = lane % 4;
+    double part = 0.0;
+    if (j < K) {
+        const double *src = red + j * kRow + q;
+        part = src[0];
+#pragma unroll
+        for (int i = 1; i < kWave / 4; ++i) part += src[4 * i];
+    }
+    wave_lds_fence();
+    part += dpp_move64<0xB1, 0xF>(part);  // quad_perm [1, 0, 3, 2]: + lane ^ 1
+    part += dpp_move64<0x4E, 0xF>(part);  // quad_perm [2, 3, 0, 1]: + lane ^ 2
+    return part;
+}
+
+// LDS doubles wave_sums_lds<K> needs per wavefront
+template <int K>
+constexpr int wave_sums_lds_doubles() {
+    return K * (kWave + 4);
+}
+
 // v of the previous lane (0 in lane 0): DPP wave_shr:1
 __device__ __forceinline__ double wave_shift_up(double v) { return dpp_move64<0x138, 0xF>(v); }
 

@@ -570,38 +570,25 @@ __device__ __forceinline__ void output_run(const Mode &m, const Coeffs<0, NA, Mo
 // The block's end state from a zero start state, when no lane state is
 // needed: sum over the lanes c of A^(kChunk (63 - c)) e_c, e_c the lane's chunk
 // end state from zero (s), instead of the in-wave scan (which also gives every
-// lane's start state).  The 2 NS weighted components of the 64 lanes go to LDS;
-// lane 4 j + q adds component j's lanes q, q + 4, ..., q + 60 in that order and
-// a quad DPP sum gives (p0 + p1) + (p2 + p3) in lane 4 j, which stores it at
-// dst[j / 2 section stride + j % 2] (dst: section 0 of this block, sections
-// nblk * 2 doubles apart).  A row of the LDS array is kWave + 4 doubles, so the
-// 16 lanes of an LDS cycle read distinct banks.
+// lane's start state); component j (section j / 2) is summed in LDS by
+// wave_sums_lds and stored by lane 4 j at dst[j / 2 section stride + j % 2]
+// (dst: section 0 of this block, sections nblk * 2 doubles apart).
 template <int NS, class BP>
 __device__ __forceinline__ void block_end_state(const IirTable &t, BP &s, double *dst, int nblk,
                                                 int lane) {
-    constexpr int kRow = kWave + 4;
     constexpr int kComps = 2 * NS;
-    static_assert(4 * kComps <= kWave, "four lanes per component");
-    __shared__ double red[kComps * kRow];
+    __shared__ double red[wave_sums_lds_doubles<kComps>()];
+    double w[kComps];
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
         const double *lp = t.lane_pw[k][kWave - 1 - lane];
         const double u = s.u(k), v = s.v(k);
-        red[(2 * k) * kRow + lane] = fma(lp[0], u, lp[1] * v);
-        red[(2 * k + 1) * kRow + lane] = fma(lp[2], u, lp[3] * v);
+        w[2 * k] = fma(lp[0], u, lp[1] * v);
+        w[2 * k + 1] = fma(lp[2], u, lp[3] * v);
     }
-    wave_lds_fence();
-    const int comp = lane / 4, q = lane % 4;
-    double part = 0.0;
-    if (comp < kComps) {
-        const double *src = red + comp * kRow + q;
-        part = src[0];
-#pragma unroll
-        for (int i = 1; i < kWave / 4; ++i) part += src[4 * i];
-    }
-    part += dpp_move64<0xB1, 0xF>(part);  // quad_perm [1, 0, 3, 2]: + the partner lane ^ 1
-    part += dpp_move64<0x4E, 0xF>(part);  // quad_perm [2, 3, 0, 1]: + the pair lane ^ 2
-    if (q == 0 && comp < kComps) dst[int64_t(comp / 2) * nblk * 2 + comp % 2] = part;
+    const double sum = wave_sums_lds(w, red, lane);
+    const int comp = lane / 4;
+    if (lane % 4 == 0 && comp < kComps) dst[int64_t(comp / 2) * nblk * 2 + comp % 2] = sum;
 }
 
 template <int NA, int NB, class Mode, bool kLaneStates>

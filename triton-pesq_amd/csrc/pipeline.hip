@@ -518,6 +518,7 @@ template <int kWaves, int kBPL>
 __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
     constexpr int kPer = kTile / kWaves;  // frames per wavefront
     __shared__ double part[2][kChainSlices][kWave * kBPL];
+    __shared__ double red_lds[kWaves][wave_sums_lds_doubles<2 * (kPer + 1)>()];
 
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
@@ -620,8 +621,9 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
         }
     }
     // per frame totals of the audible energies; slot q is frame f0 - 1 + q
-    // (a lane adds its bands, then the lanes are summed)
-    double taer[kPer + 1], tad[kPer + 1];
+    // (a lane adds its bands, then the lanes are summed, all slots together)
+    double *red = red_lds[wave];
+    double tv[2 * (kPer + 1)];
 #pragma unroll
     for (int q = 0; q <= kPer; ++q) {
         const int64_t frame = f0 - 1 + q;
@@ -637,31 +639,30 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
             ar = k == 0 ? xr : ar + xr;  // a lane's first band starts the sum
             ad = k == 0 ? xd : ad + xd;
         }
-        taer[q] = wave_sum(ar);
-        tad[q] = wave_sum(ad);
+        tv[2 * q] = ar;
+        tv[2 * q + 1] = ad;
     }
+    // totals of slot q (taer, tad) in lanes 8 q .. 8 q + 3 and 8 q + 4 .. 8 q + 7
+    const double tsum = wave_sums_lds(tv, red, lane);
 
     // per frame quantities of the wavefront's frames f0 - 1 .. f0 + kPer - 1,
-    // frame slot q in lane q (the totals are the same in every lane), read
-    // back per frame: the unsmoothed frame ratio (taer + 5e3) / (tad + 5e3),
-    // h = ((taer + 1e5) / 1e7)^0.04 and 1 / h
-    double t_lane = taer[0], d_lane = tad[0];
-#pragma unroll
-    for (int q = 1; q <= kPer; ++q) {
-        t_lane = lane == q ? taer[q] : t_lane;
-        d_lane = lane == q ? tad[q] : d_lane;
-    }
+    // frame slot q in lane q, read back per frame: the unsmoothed frame ratio
+    // (taer + 5e3) / (tad + 5e3), h = ((taer + 1e5) / 1e7)^0.04 and 1 / h
+    const int slot = lane <= kPer ? lane : 0;
+    const double t_lane = shfl(tsum, 8 * slot);
+    const double d_lane = shfl(tsum, 8 * slot + 4);
     const double fpr0_lane = (t_lane + 5e3) / (d_lane + 5e3);
     const double h_lane = exp_chain(0.04 * log_ratio_refined(t_lane + 1e5, 1e7));
     const double inv_h_lane = 1.0 / h_lane;
+    const double fpr0_prev_lane = wave_shift_up(fpr0_lane);  // slot q - 1 in lane q
 
+    double vy[2 * kPer];  // per lane terms of the weighted norms of each frame
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
+        vy[2 * q] = vy[2 * q + 1] = 0.0;
         const int64_t frame = f0 + q;
-        if (frame >= L.frames) break;
+        if (frame >= L.frames) continue;
         const double fpr0 = read_lane(fpr0_lane, q + 1);
-        const double h = read_lane(h_lane, q + 1);
-        const double inv_h = read_lane(inv_h_lane, q + 1);
         const double fpr1 = frame > 0 ? fpr0 * 0.8 + read_lane(fpr0_lane, q) * 0.2 : fpr0;
         const double fpr = fmin(fmax(fpr1, 3e-4), 5.0);
 
@@ -695,20 +696,30 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
             v2 = k == 0 ? xv : v2 + xv;
             ya = k == 0 ? xa : ya + xa;
         }
-        const double symm_raw = W * sqrt(wave_sum(v2));
-        const double asymm_raw = W * wave_sum(ya);
-        if (lane == 0) {
-            const int64_t o = int64_t(item) * L.frames + frame;
-            frame_array(a, kTaer)[o] = taer[q + 1];
-            frame_array(a, kTad)[o] = tad[q + 1];
-            frame_array(a, kFpr0)[o] = fpr0;
-            frame_array(a, kFpr1)[o] = fpr1;
-            frame_array(a, kH)[o] = h;
-            frame_array(a, kSymmRaw)[o] = symm_raw;
-            frame_array(a, kAsymmRaw)[o] = asymm_raw;
-            frame_array(a, kSymm)[o] = fmin(fmax(symm_raw, 1e-20) * inv_h, 45.0);
-            frame_array(a, kAsymm)[o] = fmin(fmax(asymm_raw, 1e-20) * inv_h, 45.0);
-        }
+        vy[2 * q] = v2;
+        vy[2 * q + 1] = ya;
+    }
+    // the norms of frame q in lanes 8 q .. 8 q + 3 (squares) and 8 q + 4 .. + 7
+    const double nsum = wave_sums_lds(vy, red, lane);
+    const int fq = lane >= 1 && lane <= kPer ? lane - 1 : 0;
+    const double v2_lane = shfl(nsum, 8 * fq), ya_lane = shfl(nsum, 8 * fq + 4);
+
+    // the chain state of frame f0 + l - 1, written by lane l = 1 .. kPer
+    const int64_t frame_l = f0 + lane - 1;
+    if (lane >= 1 && lane <= kPer && frame_l < L.frames) {
+        const double fpr1 = frame_l > 0 ? fpr0_lane * 0.8 + fpr0_prev_lane * 0.2 : fpr0_lane;
+        const double symm_raw = W * sqrt(v2_lane);
+        const double asymm_raw = W * ya_lane;
+        const int64_t o = int64_t(item) * L.frames + frame_l;
+        frame_array(a, kTaer)[o] = t_lane;
+        frame_array(a, kTad)[o] = d_lane;
+        frame_array(a, kFpr0)[o] = fpr0_lane;
+        frame_array(a, kFpr1)[o] = fpr1;
+        frame_array(a, kH)[o] = h_lane;
+        frame_array(a, kSymmRaw)[o] = symm_raw;
+        frame_array(a, kAsymmRaw)[o] = asymm_raw;
+        frame_array(a, kSymm)[o] = fmin(fmax(symm_raw, 1e-20) * inv_h_lane, 45.0);
+        frame_array(a, kAsymm)[o] = fmin(fmax(asymm_raw, 1e-20) * inv_h_lane, 45.0);
     }
 }
 
@@ -815,6 +826,7 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
     __shared__ double pl[2][kPsqmSlots];
     __shared__ double gfpr[kSlots], gh[kSlots];
     __shared__ double part[kTile][kLaneBands];  // per frame band partials
+    __shared__ double red_lds[kWaves][wave_sums_lds_doubles<kPer + 1>()];
 
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
@@ -899,6 +911,7 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
 
     // phase 1: adjoint of the per frame distances down to equ_ref / equ_deg
     double g_er[kBPL][kPer + 1], g_ed[kBPL][kPer + 1];
+    double gfv[kPer + 1], ghh[kPer + 1];  // per lane d/d fpr terms, d/d h of each slot
     const int nmine = wave == kWaves - 1 ? kPer + 1 : kPer;
 #pragma unroll
     for (int q = 0; q <= kPer; ++q) {
@@ -906,6 +919,7 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
         const int64_t frame = t0 + local;
 #pragma unroll
         for (int k = 0; k < kBPL; ++k) g_er[k][q] = g_ed[k][q] = 0.0;
+        gfv[q] = ghh[q] = 0.0;
         if (q >= nmine || frame >= L.frames) continue;
 
         const double s_sy = fr[kSymm][local];
@@ -973,10 +987,19 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
             g_ed[k][q] = my_ed;
             gf = k == 0 ? xg : gf + xg;
         }
-        gf = wave_sum(gf);
-        if (lane == 0) {
-            gfpr[local] = gf;
-            gh[local] = g_hh;
+        gfv[q] = gf;
+        ghh[q] = g_hh;
+    }
+    {
+        // the lane sums of all slots together: slot q's in lanes 4 q .. 4 q + 3
+        const double gsum = wave_sums_lds(gfv, red_lds[wave], lane);
+#pragma unroll
+        for (int q = 0; q <= kPer; ++q) {
+            const int local = wave * kPer + q;
+            if (q < nmine && t0 + local < L.frames && lane == 4 * q) {
+                gfpr[local] = gsum;
+                gh[local] = ghh[q];
+            }
         }
     }
     __syncthreads();
