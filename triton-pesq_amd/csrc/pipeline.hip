@@ -1190,16 +1190,35 @@ __global__ void __launch_bounds__(kWave *kBwdWaves, 5) stft_bwd_kernel(PipeArgs 
     }
     __syncthreads();
 
-    // overlap-add: hop block j0 + q receives frames j0 + q - 1 (second half) and j0 + q
+    // overlap-add: hop block j0 + q receives frames j0 + q - 1 (second half) and
+    // j0 + q; four consecutive samples per thread (16-byte LDS reads, global
+    // loads and stores), element by element at the end of the row
     float *gp_out = region<float>(a.bw, L.gp) + int64_t(i) * L.len;
     double acc = 0.0;
-    for (int k = threadIdx.x; k < kHops * kHop; k += blockDim.x) {
+    for (int g4 = threadIdx.x; g4 < kHops * kHop / 4; g4 += blockDim.x) {
+        const int k = 4 * g4;
         const int q = k / kHop, m = k % kHop;
         const int64_t n = (j0 + q) * kHop + m;
         if (n >= L.len) continue;
-        const double g = static_cast<double>(contrib[q][kHop + m]) + static_cast<double>(contrib[q + 1][m]);
-        gp_out[n] = static_cast<float>(g);
-        acc += g * static_cast<double>(p[n]);
+        float lo[4], hi[4], pv[4], out[4];
+        __builtin_memcpy(hi, &contrib[q][kHop + m], sizeof(hi));
+        __builtin_memcpy(lo, &contrib[q + 1][m], sizeof(lo));
+        if (n + 4 <= L.len) {
+            __builtin_memcpy(pv, p + n, sizeof(pv));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const double g = static_cast<double>(hi[e]) + static_cast<double>(lo[e]);
+                out[e] = static_cast<float>(g);
+                acc += g * static_cast<double>(pv[e]);
+            }
+            __builtin_memcpy(gp_out + n, out, sizeof(out));
+        } else {
+            for (int e = 0; e < 4 && n + e < L.len; ++e) {
+                const double g = static_cast<double>(hi[e]) + static_cast<double>(lo[e]);
+                gp_out[n + e] = static_cast<float>(g);
+                acc += g * static_cast<double>(p[n + e]);
+            }
+        }
     }
     acc = wave_sum(acc);
     if (lane == 0) scratch[wave] = acc;
