@@ -76,6 +76,14 @@ static int fill_sections(IirTable &t, int first, const pesq_iir_sections &s, dou
                 g[1] = g1;
             }
         }
+        // block pair powers M^(2 i), M = A^kSpan (level kLevelBlock)
+        {
+            double m[4] = {1.0, 0.0, 0.0, 1.0};
+            for (int i = 0; i < kWave; ++i) {
+                std::memcpy(t.blk_pw2[i][q], m, sizeof(m));
+                mat_mul(t.pw[kLevelBlock + 1][q], m, m);
+            }
+        }
         // lane start powers A^(kChunk lane): product of the levels of the set bits
         for (int lane = 0; lane < kWave; ++lane) {
             double m[4] = {1.0, 0.0, 0.0, 1.0};

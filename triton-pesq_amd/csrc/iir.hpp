@@ -74,6 +74,9 @@ struct IirTable {
     // section's state after the chunk, from a zero state (beta_k: the state
     // increment per unit input, (b1 - a1 b0, b2 - a2 b0))
     double fir[kMaxSections][kChunk][2];
+    // M^(2 i), M = A_k^kSpan the block transfer: the weight of the block pair
+    // (M e_j + e_j+1) 2 i + 2 blocks before a block (block_start_reduce)
+    double blk_pw2[kWave][kMaxSections][4];
 };
 
 // Small grids (those that keep lane states) of rows of up to
@@ -264,12 +267,10 @@ __device__ __forceinline__ void scan_wave_dpp(const Powers &t, Bank<NS> &z, int 
 // the blocks before it (row_aggr, laid out [section][block][2]):
 //     p = sum_{j < blk} M^(blk - 1 - j) e_j,  M = A^kSpan per section.
 // Lane i holds blocks j0 = blk - 128 + 2 i and j0 + 1 (0 before the row
-// start) and combines them as M e_j0 + e_j0+1; the DPP scan steps with the
-// uniform powers M^(2 2^l) then reduce the lanes exactly onto lane 63 (row
-// shifts 1, 2, 4, 8 leave each row's weighted sum in its last lane,
-// row_bcast:15 adds row 2 to lane 63 with M^32 and row_bcast:31 lanes 0..31
-// with M^64; the other lanes hold partial sums).  The loads are issued first
-// so that they overlap the kernel's other loads.
+// start), combines them as M e_j0 + e_j0+1 and carries the pair to the block
+// start with M^(2 (63 - i)) (blk_pw2); the 64 lanes' terms are then summed in
+// LDS (wave_sums_lds, `red`) and every lane reads the sums back.  The loads are
+// issued first so that they overlap the kernel's other loads.
 template <int NS>
 __device__ __forceinline__ void block_start_load(const double *row_aggr, int nblk, int blk,
                                                  int lane, Bank<NS> &e0, Bank<NS> &e1) {
@@ -287,43 +288,45 @@ __device__ __forceinline__ void block_start_load(const double *row_aggr, int nbl
     }
 }
 
-template <int NS, class Powers>
-__device__ __forceinline__ void block_start_reduce(const Powers &t, Bank<NS> &z,
-                                                   const Bank<NS> &e1) {
-    const double *pw[NS];
+// the lane's pair power M^(2 (63 - lane)) of every section, loaded with the
+// block end states (block_start_load) so that its latency overlaps theirs
+template <int NS>
+struct PairPowers {
+    double2 m[NS > 0 ? NS : 1][2];
+
+    __device__ __forceinline__ void load(const IirTable &t, int lane) {
 #pragma unroll
-    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock][k];
-    // z = M e_j0 + e_j0+1
+        for (int k = 0; k < NS; ++k) {
+            const double2 *q = reinterpret_cast<const double2 *>(t.blk_pw2[kWave - 1 - lane][k]);
+            m[k][0] = q[0];
+            m[k][1] = q[1];
+        }
+    }
+};
+
+template <int NS>
+__device__ __forceinline__ void block_start_reduce(const IirTable &t, const PairPowers<NS> &pp,
+                                                   Bank<NS> &z, const Bank<NS> &e1, double *red,
+                                                   int lane) {
+    double w[2 * NS];
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
-        const double *m = pw[k];
-        const double u = z.u[k], v = z.v[k];
-        z.u[k] = fma(m[0], u, fma(m[1], v, e1.u[k]));
-        z.v[k] = fma(m[2], u, fma(m[3], v, e1.v[k]));
+        const double *m = t.pw[kLevelBlock][k];
+        const double u = fma(m[0], z.u[k], fma(m[1], z.v[k], e1.u[k]));
+        const double v = fma(m[2], z.u[k], fma(m[3], z.v[k], e1.v[k]));
+        const double2 q0 = pp.m[k][0], q1 = pp.m[k][1];
+        w[2 * k] = fma(q0.x, u, q0.y * v);
+        w[2 * k + 1] = fma(q1.x, u, q1.y * v);
     }
-#pragma unroll
-    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock + 1][k];
-    dpp_level<0x111, 0xF, 0, NS>(pw, z);  // row_shr:1
-#pragma unroll
-    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock + 2][k];
-    dpp_level<0x112, 0xF, 0, NS>(pw, z);  // row_shr:2
-#pragma unroll
-    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock + 3][k];
-    dpp_level<0x114, 0xF, 0, NS>(pw, z);  // row_shr:4
-#pragma unroll
-    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock + 4][k];
-    dpp_level<0x118, 0xF, 0, NS>(pw, z);  // row_shr:8
-#pragma unroll
-    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock + 5][k];
-    dpp_level<0x142, 0xA, 0, NS>(pw, z);  // row_bcast:15
-#pragma unroll
-    for (int k = 0; k < NS; ++k) pw[k] = t.pw[kLevelBlock + 6][k];
-    dpp_level<0x143, 0xC, 0, NS>(pw, z);  // row_bcast:31
+    const double sum = wave_sums_lds(w, red, lane);  // component j in lane 4 j
+    if (lane % 4 == 0 && lane / 4 < 2 * NS) red[lane / 4] = sum;
+    wave_lds_fence();
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
-        z.u[k] = read_lane(z.u[k], kWave - 1);
-        z.v[k] = read_lane(z.v[k], kWave - 1);
+        z.u[k] = red[2 * k];
+        z.v[k] = red[2 * k + 1];
     }
+    wave_lds_fence();
 }
 
 template <int NA, int NB>
@@ -707,8 +710,10 @@ __global__ void __launch_bounds__(kWave)
     const double *row_aggr = aggr + int64_t(row) * NS * nblk * 2;
     BankPair<NA, NB> p;
     Bank<NS> e0, e1;  // kFusedPrefix: the block aggregates this block starts from
+    PairPowers<NS> pp;
     if constexpr (kFusedPrefix) {
         block_start_load<NS>(row_aggr, nblk, blk, lane, e0, e1);
+        pp.load(*table, lane);
     } else {
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
@@ -734,7 +739,8 @@ __global__ void __launch_bounds__(kWave)
     load_chunk(m, row, j0, len, in);
     const IirTable &t2 = *table;
     if constexpr (kFusedPrefix) {
-        block_start_reduce<NS>(t2, e0, e1);
+        __shared__ double red[wave_sums_lds_doubles<2 * NS>()];
+        block_start_reduce<NS>(t2, pp, e0, e1, red, lane);
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
             p.u(k) = e0.u[k];
