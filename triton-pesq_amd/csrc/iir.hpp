@@ -130,19 +130,6 @@ struct Bank {
     }
 };
 
-// The table pointer through an empty asm statement: loads through the result
-// are issued again instead of being kept live in registers from earlier ones
-// (the coefficients are re-read from the scalar cache for each run).
-// (p must be wave-uniform)
-template <typename T>
-__device__ __forceinline__ const T *reload(const T *p) {
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-    uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
-    asm volatile("" : "+s"(lo), "+s"(hi));
-    return reinterpret_cast<const T *>((uint64_t(hi) << 32) | lo);
-}
-
 // Coefficients of NS sections starting at section S0.  With kB2 the sections
 // are full biquads (z2' = b2 x - a2 y_k, the cascade passes); without it b2 is
 // 0 (the parallel form, whose table packing folds b2 into the direct term).
