@@ -47,7 +47,7 @@ constexpr int kChunk = PESQ_CHUNK;                         // samples per lane
 // the aggregate pass stores every lane's in-block start state and the output
 // pass reads it; larger grids (bandwidth bound) skip that traffic and the
 // output pass repeats the zero state run and the in-wave scan.  Both compute
-// the same states with the same operations.
+// the same states up to float64 rounding.
 // (8192: grids of up to 7504 wavefronts, such as 8 rows of 60 s, gained 1.5 -
 // 4 us from the stored states; 16128, 256 rows of 4 s, was 6 us faster
 // recomputing)
