@@ -101,8 +101,9 @@ def pipeline_region(batch: int, length: int, grad_mask: int, name: str):
 
 def pipeline_forward(ref, deg, table, factor, grad_mask):
     """Run the forward kernels; returns ``([d_symm, d_asymm, mos, loss], workspace)``.
-  The workspace holds the
-    state :func:`pipeline_backward` needs (regions: :func:`pipeline_region`).
+
+    The workspace holds the state :func:`pipeline_backward` needs (regions:
+    :func:`pipeline_region`).
     """
 
     lib = _lib.library()
