@@ -595,7 +595,8 @@ def main(argv=None):
         torch.autograd.grad(loss.sum(), deg)
 
     # HIP graph replay through PesqLossTriton.graphed() (forward and backward
-    # graphs; each call also copies the inputs into the graph's buffers)
+    # graphs replayed by a C++ autograd node; the inputs are the same tensors on
+    # every call, which from the second call on the forward graph reads in place)
     graph_deg = deg.detach().clone().requires_grad_(True)
     graphed = model.graphed(ref, graph_deg)
 

@@ -93,6 +93,7 @@ def _torch_flags():
         "-ltorch_cpu",
         "-ltorch_hip",
         "-ltorch_python",
+        "-lamdhip64",  # the HIP runtime PyTorch loads (graph capture and replay)
         f"-L{OUT_DIR}",
         "-lpesq_hip",
         "-Wl,-rpath,$ORIGIN",

@@ -20,6 +20,7 @@
 #include <c10/hip/HIPStream.h>
 
 #include <array>
+#include <vector>
 #include <stdexcept>
 #include <string>
 
@@ -178,18 +179,10 @@ struct ResampleBank {
     }
 };
 
-// forward: src [rows, n_in] -> [rows, n_other]; adjoint: src [rows, n_out] -> [rows, n_other]
-at::Tensor resample_launch(const at::Tensor &src, int64_t n_other, const ResampleBank &b,
-                           bool forward) {
-    const c10::DeviceGuard guard(src.device());
-    const int64_t rows = src.size(0);
-    const int64_t n_in = forward ? src.size(1) : n_other;
-    const int64_t n_out = forward ? n_other : src.size(1);
-    at::Tensor out = at::empty({rows, n_other}, src.options());
+// forward: x [rows, n_in] -> y [rows, n_out]; adjoint: x [rows, n_out] -> y [rows, n_in]
+void resample_enqueue(const float *x, float *y, int64_t rows, int64_t n_in, int64_t n_out,
+                      const ResampleBank &b, bool forward, hipStream_t stream) {
     const pesq_resample_plan_info &info = b.plan_info();
-    const hipStream_t stream = current_stream(src);
-    const float *x = src.data_ptr<float>();
-    float *y = out.data_ptr<float>();
     const int64_t ntaps = b.kernel.size(1);
     if (forward && info.fwd_span > 0) {
         check(pesq_resample_plan_forward(x, y, rows, n_in, n_out, &info, b.plan.data_ptr(), stream),
@@ -208,6 +201,18 @@ at::Tensor resample_launch(const at::Tensor &src, int64_t n_other, const Resampl
                                      b.orig_step, b.new_step, b.width, ntaps, stream),
               "pesq_resample_backward");
     }
+}
+
+// forward: src [rows, n_in] -> [rows, n_other]; adjoint: src [rows, n_out] -> [rows, n_other]
+at::Tensor resample_launch(const at::Tensor &src, int64_t n_other, const ResampleBank &b,
+                           bool forward) {
+    const c10::DeviceGuard guard(src.device());
+    const int64_t rows = src.size(0);
+    const int64_t n_in = forward ? src.size(1) : n_other;
+    const int64_t n_out = forward ? n_other : src.size(1);
+    at::Tensor out = at::empty({rows, n_other}, src.options());
+    resample_enqueue(src.data_ptr<float>(), out.data_ptr<float>(), rows, n_in, n_out, b, forward,
+                     current_stream(src));
     return out;
 }
 
@@ -246,14 +251,13 @@ variable_list Resample::backward(AutogradContext *ctx, variable_list grads) {
     return {ResampleAdjoint::apply(grads[0].to(at::kFloat), n_in, b), at::Tensor(), at::Tensor()};
 }
 
-at::Tensor resample(const at::Tensor &x, int64_t n_out, const at::Tensor &kernel,
-                    const at::Tensor &tap_lo, const at::Tensor &tap_hi, const at::Tensor &phase_lo,
-                    const at::Tensor &phase_hi, const at::Tensor &plan, const at::Tensor &info,
-                    int64_t orig_step, int64_t new_step, int64_t width) {
-    TORCH_CHECK(x.is_cuda() && x.scalar_type() == at::kFloat && x.dim() == 2 && x.is_contiguous(),
-                "resample: x must be a contiguous [rows, samples] float32 GPU tensor");
+// checks the bank's tensors against a signal on `device` and bundles them
+ResampleBank make_bank(int device, const at::Tensor &kernel, const at::Tensor &tap_lo,
+                       const at::Tensor &tap_hi, const at::Tensor &phase_lo,
+                       const at::Tensor &phase_hi, const at::Tensor &plan, const at::Tensor &info,
+                       int64_t orig_step, int64_t new_step, int64_t width) {
     for (const at::Tensor *t : {&kernel, &tap_lo, &tap_hi, &phase_lo, &phase_hi, &plan})
-        TORCH_CHECK(t->is_cuda() && t->get_device() == x.get_device() && t->is_contiguous(),
+        TORCH_CHECK(t->is_cuda() && t->get_device() == device && t->is_contiguous(),
                     "resample: the filter tables must be contiguous and on the signal's device");
     TORCH_CHECK(kernel.scalar_type() == at::kFloat && kernel.dim() == 2 &&
                     kernel.size(0) == new_step,
@@ -266,7 +270,6 @@ at::Tensor resample(const at::Tensor &x, int64_t n_out, const at::Tensor &kernel
     TORCH_CHECK(!info.is_cuda() && info.scalar_type() == at::kByte && info.is_contiguous() &&
                     info.numel() == static_cast<int64_t>(sizeof(pesq_resample_plan_info)),
                 "resample: info must be the host bytes of pesq_resample_plan_info");
-    TORCH_CHECK(n_out >= 0, "resample: negative output length");
     ResampleBank b;
     b.kernel = kernel;
     b.tap_lo = tap_lo;
@@ -282,11 +285,22 @@ at::Tensor resample(const at::Tensor &x, int64_t n_out, const at::Tensor &kernel
     TORCH_CHECK(pi.orig_step == orig_step && pi.new_step == new_step && pi.width == width &&
                     pi.width_total == kernel.size(1) && plan.numel() >= pi.bytes,
                 "resample: info does not describe this filter bank");
+    return b;
+}
+
+at::Tensor resample(const at::Tensor &x, int64_t n_out, const at::Tensor &kernel,
+                    const at::Tensor &tap_lo, const at::Tensor &tap_hi, const at::Tensor &phase_lo,
+                    const at::Tensor &phase_hi, const at::Tensor &plan, const at::Tensor &info,
+                    int64_t orig_step, int64_t new_step, int64_t width) {
+    TORCH_CHECK(x.is_cuda() && x.scalar_type() == at::kFloat && x.dim() == 2 && x.is_contiguous(),
+                "resample: x must be a contiguous [rows, samples] float32 GPU tensor");
+    TORCH_CHECK(n_out >= 0, "resample: negative output length");
+    const ResampleBank b = make_bank(x.get_device(), kernel, tap_lo, tap_hi, phase_lo, phase_hi,
+                                     plan, info, orig_step, new_step, width);
     return Resample::apply(x, n_out, b);
 }
 
-std::vector<at::Tensor> pipeline(const at::Tensor &ref, const at::Tensor &deg,
-                                 const at::Tensor &table, double factor) {
+void check_pipeline_inputs(const at::Tensor &ref, const at::Tensor &deg, const at::Tensor &table) {
     TORCH_CHECK(ref.is_cuda() && deg.is_cuda() && table.is_cuda(),
                 "pipeline: ref, deg and table must be GPU tensors");
     TORCH_CHECK(ref.get_device() == deg.get_device() && ref.get_device() == table.get_device(),
@@ -301,12 +315,297 @@ std::vector<at::Tensor> pipeline(const at::Tensor &ref, const at::Tensor &deg,
                     table.numel() == static_cast<int64_t>(pesq_model_table_bytes()),
                 "pipeline: table must be the packed model table (uint8, ",
                 pesq_model_table_bytes(), " bytes)");
+}
+
+std::vector<at::Tensor> pipeline(const at::Tensor &ref, const at::Tensor &deg,
+                                 const at::Tensor &table, double factor) {
+    check_pipeline_inputs(ref, deg, table);
     // what Python's ctx.needs_input_grad gives: the inputs autograd will ask for
     const bool grad = torch::autograd::GradMode::is_enabled();
     const int64_t mask = (grad && ref.requires_grad() ? PESQ_GRAD_REF : 0) |
                          (grad && deg.requires_grad() ? PESQ_GRAD_DEG : 0);
     return Pipeline::apply(ref, deg, table, factor, mask);
 }
+
+// ---------------------------------------------------------------------------
+// graphed loss (torch_pesq/triton_ops/loss.py:149-201): the loss of one input
+// shape and one set of requires_grad flags, captured as two HIP graphs over
+// static buffers: the forward (resampling to 16 kHz, pipeline forward) and the
+// backward (pipeline backward, resampler adjoint).  A call copies its inputs
+// into the static ones (unless they are those), replays the forward graph and
+// returns the static loss; the autograd node copies the upstream gradient in,
+// replays the backward graph and returns the static gradients.  As with
+// torch.cuda.make_graphed_callables, which the reference uses, the results
+// alias the static buffers (the next replay overwrites them) and the backward
+// is differentiable once.  The graphs hold the same library calls the eager
+// nodes make, so both give the same bits.
+// ---------------------------------------------------------------------------
+
+void check_hip(hipError_t status, const char *what) {
+    if (status != hipSuccess)
+        throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(status));
+}
+
+struct GraphedLoss : torch::CustomClassHolder {
+    at::Tensor table;
+    double factor = 0.0;
+    int mask = 0;
+    bool resampled = false;
+    ResampleBank bank;
+    std::vector<int64_t> shape;  // of the example inputs, [batch, samples] or [samples]
+    int64_t batch = 0, n_src = 0, n16 = 0;
+    at::Tensor ref_s, deg_s;        // static inputs [batch, n_src]
+    at::Tensor ref16, deg16;        // their 16 kHz rows (the static inputs themselves at 16 kHz)
+    std::array<at::Tensor, 4> out;  // d_symm, d_asymm, mos, loss [batch]
+    at::Tensor ws, scratch;         // forward workspace, backward scratch
+    at::Tensor g_loss;              // upstream gradient of the loss [batch]
+    at::Tensor g_ref16, g_deg16, g_ref, g_deg;
+    hipGraphExec_t fwd = nullptr, bwd = nullptr;  // forward from the static inputs, backward
+    hipStream_t fwd_stream = nullptr, bwd_stream = nullptr;  // of the last replays
+
+    // Forward graphs that read a caller's own input buffers, by address: a
+    // caller passing the same (ref, deg) buffers on two calls in a row (a
+    // resident batch, an allocation the caching allocator hands out again)
+    // gets one captured for them and from then on skips the two input copies.
+    struct Direct {
+        const void *ref, *deg;
+        hipGraphExec_t exec;
+    };
+    static constexpr size_t kDirectGraphs = 4;
+    std::vector<Direct> direct;  // the most recent capture last
+    const void *last_ref = nullptr, *last_deg = nullptr;
+
+    GraphedLoss() = default;
+    GraphedLoss(const GraphedLoss &) = delete;
+    GraphedLoss &operator=(const GraphedLoss &) = delete;
+    ~GraphedLoss() override {
+        // replays still running read the graphs and the static buffers
+        if (fwd_stream) (void)hipStreamSynchronize(fwd_stream);
+        if (bwd_stream) (void)hipStreamSynchronize(bwd_stream);
+        if (fwd) (void)hipGraphExecDestroy(fwd);
+        if (bwd) (void)hipGraphExecDestroy(bwd);
+        for (const Direct &d : direct) (void)hipGraphExecDestroy(d.exec);
+    }
+
+    void enqueue_forward(const float *ref_in, const float *deg_in, hipStream_t stream) const {
+        if (resampled) {
+            resample_enqueue(ref_in, ref16.data_ptr<float>(), batch, n_src, n16, bank, true, stream);
+            resample_enqueue(deg_in, deg16.data_ptr<float>(), batch, n_src, n16, bank, true, stream);
+            ref_in = ref16.data_ptr<float>();
+            deg_in = deg16.data_ptr<float>();
+        }
+        check(pesq_pipeline_forward(ref_in, deg_in, batch, n16, table.data_ptr(), factor, mask,
+                                    out[0].data_ptr<float>(), out[1].data_ptr<float>(),
+                                    out[2].data_ptr<float>(), out[3].data_ptr<float>(),
+                                    ws.data_ptr(), stream),
+              "pesq_pipeline_forward");
+    }
+
+    // the forward graph for a call's inputs (copying them into the static
+    // inputs when it is the static one)
+    hipGraphExec_t forward_graph(const at::Tensor &ref, const at::Tensor &deg, hipStream_t stream) {
+        const void *rp = ref.data_ptr(), *dp = deg.data_ptr();
+        const bool plain = ref.scalar_type() == at::kFloat && deg.scalar_type() == at::kFloat &&
+                           ref.is_contiguous() && deg.is_contiguous() &&
+                           rp != ref_s.data_ptr() && dp != deg_s.data_ptr();
+        const bool repeated = rp == last_ref && dp == last_deg;
+        last_ref = rp;
+        last_deg = dp;
+        if (plain) {
+            for (const Direct &d : direct)
+                if (d.ref == rp && d.deg == dp) return d.exec;
+            if (repeated) {
+                if (direct.size() == kDirectGraphs) {
+                    if (fwd_stream) check_hip(hipStreamSynchronize(fwd_stream), "hipStreamSynchronize");
+                    check_hip(hipGraphExecDestroy(direct.front().exec), "hipGraphExecDestroy");
+                    direct.erase(direct.begin());
+                }
+                const auto *r = static_cast<const float *>(rp);
+                const auto *d = static_cast<const float *>(dp);
+                direct.push_back({rp, dp, capture([&](hipStream_t s) { enqueue_forward(r, d, s); })});
+                return direct.back().exec;
+            }
+        }
+        stage(ref, ref_s, stream);
+        stage(deg, deg_s, stream);
+        return fwd;
+    }
+
+    void enqueue_backward(hipStream_t stream) const {
+        check(pesq_pipeline_backward(nullptr, nullptr, nullptr, g_loss.data_ptr<float>(), batch,
+                                     n16, table.data_ptr(), factor, mask,
+                                     data_or_null<float>(g_ref16), data_or_null<float>(g_deg16),
+                                     ws.data_ptr(), scratch.data_ptr(), stream),
+              "pesq_pipeline_backward");
+        if (resampled) {
+            if (g_ref.defined())
+                resample_enqueue(g_ref16.data_ptr<float>(), g_ref.data_ptr<float>(), batch, n_src,
+                                 n16, bank, false, stream);
+            if (g_deg.defined())
+                resample_enqueue(g_deg16.data_ptr<float>(), g_deg.data_ptr<float>(), batch, n_src,
+                                 n16, bank, false, stream);
+        }
+    }
+
+    // the calls of enqueue(stream) as an executable graph, captured on a
+    // stream of its own (capture records, it does not run anything)
+    template <class F>
+    hipGraphExec_t capture(F &&enqueue) {
+        hipStream_t stream = nullptr;
+        check_hip(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        hipError_t status = hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal);
+        if (status == hipSuccess) {
+            try {
+                enqueue(stream);
+            } catch (...) {
+                (void)hipStreamEndCapture(stream, &graph);
+                if (graph) (void)hipGraphDestroy(graph);
+                (void)hipStreamDestroy(stream);
+                throw;
+            }
+            status = hipStreamEndCapture(stream, &graph);
+        }
+        if (status == hipSuccess) status = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (graph) (void)hipGraphDestroy(graph);
+        (void)hipStreamDestroy(stream);
+        check_hip(status, "capturing the graphed loss");
+        return exec;
+    }
+
+    // copies a call's input into its static buffer
+    void stage(const at::Tensor &src, const at::Tensor &dst, hipStream_t stream) const {
+        if (src.data_ptr() == dst.data_ptr()) return;
+        if (src.scalar_type() == at::kFloat && src.is_contiguous()) {
+            check_hip(hipMemcpyAsync(dst.data_ptr(), src.data_ptr(), dst.nbytes(),
+                                     hipMemcpyDeviceToDevice, stream),
+                      "hipMemcpyAsync");
+        } else {
+            const at::NoGradGuard no_grad;
+            dst.view(src.sizes()).copy_(src);
+        }
+    }
+};
+
+struct GraphedCall : public torch::autograd::Function<GraphedCall> {
+    static at::Tensor forward(AutogradContext *ctx, const at::Tensor &ref, const at::Tensor &deg,
+                              const c10::intrusive_ptr<GraphedLoss> &g) {
+        TORCH_CHECK(ref.defined() && deg.defined() && ref.sizes() == g->shape &&
+                        deg.sizes() == g->shape,
+                    "graphed loss: the inputs must have the shape it was captured for, ",
+                    c10::IntArrayRef(g->shape));
+        TORCH_CHECK(ref.device() == g->ref_s.device() && deg.device() == g->ref_s.device(),
+                    "graphed loss: the inputs must be on ", g->ref_s.device());
+        const c10::DeviceGuard guard(g->ref_s.device());
+        const hipStream_t stream = current_stream(g->ref_s);
+        check_hip(hipGraphLaunch(g->forward_graph(ref, deg, stream), stream), "hipGraphLaunch");
+        g->fwd_stream = stream;
+        ctx->saved_data["graphed"] = c10::IValue::make_capsule(g);
+        ctx->set_materialize_grads(false);
+        return g->out[3].detach();
+    }
+
+    static variable_list backward(AutogradContext *ctx, variable_list grads) {
+        const auto g =
+            c10::static_intrusive_pointer_cast<GraphedLoss>(ctx->saved_data["graphed"].toCapsule());
+        variable_list result(3);  // ref, deg, the graphs
+        if (!grads[0].defined() || g->bwd == nullptr) return result;
+        const c10::DeviceGuard guard(g->g_loss.device());
+        const hipStream_t stream = current_stream(g->g_loss);
+        if (grads[0].data_ptr() != g->g_loss.data_ptr()) {
+            const at::NoGradGuard no_grad;
+            g->g_loss.copy_(grads[0]);
+        }
+        check_hip(hipGraphLaunch(g->bwd, stream), "hipGraphLaunch");
+        g->bwd_stream = stream;
+        if (g->g_ref.defined()) result[0] = g->g_ref.view(g->shape).detach();
+        if (g->g_deg.defined()) result[1] = g->g_deg.view(g->shape).detach();
+        if (torch::autograd::GradMode::is_enabled() && grads[0].requires_grad()) {
+            for (size_t i = 0; i < 2; ++i)
+                if (result[i].defined())
+                    result[i] = OnceDifferentiable::apply(result[i].requires_grad_(true));
+        }
+        return result;
+    }
+};
+
+// the Python object PesqLossTriton.graphed returns
+class GraphedLossCallable {
+  public:
+    // ref, deg: examples of the inputs (their shape and requires_grad flags);
+    // bank: the resampler's (kernel, tap_lo, tap_hi, phase_lo, phase_hi, plan,
+    // info) and steps its (orig_step, new_step, width, output length), both
+    // empty at 16 kHz
+    GraphedLossCallable(const at::Tensor &ref, const at::Tensor &deg, const at::Tensor &table,
+                        double factor, const std::vector<at::Tensor> &bank,
+                        const std::vector<int64_t> &steps) {
+        TORCH_CHECK(ref.dim() >= 1 && ref.dim() <= 2 && ref.sizes() == deg.sizes(),
+                    "graphed loss: ref and deg must be [batch, samples] or [samples] of one shape");
+        TORCH_CHECK(bank.empty() ? steps.empty() : bank.size() == 7 && steps.size() == 4,
+                    "graphed loss: the resampler bank is 7 tensors and 4 sizes");
+        auto g = c10::make_intrusive<GraphedLoss>();
+        g->shape = ref.sizes().vec();
+        g->table = table;
+        g->factor = factor;
+        g->mask = (ref.requires_grad() ? PESQ_GRAD_REF : 0) | (deg.requires_grad() ? PESQ_GRAD_DEG : 0);
+        g->batch = ref.dim() == 2 ? ref.size(0) : 1;
+        g->n_src = ref.size(-1);
+        const c10::DeviceGuard guard(ref.device());
+        const auto f32 = ref.options().dtype(at::kFloat).requires_grad(false);
+        g->ref_s = at::empty({g->batch, g->n_src}, f32);
+        g->deg_s = at::empty({g->batch, g->n_src}, f32);
+        g->resampled = !bank.empty();
+        if (g->resampled) {
+            g->bank = make_bank(ref.get_device(), bank[0], bank[1], bank[2], bank[3], bank[4],
+                                bank[5], bank[6], steps[0], steps[1], steps[2]);
+            g->n16 = steps[3];
+            TORCH_CHECK(g->n16 > 0, "graphed loss: empty signals");
+            g->ref16 = at::empty({g->batch, g->n16}, f32);
+            g->deg16 = at::empty({g->batch, g->n16}, f32);
+        } else {
+            g->n16 = g->n_src;
+            g->ref16 = g->ref_s;
+            g->deg16 = g->deg_s;
+        }
+        check_pipeline_inputs(g->ref16, g->deg16, table);
+        size_t bytes = 0;
+        check(pesq_pipeline_forward_workspace(g->batch, g->n16, g->mask, &bytes),
+              "pesq_pipeline_forward_workspace");
+        g->ws = at::empty({static_cast<int64_t>(bytes)}, f32.dtype(at::kByte));
+        for (at::Tensor &o : g->out) o = at::empty({g->batch}, f32);
+        if (g->mask != 0) {
+            check(pesq_pipeline_backward_workspace(g->batch, g->n16, g->mask, &bytes),
+                  "pesq_pipeline_backward_workspace");
+            g->scratch = at::empty({static_cast<int64_t>(bytes)}, f32.dtype(at::kByte));
+            g->g_loss = at::empty({g->batch}, f32);
+            if (g->mask & PESQ_GRAD_REF) g->g_ref16 = at::empty({g->batch, g->n16}, f32);
+            if (g->mask & PESQ_GRAD_DEG) g->g_deg16 = at::empty({g->batch, g->n16}, f32);
+            if (g->resampled) {
+                if (g->g_ref16.defined()) g->g_ref = at::empty({g->batch, g->n_src}, f32);
+                if (g->g_deg16.defined()) g->g_deg = at::empty({g->batch, g->n_src}, f32);
+            } else {
+                g->g_ref = g->g_ref16;
+                g->g_deg = g->g_deg16;
+            }
+        }
+        // the static buffers are allocated on the current stream; the capture
+        // stream only records
+        GraphedLoss &s = *g;
+        s.fwd = s.capture([&s](hipStream_t stream) {
+            s.enqueue_forward(s.ref_s.data_ptr<float>(), s.deg_s.data_ptr<float>(), stream);
+        });
+        if (s.mask != 0) s.bwd = s.capture([&s](hipStream_t stream) { s.enqueue_backward(stream); });
+        graphed_ = std::move(g);
+    }
+
+    at::Tensor call(const at::Tensor &ref, const at::Tensor &deg) const {
+        return GraphedCall::apply(ref, deg, graphed_);
+    }
+
+  private:
+    c10::intrusive_ptr<GraphedLoss> graphed_;
+};
 
 }  // namespace
 
@@ -318,4 +617,11 @@ PYBIND11_MODULE(_pesq_torch, m) {
     m.def("resample", &resample,
           "(x, n_out, kernel, tap_lo, tap_hi, phase_lo, phase_hi, plan, info, orig_step, "
           "new_step, width) -> y, differentiable twice");
+    pybind11::class_<GraphedLossCallable>(m, "GraphedLoss",
+                                          "loss(ref, deg) of one input shape replayed from HIP graphs")
+        .def(pybind11::init<const at::Tensor &, const at::Tensor &, const at::Tensor &, double,
+                            const std::vector<at::Tensor> &, const std::vector<int64_t> &>(),
+             pybind11::arg("ref"), pybind11::arg("deg"), pybind11::arg("table"),
+             pybind11::arg("factor"), pybind11::arg("bank"), pybind11::arg("steps"))
+        .def("__call__", &GraphedLossCallable::call, pybind11::arg("ref"), pybind11::arg("deg"));
 }

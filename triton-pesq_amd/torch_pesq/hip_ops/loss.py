@@ -15,16 +15,23 @@ class PesqLossHip(PesqLoss):
     """PESQ loss on HIP kernels with HIP graph capture."""
 
     def graphed(self, ref: torch.Tensor, deg: torch.Tensor):
-        """Capture the loss in a HIP graph, specialised to one input shape.
+        """Capture the loss in HIP graphs, specialised to one input shape.
 
         Mirrors ``triton_ops/loss.py:149-201``: detached sample copies with the
-        same ``requires_grad`` flags, one warm-up on a side stream (nothing is
-        tuned at run time here, the warm-up only settles the allocator), then
-        ``torch.cuda.make_graphed_callables``.  The returned callable replaces
-        ``self.__call__`` for this shape and these flags, and is bit exact with
-        the eager path.  Unlike the reference, ``self`` is left untouched (the
-        graph is captured through a thin wrapper), so the module keeps working
-        for other shapes.
+        same ``requires_grad`` flags and one warm-up on a side stream (nothing
+        is tuned at run time here; the warm-up loads the kernels before the
+        capture).  The returned callable replaces ``self.__call__`` for this
+        shape and these flags and is bit exact with the eager path, loss and
+        gradients.  As with the reference's ``make_graphed_callables``, the
+        loss and the gradients it returns are static buffers that the next
+        call overwrites.  Unlike the reference, ``self`` is left untouched, so
+        the module keeps working for other shapes.
+
+        At the PESQ geometry the graphs are captured by the C++ extension
+        (``GraphedLoss``: the forward and backward library calls, and the
+        resampler's when the rate is not 16 kHz), whose autograd node replays
+        them with no Python in between.  Other STFT geometries, which run the
+        per stage operators, go through ``torch.cuda.make_graphed_callables``.
         """
 
         sample = tuple(t.detach().clone().requires_grad_(t.requires_grad) for t in (ref, deg))
@@ -37,7 +44,20 @@ class PesqLossHip(PesqLoss):
                 torch.autograd.grad(output.sum(), [t for t in sample if t.requires_grad])
         torch.cuda.current_stream().wait_stream(stream)
         torch.cuda.synchronize()
-        return torch.cuda.make_graphed_callables(target, sample)
+        if self.general:
+            return torch.cuda.make_graphed_callables(target, sample)
+
+        from .. import _lib
+
+        bank, steps = [], []
+        rs = self.resampler
+        if rs.orig_freq != rs.new_freq:
+            bank = [rs.kernel, rs.tap_lo, rs.tap_hi, rs.phase_lo, rs.phase_hi, rs.plan,
+                    rs.plan_bytes]
+            steps = [rs.orig_step, rs.new_step, rs.width, rs.output_length(sample[0].shape[-1])]
+        return _lib.torch_ext().GraphedLoss(
+            sample[0], sample[1], self.model_table, float(self.factor), bank, steps
+        )
 
 
 class _LossCall(torch.nn.Module):
