@@ -5,8 +5,9 @@ steps of the PESQ loss on BASELINE config c2 (B = 8 items of 8 s at 16 kHz,
 gradient w.r.t. the degraded signal): the two C ABI calls that
 ``PesqLossTriton``'s autograd makes (``pesq_pipeline_forward`` and
 ``pesq_pipeline_backward``) on the resident batch.  It prints one JSON line
-with the metric, the same step through the autograd API and through HIP
-graph replay, per stage device times, the HBM roofline of the dominant stage
+with the metric, the same step through the autograd API, through
+``PesqLossTriton.graphed`` (forward and backward graph replays) and as one
+whole-step HIP graph (``graphed_step``), per stage device times, the HBM roofline of the dominant stage
 measured with HIP events on the stream the kernels run on, and a CPU baseline
 (the float32 restatement of the reference ``PesqLoss``, timed on this host).
 
@@ -613,6 +614,19 @@ def main(argv=None):
     torch.cuda.synchronize()
     graph_ms = (time.perf_counter() - t0) / args.steps * 1e3
 
+    # the whole step (forward, backward of loss.sum()) as one HIP graph on
+    # static inputs holding the batch (PesqLossTriton.graphed_step)
+    whole = model.graphed_step(ref, deg)
+    for _ in range(args.warmup):
+        whole.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        whole.replay()
+    torch.cuda.synchronize()
+    step_graph_ms = (time.perf_counter() - t0) / args.steps * 1e3
+    del whole
+
     # the PesqLossTriton autograd step (host bound: PyTorch's autograd engine
     # and the Python glue take longer per step than the GPU work)
     for _ in range(args.warmup):
@@ -697,6 +711,7 @@ def main(argv=None):
         },
         "api_eager_ms_per_step": round(api_ms, 4),
         "graph_ms_per_step": round(graph_ms, 4),
+        "step_graph_ms_per_step": round(step_graph_ms, 4),
         "device_ms_per_step": round(device_ms, 4),
         "step_model_bytes": total_bytes,
         "step_hbm_frac": round(total_bytes / (ms / 1e3) / HBM_PEAK, 4),

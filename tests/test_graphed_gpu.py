@@ -12,6 +12,9 @@ in the same buffers passed again (read in place by a graph captured for
 them, more buffer pairs than such graphs are kept), non-contiguous and 1-d
 inputs, a shape other than the captured one raises, the backward is
 differentiable once, and the per stage geometry (``make_graphed_callables``).
+``graphed_step`` (forward and backward of ``loss.sum()`` in one graph, not in
+the reference) is held to the same: the eager step's bits on every replay,
+with new data written into its static inputs.
 """
 
 import pytest
@@ -177,3 +180,41 @@ def test_per_stage_geometry_graphed():
     r, d = _pair(2, 16000, seed=36)
     d.requires_grad_(True)
     _check_replays(model, r, d, replays=2)
+
+
+@pytest.mark.parametrize("rate,samples", [(16000, 20000), (48000, 60000)])
+@pytest.mark.parametrize("flags", [(False, True), (True, True)])
+def test_graphed_step_matches_eager(rate, samples, flags):
+    """The whole step as one graph: loss and gradients of the eager step, every replay."""
+    model = PesqLossTriton(0.5, sample_rate=rate).cuda()
+    r, d = _pair(2, samples, seed=39)
+    r.requires_grad_(flags[0])
+    d.requires_grad_(flags[1])
+    step = model.graphed_step(r, d)
+    static_r, static_d = step.inputs()
+    assert torch.equal(static_r, r.detach()) and torch.equal(static_d, d.detach())
+    for scale in (1.0, 1.0, 0.5, 2.0):
+        with torch.no_grad():
+            static_d.copy_(d * scale + 0.01 * (scale - 1.0) * r)
+        rr = static_r.clone().requires_grad_(flags[0])
+        dd = static_d.clone().requires_grad_(flags[1])
+        want = model(rr, dd)
+        want_grads = torch.autograd.grad(want.sum(), [t for t in (rr, dd) if t.requires_grad])
+        step.replay()
+        torch.cuda.synchronize()
+        loss, g_ref, g_deg = step.outputs()
+        assert torch.equal(loss, want.detach()), scale
+        got_grads = [g for g, f in zip((g_ref, g_deg), flags) if f]
+        assert (g_ref is None) == (not flags[0])
+        for w, g in zip(want_grads, got_grads):
+            assert torch.equal(g, w), scale
+        # eager work on other inputs between the replays
+        model(r.detach() * 0.5, d.detach() + 0.01)
+        torch.cuda.synchronize()
+
+
+def test_graphed_step_needs_a_gradient():
+    model = PesqLossTriton(0.5, sample_rate=16000).cuda()
+    r, d = _pair(1, 16000, seed=40)
+    with pytest.raises(ValueError, match="gradient"):
+        model.graphed_step(r, d)

@@ -531,76 +531,131 @@ struct GraphedCall : public torch::autograd::Function<GraphedCall> {
 };
 
 // the Python object PesqLossTriton.graphed returns
+// The static buffers of a graphed loss for examples ref, deg (their shape and
+// requires_grad flags).  bank: the resampler's (kernel, tap_lo, tap_hi,
+// phase_lo, phase_hi, plan, info) and steps its (orig_step, new_step, width,
+// output length), both empty at 16 kHz.
+c10::intrusive_ptr<GraphedLoss> graphed_buffers(const at::Tensor &ref, const at::Tensor &deg,
+                                                const at::Tensor &table, double factor,
+                                                const std::vector<at::Tensor> &bank,
+                                                const std::vector<int64_t> &steps) {
+    TORCH_CHECK(ref.dim() >= 1 && ref.dim() <= 2 && ref.sizes() == deg.sizes(),
+                "graphed loss: ref and deg must be [batch, samples] or [samples] of one shape");
+    TORCH_CHECK(bank.empty() ? steps.empty() : bank.size() == 7 && steps.size() == 4,
+                "graphed loss: the resampler bank is 7 tensors and 4 sizes");
+    auto g = c10::make_intrusive<GraphedLoss>();
+    g->shape = ref.sizes().vec();
+    g->table = table;
+    g->factor = factor;
+    g->mask = (ref.requires_grad() ? PESQ_GRAD_REF : 0) | (deg.requires_grad() ? PESQ_GRAD_DEG : 0);
+    g->batch = ref.dim() == 2 ? ref.size(0) : 1;
+    g->n_src = ref.size(-1);
+    const c10::DeviceGuard guard(ref.device());
+    const auto f32 = ref.options().dtype(at::kFloat).requires_grad(false);
+    g->ref_s = at::empty({g->batch, g->n_src}, f32);
+    g->deg_s = at::empty({g->batch, g->n_src}, f32);
+    g->resampled = !bank.empty();
+    if (g->resampled) {
+        g->bank = make_bank(ref.get_device(), bank[0], bank[1], bank[2], bank[3], bank[4], bank[5],
+                            bank[6], steps[0], steps[1], steps[2]);
+        g->n16 = steps[3];
+        TORCH_CHECK(g->n16 > 0, "graphed loss: empty signals");
+        g->ref16 = at::empty({g->batch, g->n16}, f32);
+        g->deg16 = at::empty({g->batch, g->n16}, f32);
+    } else {
+        g->n16 = g->n_src;
+        g->ref16 = g->ref_s;
+        g->deg16 = g->deg_s;
+    }
+    check_pipeline_inputs(g->ref16, g->deg16, table);
+    size_t bytes = 0;
+    check(pesq_pipeline_forward_workspace(g->batch, g->n16, g->mask, &bytes),
+          "pesq_pipeline_forward_workspace");
+    g->ws = at::empty({static_cast<int64_t>(bytes)}, f32.dtype(at::kByte));
+    for (at::Tensor &o : g->out) o = at::empty({g->batch}, f32);
+    if (g->mask != 0) {
+        check(pesq_pipeline_backward_workspace(g->batch, g->n16, g->mask, &bytes),
+              "pesq_pipeline_backward_workspace");
+        g->scratch = at::empty({static_cast<int64_t>(bytes)}, f32.dtype(at::kByte));
+        g->g_loss = at::empty({g->batch}, f32);
+        if (g->mask & PESQ_GRAD_REF) g->g_ref16 = at::empty({g->batch, g->n16}, f32);
+        if (g->mask & PESQ_GRAD_DEG) g->g_deg16 = at::empty({g->batch, g->n16}, f32);
+        if (g->resampled) {
+            if (g->g_ref16.defined()) g->g_ref = at::empty({g->batch, g->n_src}, f32);
+            if (g->g_deg16.defined()) g->g_deg = at::empty({g->batch, g->n_src}, f32);
+        } else {
+            g->g_ref = g->g_ref16;
+            g->g_deg = g->g_deg16;
+        }
+    }
+    return g;
+}
+
+// the Python object PesqLossTriton.graphed returns
 class GraphedLossCallable {
   public:
-    // ref, deg: examples of the inputs (their shape and requires_grad flags);
-    // bank: the resampler's (kernel, tap_lo, tap_hi, phase_lo, phase_hi, plan,
-    // info) and steps its (orig_step, new_step, width, output length), both
-    // empty at 16 kHz
     GraphedLossCallable(const at::Tensor &ref, const at::Tensor &deg, const at::Tensor &table,
                         double factor, const std::vector<at::Tensor> &bank,
-                        const std::vector<int64_t> &steps) {
-        TORCH_CHECK(ref.dim() >= 1 && ref.dim() <= 2 && ref.sizes() == deg.sizes(),
-                    "graphed loss: ref and deg must be [batch, samples] or [samples] of one shape");
-        TORCH_CHECK(bank.empty() ? steps.empty() : bank.size() == 7 && steps.size() == 4,
-                    "graphed loss: the resampler bank is 7 tensors and 4 sizes");
-        auto g = c10::make_intrusive<GraphedLoss>();
-        g->shape = ref.sizes().vec();
-        g->table = table;
-        g->factor = factor;
-        g->mask = (ref.requires_grad() ? PESQ_GRAD_REF : 0) | (deg.requires_grad() ? PESQ_GRAD_DEG : 0);
-        g->batch = ref.dim() == 2 ? ref.size(0) : 1;
-        g->n_src = ref.size(-1);
-        const c10::DeviceGuard guard(ref.device());
-        const auto f32 = ref.options().dtype(at::kFloat).requires_grad(false);
-        g->ref_s = at::empty({g->batch, g->n_src}, f32);
-        g->deg_s = at::empty({g->batch, g->n_src}, f32);
-        g->resampled = !bank.empty();
-        if (g->resampled) {
-            g->bank = make_bank(ref.get_device(), bank[0], bank[1], bank[2], bank[3], bank[4],
-                                bank[5], bank[6], steps[0], steps[1], steps[2]);
-            g->n16 = steps[3];
-            TORCH_CHECK(g->n16 > 0, "graphed loss: empty signals");
-            g->ref16 = at::empty({g->batch, g->n16}, f32);
-            g->deg16 = at::empty({g->batch, g->n16}, f32);
-        } else {
-            g->n16 = g->n_src;
-            g->ref16 = g->ref_s;
-            g->deg16 = g->deg_s;
-        }
-        check_pipeline_inputs(g->ref16, g->deg16, table);
-        size_t bytes = 0;
-        check(pesq_pipeline_forward_workspace(g->batch, g->n16, g->mask, &bytes),
-              "pesq_pipeline_forward_workspace");
-        g->ws = at::empty({static_cast<int64_t>(bytes)}, f32.dtype(at::kByte));
-        for (at::Tensor &o : g->out) o = at::empty({g->batch}, f32);
-        if (g->mask != 0) {
-            check(pesq_pipeline_backward_workspace(g->batch, g->n16, g->mask, &bytes),
-                  "pesq_pipeline_backward_workspace");
-            g->scratch = at::empty({static_cast<int64_t>(bytes)}, f32.dtype(at::kByte));
-            g->g_loss = at::empty({g->batch}, f32);
-            if (g->mask & PESQ_GRAD_REF) g->g_ref16 = at::empty({g->batch, g->n16}, f32);
-            if (g->mask & PESQ_GRAD_DEG) g->g_deg16 = at::empty({g->batch, g->n16}, f32);
-            if (g->resampled) {
-                if (g->g_ref16.defined()) g->g_ref = at::empty({g->batch, g->n_src}, f32);
-                if (g->g_deg16.defined()) g->g_deg = at::empty({g->batch, g->n_src}, f32);
-            } else {
-                g->g_ref = g->g_ref16;
-                g->g_deg = g->g_deg16;
-            }
-        }
+                        const std::vector<int64_t> &steps)
+        : graphed_(graphed_buffers(ref, deg, table, factor, bank, steps)) {
         // the static buffers are allocated on the current stream; the capture
         // stream only records
-        GraphedLoss &s = *g;
+        GraphedLoss &s = *graphed_;
+        const c10::DeviceGuard guard(s.ref_s.device());
         s.fwd = s.capture([&s](hipStream_t stream) {
             s.enqueue_forward(s.ref_s.data_ptr<float>(), s.deg_s.data_ptr<float>(), stream);
         });
         if (s.mask != 0) s.bwd = s.capture([&s](hipStream_t stream) { s.enqueue_backward(stream); });
-        graphed_ = std::move(g);
     }
 
     at::Tensor call(const at::Tensor &ref, const at::Tensor &deg) const {
         return GraphedCall::apply(ref, deg, graphed_);
+    }
+
+  private:
+    c10::intrusive_ptr<GraphedLoss> graphed_;
+};
+
+// A whole training step of the loss, grad(loss.sum(), inputs), as one HIP
+// graph: the forward, then the backward with upstream gradients of one (the
+// derivative of the sum), on static inputs the caller writes into.  No
+// counterpart in the reference, whose graphs stop at the autograd boundary;
+// it is the step the library's calls make capturable as a whole.
+class GraphedStep {
+  public:
+    GraphedStep(const at::Tensor &ref, const at::Tensor &deg, const at::Tensor &table,
+                double factor, const std::vector<at::Tensor> &bank,
+                const std::vector<int64_t> &steps)
+        : graphed_(graphed_buffers(ref, deg, table, factor, bank, steps)) {
+        GraphedLoss &s = *graphed_;
+        TORCH_CHECK(s.mask != 0, "graphed step: ref or deg must require a gradient");
+        const c10::DeviceGuard guard(s.ref_s.device());
+        s.g_loss.fill_(1.0);  // d sum / d loss, written once, before any replay
+        s.fwd = s.capture([&s](hipStream_t stream) {
+            s.enqueue_forward(s.ref_s.data_ptr<float>(), s.deg_s.data_ptr<float>(), stream);
+            s.enqueue_backward(stream);
+        });
+    }
+
+    void replay() const {
+        GraphedLoss &s = *graphed_;
+        const c10::DeviceGuard guard(s.ref_s.device());
+        const hipStream_t stream = current_stream(s.ref_s);
+        check_hip(hipGraphLaunch(s.fwd, stream), "hipGraphLaunch");
+        s.fwd_stream = stream;
+    }
+
+    // the static inputs (ref, deg), shaped like the examples
+    std::vector<at::Tensor> inputs() const {
+        return {graphed_->ref_s.view(graphed_->shape), graphed_->deg_s.view(graphed_->shape)};
+    }
+
+    // loss [batch] and the gradients of ref and deg (undefined, i.e. None,
+    // for an input whose example did not require one)
+    std::vector<at::Tensor> outputs() const {
+        const GraphedLoss &s = *graphed_;
+        return {s.out[3], s.g_ref.defined() ? s.g_ref.view(s.shape) : at::Tensor(),
+                s.g_deg.defined() ? s.g_deg.view(s.shape) : at::Tensor()};
     }
 
   private:
@@ -624,4 +679,14 @@ PYBIND11_MODULE(_pesq_torch, m) {
              pybind11::arg("ref"), pybind11::arg("deg"), pybind11::arg("table"),
              pybind11::arg("factor"), pybind11::arg("bank"), pybind11::arg("steps"))
         .def("__call__", &GraphedLossCallable::call, pybind11::arg("ref"), pybind11::arg("deg"));
+    pybind11::class_<GraphedStep>(m, "GraphedStep",
+                                  "grad(loss(ref, deg).sum(), inputs) of one input shape as one "
+                                  "HIP graph on static inputs")
+        .def(pybind11::init<const at::Tensor &, const at::Tensor &, const at::Tensor &, double,
+                            const std::vector<at::Tensor> &, const std::vector<int64_t> &>(),
+             pybind11::arg("ref"), pybind11::arg("deg"), pybind11::arg("table"),
+             pybind11::arg("factor"), pybind11::arg("bank"), pybind11::arg("steps"))
+        .def("replay", &GraphedStep::replay)
+        .def("inputs", &GraphedStep::inputs)
+        .def("outputs", &GraphedStep::outputs);
 }

@@ -49,15 +49,56 @@ class PesqLossHip(PesqLoss):
 
         from .. import _lib
 
-        bank, steps = [], []
-        rs = self.resampler
-        if rs.orig_freq != rs.new_freq:
-            bank = [rs.kernel, rs.tap_lo, rs.tap_hi, rs.phase_lo, rs.phase_hi, rs.plan,
-                    rs.plan_bytes]
-            steps = [rs.orig_step, rs.new_step, rs.width, rs.output_length(sample[0].shape[-1])]
         return _lib.torch_ext().GraphedLoss(
-            sample[0], sample[1], self.model_table, float(self.factor), bank, steps
+            sample[0], sample[1], self.model_table, float(self.factor), *self._bank(sample[0])
         )
+
+    def graphed_step(self, ref: torch.Tensor, deg: torch.Tensor):
+        """``grad(self(ref, deg).sum(), inputs)`` as one HIP graph, for one input shape.
+
+        Not in the reference, whose graphs stop at the autograd boundary: the
+        forward and the backward (upstream gradients of one, the derivative
+        of the sum) of the inputs whose examples require a gradient, captured
+        together.  The returned object has ``inputs()`` (the static ``ref``,
+        ``deg`` to write into), ``replay()`` (on the current stream) and
+        ``outputs()`` (the static loss and the gradients of ``ref`` and
+        ``deg``, ``None`` where not requested), all bit exact with the eager
+        step.  The PESQ geometry only (the fused pipeline).
+        """
+
+        if self.general:
+            raise ValueError("graphed_step needs the PESQ geometry (the fused pipeline).")
+        if not (ref.requires_grad or deg.requires_grad):
+            raise ValueError("graphed_step: ref or deg must require a gradient.")
+        sample = tuple(t.detach().clone().requires_grad_(t.requires_grad) for t in (ref, deg))
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            output = self(*sample)
+            torch.autograd.grad(output.sum(), [t for t in sample if t.requires_grad])
+        torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+
+        from .. import _lib
+
+        step = _lib.torch_ext().GraphedStep(
+            sample[0], sample[1], self.model_table, float(self.factor), *self._bank(sample[0])
+        )
+        static_ref, static_deg = step.inputs()
+        with torch.no_grad():
+            static_ref.copy_(ref)
+            static_deg.copy_(deg)
+        return step
+
+    def _bank(self, example: torch.Tensor):
+        """The resampler's tables and sizes for the graphed classes (empty at 16 kHz)."""
+
+        rs = self.resampler
+        if rs.orig_freq == rs.new_freq:
+            return [], []
+        bank = [rs.kernel, rs.tap_lo, rs.tap_hi, rs.phase_lo, rs.phase_hi, rs.plan, rs.plan_bytes]
+        steps = [rs.orig_step, rs.new_step, rs.width, rs.output_length(example.shape[-1])]
+        return bank, steps
 
 
 class _LossCall(torch.nn.Module):
