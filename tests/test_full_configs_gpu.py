@@ -134,16 +134,20 @@ def test_config5_full_batch_forward_and_backward():
 
 
 def test_config3_full_batch_forward_and_backward():
-    """16 x 4 s at 44.1 kHz: the 441:160 tiled resampler and its adjoint over the
-    full batch (the 16 kHz pipeline grid is small, like c2)."""
+    """16 x 4 s at 44.1 kHz: the 441:160 phase-major resampler and its adjoint over
+    the full batch (the 16 kHz pipeline grid is small, like c2)."""
 
     ref_np, deg_np, fs, weights, outputs, g_deg, kernels = _run_step(3)
     batch = ref_np.shape[0]
     length = O.resample_length(ref_np.shape[1], fs, 16000)
     _assert_pipeline_variants(kernels, batch, length)
-    # the forward of both signals and the adjoint (the transposed bank on the
-    # forward's kernel, a resampler from 16 kHz to 44.1 kHz)
-    tiled = [k for k in kernels if k.startswith("resample_fwd_tiled")]
-    assert len(tiled) == 1 and kernels[tiled[0]] == 3, sorted(kernels.items())
+    # the forward of both signals (34 taps per phase, the 36-tap instantiation
+    # with float samples) and the adjoint (the transposed bank, a resampler from
+    # 16 kHz to 44.1 kHz with 13 taps per phase: 16 taps, double samples)
+    resamplers = {k: v for k, v in kernels.items() if k.startswith("resample")}
+    assert resamplers == {
+        "resample_phase_major<36,float>": 2,
+        "resample_phase_major<16,double>": 1,
+    }, resamplers
     _compare_with_oracle(ref_np, deg_np, fs, weights, outputs, g_deg, range(batch))
 

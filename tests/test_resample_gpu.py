@@ -44,6 +44,34 @@ def test_forward_matches_float64(orig, new, length):
     assert _close(got, want)
 
 
+@pytest.mark.parametrize("orig,new", [(44100, 16000), (22050, 16000), (16000, 44100), (44100, 48000)])
+@pytest.mark.parametrize("length", [37, 1001, 44101])
+def test_planned_forward_matches_untiled_kernel(orig, new, length):
+    """The planned forward (phase major for these many-phase pairs: each phase's
+    taps in registers, one output per phase and period) against the untiled
+    per-output kernel: both sum the non-zero taps in ascending order in
+    float64 (the planned kernel adds exact zeros past a phase's run and for
+    samples outside the row), so the outputs are the same numbers."""
+
+    from torch_pesq import _lib
+
+    mod = HipResample(orig, new).cuda()
+    x = torch.randn(3, length, generator=torch.Generator().manual_seed(7 * length)).cuda()
+    got = mod(x)
+    want = torch.empty_like(got)
+    lib = _lib.library()
+    _lib.check(
+        lib.pesq_resample_forward(
+            _lib.ptr(x), _lib.ptr(want), 3, length, got.shape[1], _lib.ptr(mod.kernel),
+            _lib.ptr(mod.tap_lo), _lib.ptr(mod.tap_hi), mod.orig_step, mod.new_step, mod.width,
+            mod.kernel.shape[1], _lib.stream_handle(x.device),
+        ),
+        "pesq_resample_forward",
+    )
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("orig", [32000, 48000, 64000, 96000])
 @pytest.mark.parametrize("length", [1, 37, 6001, 50001])
 def test_integer_decimation(orig, length):

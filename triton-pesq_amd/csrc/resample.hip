@@ -277,6 +277,194 @@ __global__ void __launch_bounds__(kResampleThreads)
     }
 }
 
+// Phase-major kernel for rate pairs of many phases (44.1 -> 16 kHz is 441:160,
+// its adjoint through the transposed bank 160:441): thread (j, h) of a
+// workgroup of `groups` x nstep threads computes phase j of kP consecutive
+// periods h kP .. h kP + kP - 1 of the workgroup's, with phase j's taps held
+// in registers as doubles (converted once), so that a tap costs one LDS read
+// of a staged sample and one FMA (the tiled kernel reads a tap and a sample
+// and converts both); the samples are staged as S (double, or float
+// converted per tap where the reads would cost more than the conversion).  The taps are the tiled
+// kernel's zero-padded table, and each sum runs over them in ascending order
+// from zero, the tiled kernel's operations, followed by exact zero terms up
+// to a multiple of four taps: the same outputs for finite samples.
+constexpr int kPhaseMinPhases = 64;     // fewer phases: the tiled kernel
+constexpr int kPhaseMaxThreads = 512;   // threads per workgroup
+constexpr int kPhasePeriods = 4;        // periods per thread
+constexpr int kPhaseLds = 65536;        // bytes of staged samples a workgroup may hold
+
+// Staging of samples lo .. lo + span - 1 of a row of n (zero outside it) as S
+// (float or double), by any number of threads: four samples per thread with
+// 16-byte loads, two loads per thread issued before their LDS writes.  The
+// destination holds span rounded up to a multiple of 4 values.
+template <typename S>
+__device__ __forceinline__ void stage_row_as(S *__restrict__ dst, const float *__restrict__ src,
+                                             int64_t lo, int64_t n, int span) {
+    const int nt = static_cast<int>(blockDim.x), tid = static_cast<int>(threadIdx.x);
+    const int span4 = (span + 3) & ~3;
+    if (n >= 4 && lo >= 0 && lo + span4 <= n) {
+        constexpr int kB = 2;
+        const float *seg = src + lo;
+        for (int s0 = 0; s0 < span; s0 += 4 * kB * nt) {
+            float q[kB][4];
+#pragma unroll
+            for (int k = 0; k < kB; ++k) {
+                const int s = s0 + 4 * (k * nt + tid);
+                __builtin_memcpy(q[k], seg + (s < span4 ? s : span4 - 4), sizeof(q[k]));
+            }
+#pragma unroll
+            for (int k = 0; k < kB; ++k) {
+                const int s = s0 + 4 * (k * nt + tid);
+                if (s < span) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) dst[s + e] = static_cast<S>(q[k][e]);
+                }
+            }
+        }
+        return;
+    }
+    for (int s = tid; s < span4; s += nt) {
+        const int64_t i = lo + s;
+        dst[s] = (s < span && i >= 0 && i < n) ? static_cast<S>(src[i]) : S(0);
+    }
+}
+
+// y[l nstep + j] = sum_{t < kTaps} taps[t][j] x[l orig + offs[j] + t] (x zero
+// outside the row), the taps past ntaps zero: the tap loop is unrolled with
+// no condition (a condition per tap makes the compiler wait out each tap's
+// LDS reads before the next tap's), and the staged window covers kTaps.
+template <int kTaps, typename S>
+__global__ void __launch_bounds__(kPhaseMaxThreads)
+    resample_phase_major(const float *__restrict__ x, float *__restrict__ y, int64_t n_in,
+                         int64_t n_out, const float *__restrict__ taps,
+                         const int32_t *__restrict__ offs, int orig, int nstep, int ntaps,
+                         int off_min, int groups, int span, int64_t blocks_per_row) {
+    extern __shared__ double lds_phase[];
+    S *xs_phase = reinterpret_cast<S *>(lds_phase);
+    const int64_t row = blockIdx.x / blocks_per_row;
+    const int64_t blk = blockIdx.x - row * blocks_per_row;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int h = tid / nstep, j = tid - h * nstep;
+    const bool active = h < groups;
+    const int jj = active ? j : 0;
+    // the phase's taps and offset, requested before the staging (rows past
+    // ntaps read the last row and are zeroed)
+    double w[kTaps];
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) {
+        const float v = taps[int64_t(t < ntaps ? t : ntaps - 1) * nstep + jj];
+        w[t] = t < ntaps ? static_cast<double>(v) : 0.0;
+    }
+    const int base = offs[jj] - off_min;
+    const int64_t l0 = blk * groups * kPhasePeriods;  // first period of the workgroup
+    stage_row_as<S>(xs_phase, x + row * n_in, l0 * orig + off_min, n_in, span);
+    __syncthreads();
+    if (!active) return;
+    double acc[kPhasePeriods];
+    const S *src[kPhasePeriods];
+#pragma unroll
+    for (int q = 0; q < kPhasePeriods; ++q) {
+        acc[q] = 0.0;
+        src[q] = xs_phase + (h * kPhasePeriods + q) * orig + base;
+    }
+    // four taps at a time: the empty asm statements pin each group's sums
+    // before the next group's reads, which keeps the compiler from hoisting
+    // every LDS read to the top (that takes all 256 VGPRs and spills)
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t) {
+#pragma unroll
+        for (int q = 0; q < kPhasePeriods; ++q) {
+            acc[q] = fma(w[t], static_cast<double>(src[q][t]), acc[q]);
+        }
+        if (t % 4 == 3) {
+#pragma unroll
+            for (int q = 0; q < kPhasePeriods; ++q) asm volatile("" : "+v"(acc[q]));
+        }
+    }
+    float *yr = y + row * n_out;
+#pragma unroll
+    for (int q = 0; q < kPhasePeriods; ++q) {
+        const int64_t m = (l0 + h * kPhasePeriods + q) * nstep + j;
+        if (m < n_out) yr[m] = static_cast<float>(acc[q]);
+    }
+}
+
+// Groups of nstep threads per workgroup of resample_phase_major: the count
+// whose threads fill their wavefronts best (ties: more groups); 0 when the
+// kernel does not apply.
+static int phase_groups(int nstep) {
+    if (nstep < kPhaseMinPhases || nstep > kPhaseMaxThreads) return 0;
+    int best = 0;
+    double best_fill = 0.0;
+    for (int g = 1; g * nstep <= kPhaseMaxThreads; ++g) {
+        const int threads = (g * nstep + kWave - 1) / kWave * kWave;
+        if (threads > kPhaseMaxThreads) break;
+        const double fill = double(g * nstep) / threads;
+        if (fill >= best_fill) {
+            best_fill = fill;
+            best = g;
+        }
+    }
+    return best;
+}
+
+// Launches resample_phase_major when the pair suits it (false otherwise):
+// y [rows, n_out] from x [rows, n_in] with the table taps [ntaps][nstep] and
+// offsets offs[nstep] in off_min .. off_max.
+static bool launch_phase_major(const float *x, float *y, int64_t rows, int64_t n_in,
+                               int64_t n_out, const float *taps, const int32_t *offs, int orig,
+                               int nstep, int ntaps, int off_min, int off_max,
+                               hipStream_t stream) {
+    // The samples are staged as doubles where a period reads at most nstep of
+    // them (upsampling, and the adjoint of downsampling through the transposed
+    // bank): the phases of a wavefront then read overlapping windows, largely
+    // the same LDS words, and no conversion is left in the tap loop (c3
+    // adjoint 10.5-10.8 us, 11.2-11.3 with floats).  With orig > nstep (the
+    // 441:160 forward) consecutive phases read about orig / nstep samples
+    // apart, and 8-byte reads per tap cost more than the tiled kernel (15.5
+    // against 14.2 us at c3), so the samples stay floats, converted per tap
+    // (11.0-11.4 us).
+    const int groups = phase_groups(nstep);
+    if (groups == 0 || ntaps < 1 || ntaps > 40) return false;
+    const bool wide = orig > nstep;  // float staging
+    const int ktaps = (ntaps + 3) / 4 * 4;  // the instantiation: taps rounded up to 4
+    const int64_t periods = int64_t(groups) * kPhasePeriods;
+    const int64_t span = (periods - 1) * orig + (off_max - off_min) + ktaps;
+    const int64_t lds = (span + 3) / 4 * 4 * int64_t(wide ? sizeof(float) : sizeof(double));
+    if (lds > kPhaseLds) return false;
+    const int64_t bpr = cdiv(cdiv(n_out, int64_t(nstep)), periods);
+    if (rows * bpr >= (int64_t(1) << 31)) return false;
+    const int threads = (groups * nstep + kWave - 1) / kWave * kWave;
+    const dim3 grid(static_cast<unsigned>(rows * bpr)), block(static_cast<unsigned>(threads));
+#define PESQ_PHASE_MAJOR(K)                                                                      \
+    case K:                                                                                       \
+        if (wide) {                                                                               \
+            hipLaunchKernelGGL((resample_phase_major<K, float>), grid, block, size_t(lds), stream, \
+                               x, y, n_in, n_out, taps, offs, orig, nstep, ntaps, off_min, groups, \
+                               static_cast<int>(span), bpr);                                      \
+        } else {                                                                                  \
+            hipLaunchKernelGGL((resample_phase_major<K, double>), grid, block, size_t(lds),       \
+                               stream, x, y, n_in, n_out, taps, offs, orig, nstep, ntaps, off_min, \
+                               groups, static_cast<int>(span), bpr);                              \
+        }                                                                                         \
+        return true;
+    switch (ktaps) {
+        PESQ_PHASE_MAJOR(4)
+        PESQ_PHASE_MAJOR(8)
+        PESQ_PHASE_MAJOR(12)
+        PESQ_PHASE_MAJOR(16)
+        PESQ_PHASE_MAJOR(20)
+        PESQ_PHASE_MAJOR(24)
+        PESQ_PHASE_MAJOR(28)
+        PESQ_PHASE_MAJOR(32)
+        PESQ_PHASE_MAJOR(36)
+        PESQ_PHASE_MAJOR(40)
+        default:
+            return false;
+    }
+#undef PESQ_PHASE_MAJOR
+}
+
 // Single phase forward (new_step 1, decimation by kOrig) with a register
 // window: thread u computes the kR consecutive outputs m0 + kR u + r.  With
 // the taps taken in chunks t = kOrig c + d, output r reads the staged sample
@@ -832,6 +1020,11 @@ extern "C" int pesq_resample_plan_forward(const float *x, float *y, int64_t rows
             return PESQ_OK;
         }
     }
+    if (launch_phase_major(x, y, rows, n_in, n_out, taps, offs, r.orig_step, r.new_step, r.taps,
+                           r.off_min, r.off_max, stream)) {
+        PESQ_CHECK_LAUNCH("resample forward (phase major)");
+        return PESQ_OK;
+    }
     const dim3 grid(static_cast<unsigned>(rows * bpr)), block(kResampleThreads);
     const size_t span_bytes = size_t(staged_floats(r.fwd_span, 0)) * sizeof(float);
     if (r.new_step == 1) {
@@ -923,6 +1116,11 @@ extern "C" int pesq_resample_plan_backward(const float *grad_y, float *grad_x, i
         // the transposed bank: the forward's tiled kernel from new_step to orig_step
         const float *adj = reinterpret_cast<const float *>(base + r.off_adj_taps);
         const int32_t *aoffs = reinterpret_cast<const int32_t *>(base + r.off_adj_offs);
+        if (launch_phase_major(grad_y, grad_x, rows, n_out, n_in, adj, aoffs, r.new_step,
+                               r.orig_step, r.adj_taps, r.adj_off_min, r.adj_off_max, stream)) {
+            PESQ_CHECK_LAUNCH("resample backward (phase major)");
+            return PESQ_OK;
+        }
         const int64_t table = int64_t(r.adj_taps) * r.orig_step;
         const size_t lds = size_t(staged_floats(r.adj_span, 0) + table) * sizeof(float);
         hipLaunchKernelGGL(resample_fwd_tiled<kTapsLds>, dim3(static_cast<unsigned>(rows * bpr)),

@@ -327,6 +327,28 @@ std::vector<at::Tensor> pipeline(const at::Tensor &ref, const at::Tensor &deg,
     return Pipeline::apply(ref, deg, table, factor, mask);
 }
 
+// pipeline() of the two signals resampled to 16 kHz (n_out samples per row):
+// the same autograd nodes (two resampler nodes, the pipeline node) as the
+// Python calls make one at a time, without their Python in between.  bank:
+// the resampler's (kernel, tap_lo, tap_hi, phase_lo, phase_hi, plan, info),
+// steps its (orig_step, new_step, width).
+std::vector<at::Tensor> pipeline_resampled(const at::Tensor &ref, const at::Tensor &deg,
+                                           const at::Tensor &table, double factor,
+                                           const std::vector<at::Tensor> &bank,
+                                           const std::vector<int64_t> &steps, int64_t n_out) {
+    TORCH_CHECK(bank.size() == 7 && steps.size() == 3,
+                "pipeline_resampled: the resampler bank is 7 tensors and 3 steps");
+    TORCH_CHECK(ref.is_cuda() && deg.is_cuda() && ref.scalar_type() == at::kFloat &&
+                    deg.scalar_type() == at::kFloat && ref.dim() == 2 &&
+                    ref.sizes() == deg.sizes() && ref.is_contiguous() && deg.is_contiguous(),
+                "pipeline_resampled: ref and deg must be contiguous [batch, samples] float32 GPU "
+                "tensors of one shape");
+    TORCH_CHECK(n_out >= 0, "pipeline_resampled: negative output length");
+    const ResampleBank b = make_bank(ref.get_device(), bank[0], bank[1], bank[2], bank[3],
+                                     bank[4], bank[5], bank[6], steps[0], steps[1], steps[2]);
+    return pipeline(Resample::apply(ref, n_out, b), Resample::apply(deg, n_out, b), table, factor);
+}
+
 // ---------------------------------------------------------------------------
 // graphed loss (torch_pesq/triton_ops/loss.py:149-201): the loss of one input
 // shape and one set of requires_grad flags, captured as two HIP graphs over
@@ -669,6 +691,12 @@ PYBIND11_MODULE(_pesq_torch, m) {
     m.def("pipeline", &pipeline, "(ref, deg, table, factor) -> [d_symm, d_asymm, mos, loss]",
           pybind11::arg("ref"), pybind11::arg("deg"), pybind11::arg("table"),
           pybind11::arg("factor"));
+    m.def("pipeline_resampled", &pipeline_resampled,
+          "(ref, deg, table, factor, bank, steps, n_out) -> [d_symm, d_asymm, mos, loss] of the "
+          "signals resampled to 16 kHz",
+          pybind11::arg("ref"), pybind11::arg("deg"), pybind11::arg("table"),
+          pybind11::arg("factor"), pybind11::arg("bank"), pybind11::arg("steps"),
+          pybind11::arg("n_out"));
     m.def("resample", &resample,
           "(x, n_out, kernel, tap_lo, tap_hi, phase_lo, phase_hi, plan, info, orig_step, "
           "new_step, width) -> y, differentiable twice");

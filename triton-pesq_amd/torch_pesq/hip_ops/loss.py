@@ -96,9 +96,8 @@ class PesqLossHip(PesqLoss):
         rs = self.resampler
         if rs.orig_freq == rs.new_freq:
             return [], []
-        bank = [rs.kernel, rs.tap_lo, rs.tap_hi, rs.phase_lo, rs.phase_hi, rs.plan, rs.plan_bytes]
-        steps = [rs.orig_step, rs.new_step, rs.width, rs.output_length(example.shape[-1])]
-        return bank, steps
+        bank, steps = rs.bank()
+        return bank, steps + [rs.output_length(example.shape[-1])]
 
 
 class _LossCall(torch.nn.Module):

@@ -89,6 +89,7 @@ class HipResample(torch.nn.Module):
         self.rolloff = rolloff
         self.resampling_method = resampling_method
         self.beta = beta
+        self._lengths = {}  # output length per input length
 
         if self.orig_freq == self.new_freq:
             self.width = 0
@@ -135,7 +136,26 @@ class HipResample(torch.nn.Module):
         self.register_buffer("plan", plan)
 
     def output_length(self, n_samples: int) -> int:
-        return resample_length(n_samples, self.orig_step, self.new_step)
+        n = self._lengths.get(n_samples)
+        if n is None:
+            n = self._lengths[n_samples] = resample_length(n_samples, self.orig_step, self.new_step)
+        return n
+
+    def check_length(self, n_in: int, n_out: int) -> None:
+        """Raise when a row of n_in samples (n_out out) exceeds the 32 bit launch grid."""
+
+        slack = 128 * max(self.orig_step, self.new_step) + self.kernel.shape[1]
+        if max(n_in, n_out) > _INDEX_LIMIT - slack:
+            raise RuntimeError("The signal is too long for the resampler's 32 bit launch grid.")
+
+    def bank(self):
+        """The filter tables and steps the C++ entry points take, ``(tensors, steps)``."""
+
+        return (
+            [self.kernel, self.tap_lo, self.tap_hi, self.phase_lo, self.phase_hi, self.plan,
+             self.plan_bytes],
+            [self.orig_step, self.new_step, self.width],
+        )
 
     def forward(self, waveform: torch.Tensor) -> torch.Tensor:
         """Resample ``[..., sample]`` signals along the last axis."""
@@ -151,9 +171,7 @@ class HipResample(torch.nn.Module):
         batch = math.prod(shape[:-1])
         packed = check_input(waveform.reshape(batch, shape[-1]), "waveform")
         n_out = self.output_length(shape[-1])
-        slack = 128 * max(self.orig_step, self.new_step) + self.kernel.shape[1]
-        if max(shape[-1], n_out) > _INDEX_LIMIT - slack:
-            raise RuntimeError("The signal is too long for the resampler's 32 bit launch grid.")
+        self.check_length(shape[-1], n_out)
         out = _lib.torch_ext().resample(
             packed, n_out, self.kernel, self.tap_lo, self.tap_hi, self.phase_lo, self.phase_hi,
             self.plan, self.plan_bytes, self.orig_step, self.new_step, self.width,

@@ -185,10 +185,17 @@ class PesqLoss(torch.nn.Module):
         if self.general:
             return self._run_stages(ref, deg)
 
-        if self.source_sample_rate != 16000:
-            ref, deg = self.resampler(ref), self.resampler(deg)
-
-        length = ref.shape[1]
+        resampled = self.source_sample_rate != 16000
+        if resampled:
+            if self.resampler.kernel.device != ref.device:
+                raise RuntimeError(
+                    f"The resampling kernel lives on {self.resampler.kernel.device} but the "
+                    f"signals on {ref.device}, move the module with `.to(...)`."
+                )
+            length = self.resampler.output_length(ref.shape[1])
+            self.resampler.check_length(ref.shape[1], length)
+        else:
+            length = ref.shape[1]
         padded = length + length % 256
         frames = 1 + (padded - 512) // 256 if padded >= 512 else 0
         if length < 15:
@@ -204,6 +211,13 @@ class PesqLoss(torch.nn.Module):
             raise RuntimeError(
                 "The loss treats `factor` as a constant, pass a Python float. A tensor "
                 "that requires a gradient would receive none."
+            )
+        if resampled:
+            bank, steps = self.resampler.bank()
+            return tuple(
+                _lib.torch_ext().pipeline_resampled(
+                    ref, deg, self.model_table, float(self.factor), bank, steps, length
+                )
             )
         return tuple(_lib.torch_ext().pipeline(ref, deg, self.model_table, float(self.factor)))
 
