@@ -355,12 +355,34 @@ VARIANTS = {
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, true>"],
     ),
-    # BASELINE c4: 938 blocks per row (prefix kernel), 4 x 235 = 940 tiles
+    # BASELINE c4: 938 blocks per row (prefix kernel), 4 x 235 = 940 tiles, items
+    # of 235 tiles (per item band totals)
     (4, 960000, 2): (
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
-         "stft_fwd_kernel<float, true, 8>", "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
-        ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float, 2>",
+         "stft_fwd_kernel<float, true, 8>", "band_totals_kernel<16, 2>",
+         "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
+        ["chain_bwd_kernel<4, 1>", "band_totals_kernel<8, 1>", "stft_bwd_kernel<float, 2>",
+         "iir_aggregate_kernel<5, 1, PipeBwdMode, true>", "iir_prefix_kernel<6>",
+         "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
+    ),
+    # one item of 65 tiles (1033 frames): just past the band totals threshold
+    # (259 blocks per row: the prefix kernel)
+    (1, 264704, 1): (
+        ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>", "iir_prefix_kernel<6>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
+         "stft_fwd_kernel<float, false, 8>", "band_totals_kernel<16, 2>",
+         "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
+        ["chain_bwd_kernel<16, 1>", "band_totals_kernel<8, 1>", "stft_bwd_kernel<float, 1>",
+         "iir_aggregate_kernel<5, 1, PipeBwdMode, true>", "iir_prefix_kernel<6>",
+         "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
+    ),
+    # one item of 64 tiles (1023 frames): the largest without band totals
+    (1, 262144, 1): (
+        ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>", "iir_prefix_kernel<6>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
+         "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
+        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
     ),

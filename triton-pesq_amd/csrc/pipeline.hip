@@ -487,6 +487,52 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// 3b. per item band totals (items of more than kTotalsTiles chain tiles)
+// ---------------------------------------------------------------------------
+
+// Sums over all tiles of an item of the per tile band partials: forward
+// (kArrays 2), the audible band powers of both signals (bandref, banddeg ->
+// bandtot), read by the chain forward; backward (kArrays 1), the band
+// gradient partials (grpart -> gradtot), read by the STFT backward.  Each sum
+// runs in the order the reading kernel would take it itself: kSlices slices
+// of tiles v, v + kSlices, ... (in tile order), then the slices in order, so
+// the totals are those bits.  One workgroup per item, wavefront v a slice,
+// a lane a band.
+template <int kSlices, int kArrays>
+__global__ void __launch_bounds__(kWave *kSlices) band_totals_kernel(PipeArgs a) {
+    __shared__ double part[kArrays][kSlices][kBands];
+    const PipeLayout &L = a.L;
+    const int item = blockIdx.x;
+    const int wave = wave_index();
+    const int lane = threadIdx.x % kWave;
+    const double *src[kArrays];
+    double *dst;
+    if constexpr (kArrays == 2) {
+        src[0] = region<double>(a.ws, L.bandref) + int64_t(item) * L.ntile * kBands;
+        src[kArrays - 1] = region<double>(a.ws, L.banddeg) + int64_t(item) * L.ntile * kBands;
+        dst = region<double>(a.ws, L.bandtot) + int64_t(item) * 2 * kBands;
+    } else {
+        src[0] = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
+        dst = region<double>(a.bw, L.gradtot) + int64_t(item) * kBands;
+    }
+    if (lane < kBands) {
+#pragma unroll
+        for (int k = 0; k < kArrays; ++k) {
+            part[k][wave][lane] = tile_partial(src[k], L.ntile, wave, kSlices, lane, kBands);
+        }
+    }
+    __syncthreads();
+    if (wave == 0 && lane < kBands) {
+#pragma unroll
+        for (int k = 0; k < kArrays; ++k) {
+            double sum = 0.0;
+            for (int v = 0; v < kSlices; ++v) sum += part[k][v][lane];
+            dst[k * kBands + lane] = sum;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // 4. chain forward per (item, 16 frames)
 // ---------------------------------------------------------------------------
 
@@ -562,8 +608,9 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
     // mean band powers over all frames of the item: slice v sums the band
     // partials of tiles v, v + kChainSlices, ...; the slices are then added in
     // order, the same order in every workgroup (wavefront w takes slices w,
-    // w + kWaves, ...)
-    {
+    // w + kWaves, ...).  Items of many tiles read the sums band_totals_kernel
+    // took in that order.
+    if (!L.totals) {
         const double *pr = region<double>(a.ws, L.bandref) + int64_t(item) * L.ntile * nb;
         const double *pd = region<double>(a.ws, L.banddeg) + int64_t(item) * L.ntile * nb;
         constexpr int kMine = kChainSlices / kWaves;  // slices per wavefront
@@ -605,9 +652,15 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
         r[k] = 0.0;
         if (live[k]) {
             double sr = 0.0, sd = 0.0;
-            for (int v = 0; v < kChainSlices; ++v) {
-                sr += part[0][v][band];
-                sd += part[1][v][band];
+            if (L.totals) {
+                const double *tot = region<double>(a.ws, L.bandtot) + int64_t(item) * 2 * nb;
+                sr = tot[band];
+                sd = tot[nb + band];
+            } else {
+                for (int v = 0; v < kChainSlices; ++v) {
+                    sr += part[0][v][band];
+                    sd += part[1][v][band];
+                }
             }
             const double mref = sr / frames_f;
             const double mdeg = sd / frames_f;
@@ -1114,7 +1167,9 @@ __global__ void __launch_bounds__(kWave *kBwdWaves, 5) stft_bwd_kernel(PipeArgs 
     // powers: wavefront w sums the band partials of tiles w, w + kBwdWaves, ...
     // and every wavefront adds the partial sums in wavefront order
     const double *grp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
-    if (lane < kBands) gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kBwdWaves, lane, kBands);
+    if (lane < kBands && !L.totals) {
+        gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kBwdWaves, lane, kBands);
+    }
     for (int k = threadIdx.x; k < kNfft; k += kWave * kBwdWaves) {
         if (k < kPassTwiddles) lds_pass[k] = StagedTwiddles<real>::pass(t)[k];
         if (k < kHalf) {
@@ -1127,7 +1182,11 @@ __global__ void __launch_bounds__(kWave *kBwdWaves, 5) stft_bwd_kernel(PipeArgs 
     double gm = 0.0, th100 = 0.0, corr = 0.0;
     if (lane < kBands) {
         double g = 0.0;
-        for (int w = 0; w < kBwdWaves; ++w) g += gpart[w][lane];
+        if (L.totals) {
+            g = region<double>(a.bw, L.gradtot)[int64_t(item) * kBands + lane];
+        } else {
+            for (int w = 0; w < kBwdWaves; ++w) g += gpart[w][lane];
+        }
         const double ratio = band_array(a, kRatio)[item * kBands + lane];
         const double mref = band_array(a, kMref)[item * kBands + lane];
         const double gr = (ratio >= 0.01 && ratio <= 100.0) ? g : 0.0;
@@ -1598,12 +1657,14 @@ extern "C" int pesq_pipeline_kernels(int64_t batch, int64_t len, int grad_mask, 
         scan_kernel_names(P.fwd_scan, "PipeFwdMode", out);
         out += std::string("stft_fwd_kernel<") + real + ", " + (P.stft_lean ? "true" : "false") +
                ", " + std::to_string(kStftWaves) + ">;";
+        if (L.totals) out += "band_totals_kernel<" + std::to_string(kChainSlices) + ", 2>;";
         out += "chain_fwd_kernel<" + std::to_string(P.chain_fwd_waves) + ", " +
                std::to_string(P.chain_bpl) + ">;";
         out += "chain_final_kernel;";
     } else {
         out += "chain_bwd_kernel<" + std::to_string(P.chain_bwd_waves) + ", " +
                std::to_string(P.chain_bpl) + ">;";
+        if (L.totals) out += "band_totals_kernel<" + std::to_string(kBwdWaves) + ", 1>;";
         out += std::string("stft_bwd_kernel<") + bwd_real + ", " + std::to_string(L.bwd_fpw) + ">;";
         scan_kernel_names(P.bwd_scan, "PipeBwdMode", out);
     }
@@ -1673,6 +1734,12 @@ extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, 
         PESQ_CHECK_LAUNCH("pipeline stft");
     }
     if (stages & 8u) {
+        if (L.totals) {
+            hipLaunchKernelGGL((band_totals_kernel<kChainSlices, 2>),
+                               dim3(static_cast<unsigned>(batch)), dim3(kWave * kChainSlices), 0,
+                               stream, a);
+            PESQ_CHECK_LAUNCH("pipeline band totals");
+        }
         launch_chain_fwd(a, static_cast<unsigned>(batch * L.ntile), stream);
         PESQ_CHECK_LAUNCH("pipeline chain");
     }
@@ -1726,6 +1793,12 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
         PESQ_CHECK_LAUNCH("pipeline chain backward");
     }
     if (stages & 2u) {
+        if (L.totals) {
+            hipLaunchKernelGGL((band_totals_kernel<kBwdWaves, 1>),
+                               dim3(static_cast<unsigned>(batch)), dim3(kWave * kBwdWaves), 0,
+                               stream, a);
+            PESQ_CHECK_LAUNCH("pipeline gradient totals");
+        }
         const dim3 grid(static_cast<unsigned>(L.nrg * L.nhoptile));
         if (L.bwd_fpw == 2) {
             hipLaunchKernelGGL((stft_bwd_kernel<StftBwdReal, 2>), grid, dim3(kWave * kBwdWaves), 0,

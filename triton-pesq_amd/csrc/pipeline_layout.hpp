@@ -22,6 +22,11 @@ constexpr int kBwdWaves = 8;       // wavefronts per workgroup of the fused STFT
 #define PESQ_WIDE_TILES 512
 #endif
 constexpr int64_t kWideTiles = PESQ_WIDE_TILES;
+// Items of more chain tiles than this sum their per tile band partials once
+// per item (band_totals_kernel) instead of in every workgroup that reads them
+// (the chain forward's and the STFT backward's, whose reads then grow with
+// the square of the item length).
+constexpr int64_t kTotalsTiles = 64;
 constexpr int kWin = 20;           // PSQM window (frames)
 constexpr int kStride = 10;        // PSQM stride (frames)
 
@@ -41,13 +46,16 @@ struct PipeLayout {
     int nb = kBands;            // Bark bands (the stand-alone chain takes 1 .. 128)
     int loud_store = 0;         // the forward writes the `loud` region (a backward follows)
     int bwd_fpw = 1;            // frames per wavefront of the fused STFT backward (1 or 2)
+    int totals = 0;             // per item band totals (items of more than kTotalsTiles tiles)
 
     // forward workspace
     size_t aggr = 0, energy = 0, p = 0, f = 0, rowconst = 0, bark = 0, keep = 0;
     size_t bandref = 0, banddeg = 0, frame = 0, band = 0, psqm = 0, dist = 0, loud = 0;
+    size_t bandtot = 0;  // [batch, 2, nb] totals of bandref, banddeg (with `totals`)
     size_t fwd_bytes = 0;
     // backward workspace
     size_t gbark = 0, grpart = 0, gp = 0, spart = 0, aggr_b = 0, bwd_bytes = 0;
+    size_t gradtot = 0;  // [batch, nb] totals of grpart (with `totals`)
 
     static size_t align(size_t v) { return (v + 255) & ~size_t(255); }
 
@@ -66,6 +74,7 @@ struct PipeLayout {
         nblk = cdiv(n, kBlockSpan);
         ntile = cdiv(frames, kTile);
         bwd_fpw = b * ntile > kWideTiles ? 2 : 1;
+        totals = ntile > kTotalsTiles;
         nhoptile = cdiv(cdiv(n, kHop), kBwdWaves * bwd_fpw - 1);
         nwin = frames >= kWin ? (frames - kWin) / kStride + 1 : 0;
         row0 = (mask & PESQ_GRAD_REF) ? 0 : b;
@@ -91,6 +100,7 @@ struct PipeLayout {
         take(dist, size_t(batch) * 2 * sizeof(double));
         loud_store = mask != 0;
         take(loud, loud_store ? size_t(kLoudArrays) * batch * frames * nb * sizeof(double) : 0);
+        take(bandtot, totals ? size_t(2) * batch * nb * sizeof(double) : 0);
         fwd_bytes = off;
 
         off = 0;
@@ -99,6 +109,7 @@ struct PipeLayout {
         take(gp, size_t(nrg) * len * sizeof(float));
         take(spart, size_t(nrg) * nhoptile * sizeof(double));
         take(aggr_b, size_t(scan_workspace_doubles(nrg, nblk, kPipeSections)) * sizeof(double));
+        take(gradtot, totals ? size_t(batch) * nb * sizeof(double) : 0);
         bwd_bytes = off;
     }
 
