@@ -630,8 +630,25 @@ __global__ void __launch_bounds__(kWave)
 }
 
 // Exclusive scan of the block aggregates, one (row, section) sequence per
-// wavefront; aggr[b] is replaced by the state at the start of block b.
+// wavefront; aggr[b] is replaced by the state at the start of block b
+// (s_{b+1} = M s_b + e_b, M = A^1024 the block transfer, e_b the aggregate).
+// Lane l owns the per = ceil(nblk / 64) consecutive blocks l per .. l per +
+// per - 1: it runs them from a zero start (its chunk total), a Kogge-Stone
+// scan over the lanes with the chunk transfer P = M^per and its squares gives
+// every chunk's start state, and the lane runs its blocks again from there,
+// storing each block's start.  The serial depth is 2 per + 6 steps (a scan
+// over groups of 64 blocks with a carry between them waits out a memory round
+// trip per group: 14.4 us per pass at c4, 938 blocks per row).
 constexpr int kPrefixWaves = 4;
+
+struct Mat2 {
+    double a, b, c, d;  // row major
+};
+
+__device__ __forceinline__ Mat2 mat2_mul(const Mat2 &x, const Mat2 &y) {
+    return {fma(x.a, y.a, x.b * y.c), fma(x.a, y.b, x.b * y.d), fma(x.c, y.a, x.d * y.c),
+            fma(x.c, y.b, x.d * y.d)};
+}
 
 template <int NS>
 __global__ void __launch_bounds__(kWave *kPrefixWaves)
@@ -643,40 +660,50 @@ __global__ void __launch_bounds__(kWave *kPrefixWaves)
     if (seq >= nseq) return;  // whole wavefronts only
     const int k = static_cast<int>(seq % NS);
     const int lane = threadIdx.x % kWave;
-    double *agg = aggr + seq * nblk * 2;
-    double cu = 0.0, cv = 0.0;  // carry: state at the end of block base - 1
-    for (int base = 0; base < nblk; base += kWave) {
-        const int jb = base + lane;
-        const int jc = jb < nblk ? jb : nblk - 1;
-        double u = agg[2 * jc], v = agg[2 * jc + 1];
-        if (jb >= nblk) u = v = 0.0;
-        if (lane == 0) {
-            const double *p = t.pw[kLevelBlock][k];
-            u = fma(p[0], cu, fma(p[1], cv, u));
-            v = fma(p[2], cu, fma(p[3], cv, v));
-        }
+    double2 *agg = reinterpret_cast<double2 *>(aggr + seq * nblk * 2);
+    const double *pm = t.pw[kLevelBlock][k];
+    const Mat2 m{pm[0], pm[1], pm[2], pm[3]};
+    const int per = (nblk + kWave - 1) / kWave;
+    const int j0 = lane * per;
+    const int j1 = j0 + per < nblk ? j0 + per : nblk;
+    // the chunk's end state from a zero start
+    double tu = 0.0, tv = 0.0;
+#pragma unroll 4
+    for (int j = j0; j < j1; ++j) {
+        const double2 e = agg[j];
+        const double u = fma(m.a, tu, fma(m.b, tv, e.x));
+        const double v = fma(m.c, tu, fma(m.d, tv, e.y));
+        tu = u;
+        tv = v;
+    }
+    // P = M^per, square and multiply
+    Mat2 q{1.0, 0.0, 0.0, 1.0}, sq = m;
+    for (int e = per; e != 0; e >>= 1) {
+        if (e & 1) q = mat2_mul(q, sq);
+        sq = mat2_mul(sq, sq);
+    }
+    // inclusive scan of the chunk ends over the lanes, level j with P^(2^j)
 #pragma unroll
-        for (int j = 0; j < 6; ++j) {
-            const int d = 1 << j;
-            const double ou = shfl_up(u, d), ov = shfl_up(v, d);
-            if (lane >= d) {
-                const double *p = t.pw[kLevelBlock + j][k];
-                u = fma(p[0], ou, fma(p[1], ov, u));
-                v = fma(p[2], ou, fma(p[3], ov, v));
-            }
+    for (int j = 0; j < 6; ++j) {
+        const int d = 1 << j;
+        const double ou = shfl_up(tu, d), ov = shfl_up(tv, d);
+        if (lane >= d) {
+            tu = fma(q.a, ou, fma(q.b, ov, tu));
+            tv = fma(q.c, ou, fma(q.d, ov, tv));
         }
-        double eu = shfl_up(u, 1), ev = shfl_up(v, 1);
-        if (lane == 0) {
-            eu = cu;
-            ev = cv;
-        }
-        if (jb < nblk) {
-            agg[2 * jb] = eu;
-            agg[2 * jb + 1] = ev;
-        }
-        const int src = (nblk - base < kWave ? nblk - base : kWave) - 1;
-        cu = shfl(u, src);
-        cv = shfl(v, src);
+        q = mat2_mul(q, q);
+    }
+    // the lane's start state is the end state of the chunks before it
+    double su = shfl_up(tu, 1), sv = shfl_up(tv, 1);
+    if (lane == 0) su = sv = 0.0;
+#pragma unroll 4
+    for (int j = j0; j < j1; ++j) {
+        const double2 e = agg[j];
+        agg[j] = make_double2(su, sv);
+        const double u = fma(m.a, su, fma(m.b, sv, e.x));
+        const double v = fma(m.c, su, fma(m.d, sv, e.y));
+        su = u;
+        sv = v;
     }
 }
 
