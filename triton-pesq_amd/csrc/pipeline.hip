@@ -516,10 +516,20 @@ __global__ void __launch_bounds__(kWave *kSlices) band_totals_kernel(PipeArgs a)
         dst = region<double>(a.bw, L.gradtot) + int64_t(item) * kBands;
     }
     if (lane < kBands) {
+        // the slice's tiles wave, wave + kSlices, ... of every array, with the
+        // loads of all arrays in flight together, 8 per array at a time
+        const double *ptr[kArrays];
+        int cnt[kArrays];
+        const int n = L.ntile > wave ? static_cast<int>((L.ntile - 1 - wave) / kSlices) + 1 : 0;
 #pragma unroll
         for (int k = 0; k < kArrays; ++k) {
-            part[k][wave][lane] = tile_partial(src[k], L.ntile, wave, kSlices, lane, kBands);
+            ptr[k] = src[k] + int64_t(wave) * kBands + lane;
+            cnt[k] = n;
         }
+        double sums[kArrays];
+        strided_sums<kArrays, 8>(ptr, cnt, int64_t(kSlices) * kBands, sums);
+#pragma unroll
+        for (int k = 0; k < kArrays; ++k) part[k][wave][lane] = sums[k];
     }
     __syncthreads();
     if (wave == 0 && lane < kBands) {
@@ -780,14 +790,21 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
 // 5. overlapping sums, distances, MOS and loss, one workgroup per item
 // ---------------------------------------------------------------------------
 
-constexpr int kFinalThreads = 256;
+constexpr int kFinalMaxThreads = 1024;
+
+// Threads per workgroup of chain_final_kernel: one PSQM window per thread up to
+// 1024 windows (a second window per thread doubles the kernel's latency), at
+// least 256.
+static unsigned final_threads(int64_t nwin) {
+    return nwin <= 256 ? 256u : (nwin <= 512 ? 512u : 1024u);
+}
 
 // both frame arrays (symmetric, asymmetric) in the same pass over the PSQM
 // windows, so that their loads, powers and block sums overlap; each sum is
 // per wave (wave_sum), then over the waves in order
-__global__ void __launch_bounds__(kFinalThreads) chain_final_kernel(PipeArgs a) {
-    constexpr int kFinalWaves = kFinalThreads / kWave;
-    __shared__ double scratch[2][kFinalWaves];
+__global__ void __launch_bounds__(kFinalMaxThreads) chain_final_kernel(PipeArgs a) {
+    __shared__ double scratch[2][kFinalMaxThreads / kWave];
+    const int waves = static_cast<int>(blockDim.x) / kWave;
     const PipeLayout &L = a.L;
     const int item = blockIdx.x;
     const double *s0 = frame_array(a, kSymm) + int64_t(item) * L.frames;
@@ -820,7 +837,7 @@ __global__ void __launch_bounds__(kFinalThreads) chain_final_kernel(PipeArgs a) 
     }
     __syncthreads();
     double d[2] = {0.0, 0.0};
-    for (int i = 0; i < kFinalWaves; ++i) {
+    for (int i = 0; i < waves; ++i) {
         d[0] += scratch[0][i];
         d[1] += scratch[1][i];
     }
@@ -1745,7 +1762,7 @@ extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, 
     }
     if (stages & 16u) {
         hipLaunchKernelGGL(chain_final_kernel, dim3(static_cast<unsigned>(batch)),
-                           dim3(kFinalThreads), 0, stream, a);
+                           dim3(final_threads(L.nwin)), 0, stream, a);
         PESQ_CHECK_LAUNCH("pipeline chain final");
     }
     return PESQ_OK;
@@ -1896,8 +1913,8 @@ extern "C" int pesq_chain_forward(const float *ref_bark, const float *deg_bark, 
     PESQ_CHECK_LAUNCH("chain partials");
     launch_chain_fwd(a, grid, stream);
     PESQ_CHECK_LAUNCH("chain");
-    hipLaunchKernelGGL(chain_final_kernel, dim3(static_cast<unsigned>(batch)), dim3(kFinalThreads),
-                       0, stream, a);
+    hipLaunchKernelGGL(chain_final_kernel, dim3(static_cast<unsigned>(batch)),
+                       dim3(final_threads(a.L.nwin)), 0, stream, a);
     PESQ_CHECK_LAUNCH("chain final");
     return PESQ_OK;
 }
