@@ -640,6 +640,7 @@ __global__ void __launch_bounds__(kWave)
 // over groups of 64 blocks with a carry between them waits out a memory round
 // trip per group: 14.4 us per pass at c4, 938 blocks per row).
 constexpr int kPrefixWaves = 4;
+constexpr int kPrefixHeld = 16;  // aggregates a lane keeps in registers
 
 struct Mat2 {
     double a, b, c, d;  // row major
@@ -666,10 +667,27 @@ __global__ void __launch_bounds__(kWave *kPrefixWaves)
     const int per = (nblk + kWave - 1) / kWave;
     const int j0 = lane * per;
     const int j1 = j0 + per < nblk ? j0 + per : nblk;
+    // the chunk's first kPrefixHeld aggregates stay in registers for both
+    // runs (one memory round trip for chunks of up to kPrefixHeld blocks)
+    double2 held[kPrefixHeld];
+#pragma unroll
+    for (int i = 0; i < kPrefixHeld; ++i) {
+        const int j = j0 + i < j1 ? j0 + i : (j1 > 0 ? j1 - 1 : 0);
+        held[i] = agg[j];
+    }
     // the chunk's end state from a zero start
     double tu = 0.0, tv = 0.0;
+#pragma unroll
+    for (int i = 0; i < kPrefixHeld; ++i) {
+        if (j0 + i < j1) {
+            const double u = fma(m.a, tu, fma(m.b, tv, held[i].x));
+            const double v = fma(m.c, tu, fma(m.d, tv, held[i].y));
+            tu = u;
+            tv = v;
+        }
+    }
 #pragma unroll 4
-    for (int j = j0; j < j1; ++j) {
+    for (int j = j0 + kPrefixHeld; j < j1; ++j) {
         const double2 e = agg[j];
         const double u = fma(m.a, tu, fma(m.b, tv, e.x));
         const double v = fma(m.c, tu, fma(m.d, tv, e.y));
@@ -696,8 +714,18 @@ __global__ void __launch_bounds__(kWave *kPrefixWaves)
     // the lane's start state is the end state of the chunks before it
     double su = shfl_up(tu, 1), sv = shfl_up(tv, 1);
     if (lane == 0) su = sv = 0.0;
+#pragma unroll
+    for (int i = 0; i < kPrefixHeld; ++i) {
+        if (j0 + i < j1) {
+            agg[j0 + i] = make_double2(su, sv);
+            const double u = fma(m.a, su, fma(m.b, sv, held[i].x));
+            const double v = fma(m.c, su, fma(m.d, sv, held[i].y));
+            su = u;
+            sv = v;
+        }
+    }
 #pragma unroll 4
-    for (int j = j0; j < j1; ++j) {
+    for (int j = j0 + kPrefixHeld; j < j1; ++j) {
         const double2 e = agg[j];
         agg[j] = make_double2(su, sv);
         const double u = fma(m.a, su, fma(m.b, sv, e.x));
