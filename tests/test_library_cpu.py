@@ -351,7 +351,7 @@ VARIANTS = {
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, true>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
-        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1>",
+        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, true>"],
     ),
@@ -362,7 +362,7 @@ VARIANTS = {
          "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
          "stft_fwd_kernel<float, true, 8>", "band_totals_kernel<16, 2>",
          "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
-        ["chain_bwd_kernel<4, 1>", "band_totals_kernel<8, 1>", "stft_bwd_kernel<float, 2>",
+        ["chain_bwd_kernel<4, 1>", "band_totals_kernel<8, 1>", "stft_bwd_kernel<float, 2, 8>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
     ),
@@ -373,7 +373,7 @@ VARIANTS = {
          "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
          "stft_fwd_kernel<float, false, 8>", "band_totals_kernel<16, 2>",
          "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
-        ["chain_bwd_kernel<16, 1>", "band_totals_kernel<8, 1>", "stft_bwd_kernel<float, 1>",
+        ["chain_bwd_kernel<16, 1>", "band_totals_kernel<9, 1>", "stft_bwd_kernel<float, 1, 9>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
     ),
@@ -382,7 +382,7 @@ VARIANTS = {
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
-        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1>",
+        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
     ),
@@ -392,7 +392,7 @@ VARIANTS = {
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, false>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeFwdMode, false, false>",
          "stft_fwd_kernel<float, true, 8>", "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
-        ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float, 2>",
+        ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float, 2, 8>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, false>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, false, false>"],
     ),
@@ -401,7 +401,7 @@ VARIANTS = {
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, true>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, true>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
-        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1>",
+        ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, true>"],
     ),

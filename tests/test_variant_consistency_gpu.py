@@ -3,7 +3,8 @@
 The pipeline picks its kernels by grid size (``pesq_pipeline_kernels``): a
 batch of eighteen 30 s items runs the large-grid variants (the scans recompute
 the lane states, the STFT forward takes its lean form, the chain kernels four
-frames per wavefront, the STFT backward two frames per wavefront), while the
+frames per wavefront, the STFT backward two frames per wavefront in eight
+wavefronts instead of one in nine), while the
 same items one at a time run the small-grid ones.  Batch items are scored
 independently, so both must give the same losses and gradients up to
 rounding.  Measured: the losses agree bitwise and so do the scans' outputs
@@ -49,7 +50,7 @@ def test_large_grid_variants_match_small_grid_ones():
     assert "chain_fwd_kernel<4, 1>" in wide and "chain_fwd_kernel<8, 1>" in narrow
     assert "iir_output_kernel<5, 1, PipeFwdMode, false, false>" in wide
     assert "iir_output_kernel<5, 1, PipeFwdMode, true, false>" in narrow
-    assert "stft_bwd_kernel<float, 2>" in wide_b and "stft_bwd_kernel<float, 1>" in narrow_b
+    assert "stft_bwd_kernel<float, 2, 8>" in wide_b and "stft_bwd_kernel<float, 1, 9>" in narrow_b
     assert "chain_bwd_kernel<4, 1>" in wide_b and "chain_bwd_kernel<16, 1>" in narrow_b
     assert "iir_output_kernel<5, 1, PipeBwdMode, false, false>" in wide_b
     assert "iir_output_kernel<5, 1, PipeBwdMode, true, false>" in narrow_b

@@ -1131,22 +1131,27 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
 }
 
 // ---------------------------------------------------------------------------
-// 7. STFT backward per (grad row, kBwdWaves kFPW - 1 hop blocks)
+// 7. STFT backward per (grad row, kW kFPW - 1 hop blocks)
 // ---------------------------------------------------------------------------
 
-// kFPW frames per wavefront: wavefront w transforms the workgroup's frames w,
-// w + kBwdWaves, ...  (1 for small grids; 2 for large ones, which halves the
-// per workgroup table staging and band sums per frame and the frames shared
-// by two workgroups).  The sums are taken in the same order either way.
-template <typename real, int kFPW>
-__global__ void __launch_bounds__(kWave *kBwdWaves, 5) stft_bwd_kernel(PipeArgs a) {
-    constexpr int kFrames = kBwdWaves * kFPW;  // frames per workgroup
+// kW wavefronts of kFPW frames each: wavefront w transforms the workgroup's
+// frames w, w + kW, ...  Small grids take one frame per wavefront and nine
+// wavefronts (at c2 the 504 workgroups of 9 all fit on the chip at once, two
+// per CU, where 576 of 8 do not: 10.2 against 11.4 us; 448 of 10, 10.7 us);
+// large ones two frames per wavefront and eight wavefronts,
+// which halves the per workgroup table staging and band sums per frame and
+// the frames shared by two workgroups.  The sums are taken in the same order
+// for every kFPW; kW sets the split of the band gradient totals and of the
+// partials of S.
+template <typename real, int kFPW, int kW>
+__global__ void __launch_bounds__(kWave *kW, 5) stft_bwd_kernel(PipeArgs a) {
+    constexpr int kFrames = kW * kFPW;  // frames per workgroup
     constexpr int kHops = kFrames - 1;         // output hop blocks per workgroup
-    __shared__ cplx<real> fftbuf[kBwdWaves][kHalf];
+    __shared__ cplx<real> fftbuf[kW][kHalf];
     __shared__ float contrib[kFrames][kNfft];
-    __shared__ double gpart[kBwdWaves][kBands];
-    __shared__ float gband[kBwdWaves][kBands];
-    __shared__ double scratch[kBwdWaves];
+    __shared__ double gpart[kW][kBands];
+    __shared__ float gband[kW][kBands];
+    __shared__ double scratch[kW];
     // the twiddle tables, window and bin-to-band map, staged once per
     // workgroup (both FFTs of every frame read them)
     using T2 = typename Vec2<real>::type;
@@ -1171,7 +1176,7 @@ __global__ void __launch_bounds__(kWave *kBwdWaves, 5) stft_bwd_kernel(PipeArgs 
     float smp[kFPW][8], bk_v[kFPW], gbk_v[kFPW], keep[kFPW];
 #pragma unroll
     for (int f = 0; f < kFPW; ++f) {
-        const int64_t frame = j0 - 1 + wave + kBwdWaves * f;
+        const int64_t frame = j0 - 1 + wave + kW * f;
         const int64_t fc = frame < 0 ? 0 : (frame >= L.frames ? L.frames - 1 : frame);
         load_frame(p, fc * kHop, L.len, lane, smp[f]);
         const int64_t fo = fc * kBands;
@@ -1181,13 +1186,13 @@ __global__ void __launch_bounds__(kWave *kBwdWaves, 5) stft_bwd_kernel(PipeArgs 
     }
 
     // adjoint of the band power ratio and its clamp, then of the mean band
-    // powers: wavefront w sums the band partials of tiles w, w + kBwdWaves, ...
+    // powers: wavefront w sums the band partials of tiles w, w + kW, ...
     // and every wavefront adds the partial sums in wavefront order
     const double *grp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
     if (lane < kBands && !L.totals) {
-        gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kBwdWaves, lane, kBands);
+        gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kW, lane, kBands);
     }
-    for (int k = threadIdx.x; k < kNfft; k += kWave * kBwdWaves) {
+    for (int k = threadIdx.x; k < kNfft; k += kWave * kW) {
         if (k < kPassTwiddles) lds_pass[k] = StagedTwiddles<real>::pass(t)[k];
         if (k < kHalf) {
             lds_tw512[k] = StagedTwiddles<real>::fold(t)[k];
@@ -1202,7 +1207,7 @@ __global__ void __launch_bounds__(kWave *kBwdWaves, 5) stft_bwd_kernel(PipeArgs 
         if (L.totals) {
             g = region<double>(a.bw, L.gradtot)[int64_t(item) * kBands + lane];
         } else {
-            for (int w = 0; w < kBwdWaves; ++w) g += gpart[w][lane];
+            for (int w = 0; w < kW; ++w) g += gpart[w][lane];
         }
         const double ratio = band_array(a, kRatio)[item * kBands + lane];
         const double mref = band_array(a, kMref)[item * kBands + lane];
@@ -1229,7 +1234,7 @@ __global__ void __launch_bounds__(kWave *kBwdWaves, 5) stft_bwd_kernel(PipeArgs 
     }
 #pragma unroll
     for (int f = 0; f < kFPW; ++f) {
-        const int local = wave + kBwdWaves * f;
+        const int local = wave + kW * f;
         const int64_t frame = j0 - 1 + local;
         if (frame < 0 || frame >= L.frames) {
             for (int k = lane; k < kNfft; k += kWave) contrib[local][k] = 0.0f;
@@ -1301,7 +1306,7 @@ __global__ void __launch_bounds__(kWave *kBwdWaves, 5) stft_bwd_kernel(PipeArgs 
     __syncthreads();
     if (threadIdx.x == 0) {
         double sum = 0.0;
-        for (int w = 0; w < kBwdWaves; ++w) sum += scratch[w];
+        for (int w = 0; w < kW; ++w) sum += scratch[w];
         region<double>(a.bw, L.spart)[int64_t(i) * L.nhoptile + ht] = sum;
     }
 }
@@ -1681,8 +1686,9 @@ extern "C" int pesq_pipeline_kernels(int64_t batch, int64_t len, int grad_mask, 
     } else {
         out += "chain_bwd_kernel<" + std::to_string(P.chain_bwd_waves) + ", " +
                std::to_string(P.chain_bpl) + ">;";
-        if (L.totals) out += "band_totals_kernel<" + std::to_string(kBwdWaves) + ", 1>;";
-        out += std::string("stft_bwd_kernel<") + bwd_real + ", " + std::to_string(L.bwd_fpw) + ">;";
+        if (L.totals) out += "band_totals_kernel<" + std::to_string(L.bwd_waves) + ", 1>;";
+        out += std::string("stft_bwd_kernel<") + bwd_real + ", " + std::to_string(L.bwd_fpw) +
+               ", " + std::to_string(L.bwd_waves) + ">;";
         scan_kernel_names(P.bwd_scan, "PipeBwdMode", out);
     }
     out.pop_back();  // the last ';'
@@ -1811,18 +1817,22 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
     }
     if (stages & 2u) {
         if (L.totals) {
-            hipLaunchKernelGGL((band_totals_kernel<kBwdWaves, 1>),
-                               dim3(static_cast<unsigned>(batch)), dim3(kWave * kBwdWaves), 0,
-                               stream, a);
+            const dim3 tgrid(static_cast<unsigned>(batch)), tblock(kWave * L.bwd_waves);
+            if (L.bwd_waves == kBwdWaves) {
+                hipLaunchKernelGGL((band_totals_kernel<kBwdWaves, 1>), tgrid, tblock, 0, stream, a);
+            } else {
+                hipLaunchKernelGGL((band_totals_kernel<kBwdWavesSmall, 1>), tgrid, tblock, 0,
+                                   stream, a);
+            }
             PESQ_CHECK_LAUNCH("pipeline gradient totals");
         }
         const dim3 grid(static_cast<unsigned>(L.nrg * L.nhoptile));
         if (L.bwd_fpw == 2) {
-            hipLaunchKernelGGL((stft_bwd_kernel<StftBwdReal, 2>), grid, dim3(kWave * kBwdWaves), 0,
-                               stream, a);
+            hipLaunchKernelGGL((stft_bwd_kernel<StftBwdReal, 2, kBwdWaves>), grid,
+                               dim3(kWave * kBwdWaves), 0, stream, a);
         } else {
-            hipLaunchKernelGGL((stft_bwd_kernel<StftBwdReal, 1>), grid, dim3(kWave * kBwdWaves), 0,
-                               stream, a);
+            hipLaunchKernelGGL((stft_bwd_kernel<StftBwdReal, 1, kBwdWavesSmall>), grid,
+                               dim3(kWave * kBwdWavesSmall), 0, stream, a);
         }
         PESQ_CHECK_LAUNCH("pipeline stft backward");
     }

@@ -15,7 +15,11 @@ constexpr int kPipeSections = kPowerSections + kPreSections;  // scanned in one 
 constexpr int kTile = 16;          // frames per workgroup of the STFT / chain kernels
 constexpr int kBwdFrames = 8;      // frames per workgroup of the plain STFT backward
 constexpr int kBwdHops = kBwdFrames - 1;  // output hop blocks per such workgroup
-constexpr int kBwdWaves = 8;       // wavefronts per workgroup of the fused STFT backward
+constexpr int kBwdWaves = 8;       // wavefronts per workgroup of the fused STFT backward (large grids)
+#ifndef PESQ_BWD_WAVES_SMALL
+#define PESQ_BWD_WAVES_SMALL 9
+#endif
+constexpr int kBwdWavesSmall = PESQ_BWD_WAVES_SMALL;  // and of small grids (one frame each)
 // Grids of more chain tiles (batch x ntile) than this are throughput bound:
 // the kernels take their wide variants (more frames per wavefront).
 #ifndef PESQ_WIDE_TILES
@@ -46,6 +50,7 @@ struct PipeLayout {
     int nb = kBands;            // Bark bands (the stand-alone chain takes 1 .. 128)
     int loud_store = 0;         // the forward writes the `loud` region (a backward follows)
     int bwd_fpw = 1;            // frames per wavefront of the fused STFT backward (1 or 2)
+    int bwd_waves = kBwdWaves;  // wavefronts per workgroup of the fused STFT backward
     int totals = 0;             // per item band totals (items of more than kTotalsTiles tiles)
 
     // forward workspace
@@ -75,7 +80,8 @@ struct PipeLayout {
         ntile = cdiv(frames, kTile);
         bwd_fpw = b * ntile > kWideTiles ? 2 : 1;
         totals = ntile > kTotalsTiles;
-        nhoptile = cdiv(cdiv(n, kHop), kBwdWaves * bwd_fpw - 1);
+        bwd_waves = bwd_fpw == 2 ? kBwdWaves : kBwdWavesSmall;
+        nhoptile = cdiv(cdiv(n, kHop), bwd_waves * bwd_fpw - 1);
         nwin = frames >= kWin ? (frames - kWin) / kStride + 1 : 0;
         row0 = (mask & PESQ_GRAD_REF) ? 0 : b;
         nrg = mask == (PESQ_GRAD_REF | PESQ_GRAD_DEG) ? 2 * b : (mask ? b : 0);
