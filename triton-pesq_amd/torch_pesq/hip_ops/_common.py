@@ -28,5 +28,5 @@ def check_input(tensor: torch.Tensor, name: str = "input") -> torch.Tensor:
         raise RuntimeError(f"The HIP backend needs `{name}` to live on a GPU.")
     if tensor.dtype != torch.float32:
         raise RuntimeError(f"The HIP backend only supports float32, `{name}` is {tensor.dtype}.")
-    require_hip()
+    _lib.library()  # a GPU tensor means a visible GPU; this loads (once) the HIP library
     return tensor.contiguous()
