@@ -55,8 +55,11 @@ def test_forward_and_adjoint(name, length):
 
 
 # up to 128 blocks the output kernel scans the preceding block aggregates
-# itself (in groups of 64 blocks); longer rows go through the prefix kernel
-@pytest.mark.parametrize("length", [65537, 128000, 131072, 132097, 960000])
+# itself (in groups of 64 blocks); longer rows go through the prefix kernel,
+# whose lanes take ceil(blocks / 64) consecutive blocks each: 3 at 132097
+# samples (130 blocks: a partial lane, then empty ones), 15 at 960000 (all
+# held in registers), 23 at 1.5 M (past the 16 a lane holds)
+@pytest.mark.parametrize("length", [65537, 128000, 131072, 132097, 960000, 1_500_000])
 def test_long_signals(length):
     b, a = FILTERS["power"]
     mod = HipIIR(b, a).cuda()
