@@ -29,9 +29,27 @@ How each part is pinned (``tests/test_oracle.py``):
 * ``stft_bark``: a direct float64 DFT on short inputs, the frame count known
   answer (4000 samples -> 14 frames, ``test_triton_spectral.py:397-412``) and
   finite differences;
-* chain: the identical-input known answer (``1e-20 / h`` floor,
-  ``test_triton_chain.py:365-383``), a float64 finite difference check of the
-  autograd gradient, and a pure-Python loop evaluation on a tiny spectrum;
+* formula constants: every scalar of the formulas lives in :data:`FORMULA`,
+  which must equal, name by name, the literals ``tests/golden/make_tables.py``
+  parses from the reference's statements (``loss.py``, ``loudness.py``,
+  ``bark.py``, ``triton_ops/reference.py``); no other numeric literal than a
+  structural 0, 1 or 2 appears in the formula functions;
+* chain, step by step, against closed-form consequences that a misread
+  constant or a misplaced term fails (each test also plants such a mistake and
+  sees it fail): the loudness law's zero at the threshold, its ``sl x^e``
+  asymptote and its slope above the threshold; the dead zone's
+  ``0.75 L_ref`` / ``0`` / ``-0.375 L_ref`` answers; the silence decision and
+  the all-frame band means; the band and frame ratios' offsets, smoothing and
+  clamps; the asymmetry factor at ``2.5^1.2`` and its cut and cap; ``h(0) =
+  0.01^0.04`` (the 0.83175 of ``test_triton_chain.py:725-750``); the norms'
+  absolute scale ``sqrt(W) w_k |d|`` and ``w_k |d|``; the overlapping sums of
+  one non-zero frame ``v 20^(-1/6) sqrt(m / nwin)``; whole-chain distances of
+  constant single-band spectra in closed form; plus the identical-input known
+  answer (``1e-20 / h`` floor, ``test_triton_chain.py:365-383``), a float64
+  finite difference check of the autograd gradient, and a pure-Python loop
+  evaluation on a tiny spectrum;
+* epilogue: values evaluated by hand from the published ITU-T P.862 raw score
+  and P.862.2 wideband mapping (4.6439 at zero disturbance);
 * pipeline: scale invariance (``test_triton_elementwise.py:1396-1450``),
   batch independence, ``loss(ref, ref) ~ 0`` (``test_torch.py:18-27``);
 * resampler taps: width / length known answers of
@@ -54,8 +72,82 @@ from scipy.signal import butter, lfilter as scipy_lfilter
 ROOT = Path(__file__).resolve().parents[1]
 TABLES = json.loads((ROOT / "tests" / "golden" / "tables.json").read_text())
 
-SL = 0.1866055  # torch_pesq/triton_ops/reference.py:322
-WINDOW, STRIDE = 20, 10  # torch_pesq/loss.py:291-298
+#: Every scalar constant of the loss's formulas, typed from a reading of the
+#: reference (the line each is read from).  ``tests/test_oracle.py`` checks
+#: this dict, key by key, against the values ``tests/golden/make_tables.py``
+#: parses from the reference's source text, and the functions below read
+#: their constants only from here.
+FORMULA = {
+    # level alignment, torch_pesq/loss.py:132-139
+    "align_pad": 5120,
+    "align_divisor": 1.04684,
+    "align_target_base": 10,
+    "align_target_exponent": 7,
+    # edge ramp, torch_pesq/loss.py:163-165
+    "ramp_length": 15,
+    "ramp_points": 16,
+    "ramp_divisor": 16.0,
+    # N % 256 padding, torch_pesq/loss.py:191-192
+    "pad_multiple": 256,
+    # silent frames and band means, loss.py:206, loudness.py:102
+    "silent_threshold_factor": 100.0,
+    "silent_energy": 1e7,
+    "mean_threshold_factor": 100.0,
+    # band power ratio, loss.py:212-216
+    "band_ratio_offset": 1000,
+    "band_ratio_min": 0.01,
+    "band_ratio_max": 100.0,
+    # frame power ratio, loss.py:220-228
+    "total_threshold_factor": 1,
+    "frame_ratio_offset": 5e3,
+    "frame_smooth_current": 0.8,
+    "frame_smooth_previous": 0.2,
+    "frame_ratio_min": 3e-4,
+    "frame_ratio_max": 5.0,
+    # Zwicker loudness, loudness.py:124-129 and its exponents, loudness.py:52-55
+    "loudness_threshold_scale": 2.0,
+    "loudness_half": 0.5,
+    "loudness_one": 1,
+    "loudness_below_threshold": 0.0,
+    "exponent_numerator": 6,
+    "exponent_offset": 2.0,
+    "exponent_min": 1.0,
+    "exponent_max": 2.0,
+    "exponent_power": 0.15,
+    # disturbance and its norms, loss.py:235-249, bark.py:193-195
+    "deadzone": 0.25,
+    "symm_norm_p": 2,
+    "asymm_norm_p": 1,
+    "norm_first_band": 1,
+    "distance_floor": 1e-20,
+    "asymm_offset": 50.0,
+    "asymm_exponent": 1.2,
+    "asymm_cut": 3.0,
+    "asymm_cut_value": 0.0,
+    "asymm_cap": 12.0,
+    # frame weighting and cap, loss.py:252-253
+    "h_offset": 1e5,
+    "h_scale": 1e7,
+    "h_exponent": 0.04,
+    "distance_cap": 45.0,
+    # overlapping sums, loss.py:256-266
+    "psqm_window": 20,
+    "psqm_stride": 10,
+    "psqm_power": 6,
+    # MOS and loss, loss.py:292-295,322
+    "pesq_offset": 4.5,
+    "pesq_symm_weight": 0.1,
+    "pesq_asymm_weight": 0.0309,
+    "mos_floor": 0.999,
+    "mos_span": 4,
+    "mos_slope": 1.3669,
+    "mos_shift": 3.8224,
+    # loudness calibration passed to the chain, triton_ops/reference.py:315-322
+    "sl": 0.1866055,
+}
+F = FORMULA
+SL = F["sl"]
+WINDOW, STRIDE = F["psqm_window"], F["psqm_stride"]
 
 
 # ---------------------------------------------------------------------------
@@ -153,8 +245,11 @@ def constants(nbarks: int = 49, n_fft: int = 512):
     corr = _interp(TABLES["pow_dens_correction_factor_16k"], nbarks) * TABLES["Sp_16k"]
     threshs = _interp(TABLES["abs_thresh_power_16k"], nbarks)
 
-    exp32 = 6 / (torch.tensor(TABLES["centre_of_band_bark_16k"], dtype=torch.float32) + 2.0)
-    exp32 = exp32.clamp(min=1.0, max=2.0) ** 0.15 * TABLES["zwicker_power"]
+    exp32 = F["exponent_numerator"] / (
+        torch.tensor(TABLES["centre_of_band_bark_16k"], dtype=torch.float32) + F["exponent_offset"]
+    )
+    exp32 = exp32.clamp(min=F["exponent_min"], max=F["exponent_max"]) ** F["exponent_power"]
+    exp32 = exp32 * TABLES["zwicker_power"]
 
     design = TABLES["power_filter_design"]
     pb, pa = butter(design["order"], design["band_hz"], fs=design["fs"], btype="band")
@@ -324,18 +419,21 @@ def align_level(signal: torch.Tensor, c=None) -> torch.Tensor:
 
     c = constants() if c is None else c
     filtered = lfilter(signal, c["power_b"], c["power_a"])
-    power = (filtered**2).sum(dim=1, keepdim=True) / (filtered.shape[1] + 5120) / 1.04684
-    return signal * (10**7 / power).sqrt()
+    power = (filtered**2).sum(dim=1, keepdim=True) / (filtered.shape[1] + F["align_pad"])
+    power = power / F["align_divisor"]
+    target = F["align_target_base"] ** F["align_target_exponent"]
+    return signal * (target / power).sqrt()
 
 
 def edge_ramp(signal: torch.Tensor) -> torch.Tensor:
     """First and last 15 samples times ``k/16``, applied in that order (``loss.py:163-165``)."""
 
-    emp = torch.linspace(0, 15, 16, dtype=torch.float32)[1:] / 16.0
+    n = F["ramp_length"]
+    emp = torch.linspace(0, n, F["ramp_points"], dtype=torch.float32)[1:] / F["ramp_divisor"]
     emp = emp.to(signal.dtype)
     out = signal.clone()
-    out[:, :15] = out[:, :15] * emp
-    out[:, -15:] = out[:, -15:] * torch.flip(emp, dims=(0,))
+    out[:, :n] = out[:, :n] * emp
+    out[:, -n:] = out[:, -n:] * torch.flip(emp, dims=(0,))
     return out
 
 
@@ -349,7 +447,7 @@ def preemphasize(signal: torch.Tensor, c=None) -> torch.Tensor:
 def n_frames(n_samples: int, n_fft: int = 512, hop: int = 256) -> int:
     """Frames after the reference's ``length % 256`` padding (``loss.py:191-192``)."""
 
-    padded = n_samples + n_samples % 256
+    padded = n_samples + n_samples % F["pad_multiple"]
     return 1 + (padded - n_fft) // hop
 
 
@@ -357,7 +455,7 @@ def stft_bark(signal: torch.Tensor, c=None) -> torch.Tensor:
     """Pad by ``N % 256``, float64 STFT, DC dropped, Bark sums (``reference.py:79-127``)."""
 
     c = constants() if c is None else c
-    signal = torch.nn.functional.pad(signal, (0, signal.shape[1] % 256))
+    signal = torch.nn.functional.pad(signal, (0, signal.shape[1] % F["pad_multiple"]))
     spec = torch.stft(
         signal,
         n_fft=c["n_fft"],
@@ -374,63 +472,124 @@ def stft_bark(signal: torch.Tensor, c=None) -> torch.Tensor:
     return bark * c["corr"].to(spec.dtype)
 
 
-def _total_audible(tensor, threshs, factor):
-    return (tensor * (tensor > threshs * factor)).sum(dim=2)
+def total_audible(spec, threshs, factor):
+    """Energy of the bands above ``factor`` times their threshold, per frame
+    (``loudness.py:61-79``)."""
+
+    return (spec * (spec > threshs * factor)).sum(dim=2)
 
 
-def _loudness(pow_dens, threshs, exp, sl):
-    loud = (2.0 * threshs) ** exp * ((0.5 + 0.5 * pow_dens / threshs) ** exp - 1)
-    loud = torch.where(pow_dens <= threshs, torch.zeros_like(loud), loud)
+def silent_frames(ref, threshs):
+    """Frames whose reference energy above ``100 th`` is below ``1e7``
+    (``loss.py:205-206``)."""
+
+    return total_audible(ref, threshs, F["silent_threshold_factor"]) < F["silent_energy"]
+
+
+def band_means(spec, threshs, silent):
+    """Per band mean over *all* frames of the powers above ``100 th`` in the
+    non-silent frames (``loudness.py:82-105``)."""
+
+    mask = (spec > threshs * F["mean_threshold_factor"]) * (~silent.unsqueeze(2))
+    return (spec * mask).mean(dim=1)
+
+
+def band_ratio(mean_ref, mean_deg):
+    """``clamp((m_deg + 1000) / (m_ref + 1000), 0.01, 100)`` per band (``loss.py:212-216``)."""
+
+    off = F["band_ratio_offset"]
+    return ((mean_deg + off) / (mean_ref + off)).clamp(min=F["band_ratio_min"], max=F["band_ratio_max"])
+
+
+def frame_ratio(taer, tad):
+    """Frame power ratio ``(taer + 5e3) / (tad + 5e3)``, smoothed
+    ``0.8 f_t + 0.2 f_(t-1)`` for ``t > 0`` and clamped to ``[3e-4, 5]``
+    (``loss.py:219-228``)."""
+
+    off = F["frame_ratio_offset"]
+    f = (taer + off) / (tad + off)
+    smoothed = f[:, 1:] * F["frame_smooth_current"] + f[:, :-1] * F["frame_smooth_previous"]
+    f = torch.cat([f[:, :1], smoothed], dim=1)
+    return f.clamp(min=F["frame_ratio_min"], max=F["frame_ratio_max"])
+
+
+def loudness(pow_dens, threshs, exp, sl):
+    """Zwicker loudness ``sl (2 th)^e ((0.5 + 0.5 x / th)^e - 1)``, zero where
+    ``x <= th`` (``loudness.py:108-129``)."""
+
+    half = F["loudness_half"]
+    loud = (F["loudness_threshold_scale"] * threshs) ** exp * (
+        (half + half * pow_dens / threshs) ** exp - F["loudness_one"]
+    )
+    loud = torch.where(pow_dens <= threshs, torch.full_like(loud, F["loudness_below_threshold"]), loud)
     return loud * sl
 
 
-def _weighted_norm(tensor, width_bark, total_width, p):
-    return total_width * (width_bark * tensor / total_width ** (1 / p))[:, :, 1:].norm(p, dim=2)
+def disturbance(deg_loud, ref_loud):
+    """``sign(u) max(|u| - 0.25 min(L_deg, L_ref), 0)`` with ``u = L_deg - L_ref``
+    (``loss.py:234-237``)."""
+
+    deadzone = F["deadzone"] * torch.min(deg_loud, ref_loud)
+    dist = deg_loud - ref_loud
+    return dist.sign() * (dist.abs() - deadzone).clamp(min=0)
+
+
+def weighted_norm(tensor, width_bark, total_width, p):
+    """``W ||w x / W^(1/p)||_p`` over bands ``1..`` (``bark.py:176-195``)."""
+
+    scaled = width_bark * tensor / total_width ** (1 / p)
+    return total_width * scaled[:, :, F["norm_first_band"]:].norm(p, dim=2)
+
+
+def asymmetry_factor(equ_deg, equ_ref):
+    """``((equ_deg + 50) / (equ_ref + 50))^1.2``, zero below 3, at most 12
+    (``loss.py:243-246``)."""
+
+    off = F["asymm_offset"]
+    asc = ((equ_deg + off) / (equ_ref + off)) ** F["asymm_exponent"]
+    asc = torch.where(asc < F["asymm_cut"], torch.full_like(asc, F["asymm_cut_value"]), asc)
+    return asc.clamp(max=F["asymm_cap"])
+
+
+def frame_weight(taer):
+    """``h = ((taer + 1e5) / 1e7)^0.04`` (``loss.py:251-252``)."""
+
+    return ((taer + F["h_offset"]) / F["h_scale"]) ** F["h_exponent"]
 
 
 def frame_distances(ref: torch.Tensor, deg: torch.Tensor, c=None):
-    """Per frame clamped disturbances ``(symm, asymm)`` of ``reference.py:196-248``."""
+    """Per frame clamped disturbances ``(symm, asymm)`` of ``loss.py:204-253``
+    (``reference.py:196-248``)."""
 
     c = constants() if c is None else c
     th, ex, wb, tw = c["threshs"], c["exp"], c["width_bark"], c["total_width"]
 
-    silent = _total_audible(ref, th, 1e2) < 1e7
-    mask_ref = (ref > th * 100.0) * (~silent.unsqueeze(2))
-    mask_deg = (deg > th * 100.0) * (~silent.unsqueeze(2))
-    mean_ref = (ref * mask_ref).mean(dim=1)
-    mean_deg = (deg * mask_deg).mean(dim=1)
+    silent = silent_frames(ref, th)
+    ratio = band_ratio(band_means(ref, th, silent), band_means(deg, th, silent))
+    equ_ref = ratio.unsqueeze(1) * ref
 
-    ratio = ((mean_deg + 1000) / (mean_ref + 1000)).unsqueeze(1).clamp(min=0.01, max=100.0)
-    equ_ref = ratio * ref
+    taer = total_audible(equ_ref, th, F["total_threshold_factor"])
+    tad = total_audible(deg, th, F["total_threshold_factor"])
+    equ_deg = frame_ratio(taer, tad).unsqueeze(2) * deg
 
-    taer = _total_audible(equ_ref, th, 1.0)
-    fpr = (taer + 5e3) / (_total_audible(deg, th, 1.0) + 5e3)
-    fpr = torch.cat([fpr[:, :1], fpr[:, 1:] * 0.8 + fpr[:, :-1] * 0.2], dim=1)
-    fpr = fpr.clamp(min=3e-4, max=5.0)
-    equ_deg = fpr.unsqueeze(2) * deg
+    dist = disturbance(loudness(equ_deg, th, ex, SL), loudness(equ_ref, th, ex, SL))
 
-    deg_loud = _loudness(equ_deg, th, ex, SL)
-    ref_loud = _loudness(equ_ref, th, ex, SL)
+    floor, cap = F["distance_floor"], F["distance_cap"]
+    symm = weighted_norm(dist, wb, tw, F["symm_norm_p"]).clamp(min=floor)
+    asc = asymmetry_factor(equ_deg, equ_ref)
+    asymm = weighted_norm(dist * asc, wb, tw, F["asymm_norm_p"]).clamp(min=floor)
 
-    deadzone = 0.25 * torch.min(deg_loud, ref_loud)
-    dist = deg_loud - ref_loud
-    dist = dist.sign() * (dist.abs() - deadzone).clamp(min=0)
-
-    symm = _weighted_norm(dist, wb, tw, 2.0).clamp(min=1e-20)
-
-    asc = ((equ_deg + 50.0) / (equ_ref + 50.0)) ** 1.2
-    asc = torch.where(asc < 3.0, torch.zeros_like(asc), asc).clamp(max=12.0)
-    asymm = _weighted_norm(dist * asc, wb, tw, 1.0).clamp(min=1e-20)
-
-    h = ((taer + 1e5) / 1e7) ** 0.04
-    return (symm / h).clamp(max=45.0), (asymm / h).clamp(max=45.0)
+    h = frame_weight(taer)
+    return (symm / h).clamp(max=cap), (asymm / h).clamp(max=cap)
 
 
 def overlapping_sums(frames: torch.Tensor) -> torch.Tensor:
-    """6th power means over windows of 20 frames at stride 10, then the RMS."""
+    """6th power means over windows of 20 frames at stride 10, then the RMS
+    over the windows (``loss.py:255-266``)."""
 
+    power = F["psqm_power"]
     windows = frames.unfold(1, WINDOW, STRIDE)
-    psqm = (windows**6).mean(dim=2) ** (1.0 / 6)
+    psqm = (windows**power).mean(dim=2) ** (1.0 / power)
     return psqm.square().mean(dim=1).sqrt()
 
 
@@ -444,9 +603,10 @@ def chain(ref: torch.Tensor, deg: torch.Tensor, c=None):
 def epilogue(d_symm: torch.Tensor, d_asymm: torch.Tensor, factor: float):
     """MOS curve and loss (``loss.py:292-295,322``)."""
 
-    inner = 4.5 - 0.1 * d_symm - 0.0309 * d_asymm
-    mos = 0.999 + 4 / (1 + torch.exp(-1.3669 * inner + 3.8224))
-    return mos, factor * (0.1 * d_symm + 0.0309 * d_asymm)
+    ws, wa = F["pesq_symm_weight"], F["pesq_asymm_weight"]
+    inner = F["pesq_offset"] - ws * d_symm - wa * d_asymm
+    mos = F["mos_floor"] + F["mos_span"] / (1 + torch.exp(-F["mos_slope"] * inner + F["mos_shift"]))
+    return mos, factor * (ws * d_symm + wa * d_asymm)
 
 
 def pipeline(ref: torch.Tensor, deg: torch.Tensor, sample_rate: int = 16000, c=None):

@@ -297,7 +297,17 @@ def test_pipeline_workspace_queries_validate():
     # fewer than 20 frames
     assert lib.pesq_pipeline_forward_workspace(1, 4000, 0, ctypes.byref(size)) != 0
     assert b"20 frames" in lib.pesq_last_error()
-    assert lib.pesq_pipeline_forward_workspace(0, 16000, 0, ctypes.byref(size)) != 0
+    # an empty batch is valid (its calls are no-ops), a negative one is not
+    assert lib.pesq_pipeline_forward_workspace(0, 16000, 0, ctypes.byref(size)) == 0
+    assert lib.pesq_pipeline_forward_workspace(-1, 16000, 0, ctypes.byref(size)) != 0
+    assert b"negative" in lib.pesq_last_error()
+    # the empty batch returns before any pointer is read: NULLs are fine
+    assert lib.pesq_pipeline_forward(None, None, 0, 16000, None, 1.0, 2, None, None, None, None,
+                                     None, None) == 0
+    assert lib.pesq_pipeline_backward(None, None, None, None, 0, 16000, None, 1.0, 2, None, None,
+                                      None, None, None) == 0
+    assert lib.pesq_chain_forward(None, None, 0, 62, 49, ctypes.c_void_p(1), None, None, None,
+                                  None) == 0
     off, nbytes = ctypes.c_size_t(0), ctypes.c_size_t(0)
     assert lib.pesq_pipeline_region(2, 16000, 2, b"bark", ctypes.byref(off), ctypes.byref(nbytes)) == 0
     assert nbytes.value >= 4 * 62 * 49 * 4

@@ -273,14 +273,341 @@ def test_chain_gradient_finite_difference():
         assert abs(float(fd) - float(flat[idx])) <= 1e-4 * abs(float(flat[idx]))
 
 
-def test_epilogue_closed_form():
-    ds = torch.tensor([0.0, 10.0, 40.0], dtype=torch.float64)
-    da = torch.tensor([0.0, 20.0, 45.0], dtype=torch.float64)
+def test_epilogue_known_answers():
+    """The epilogue against values evaluated by hand (40-digit decimal
+    arithmetic), from the published definitions rather than the reference:
+    ITU-T P.862 (02/2001) section 10.2.2 gives the raw score
+    ``4.5 - 0.1 d_symm - 0.0309 d_asymm``, and ITU-T P.862.2 (11/2005) maps a
+    raw score ``x`` to wideband MOS-LQO ``0.999 + (4.999 - 0.999) / (1 +
+    exp(-1.3669 x + 3.8224))``.  (0, 0) is the well known top of the wideband
+    scale, 4.644."""
+
+    ds = torch.tensor([0.0, 45.0, 10.0, 2.5], dtype=torch.float64)
+    da = torch.tensor([0.0, 45.0, 20.0, 7.5], dtype=torch.float64)
     mos, loss = O.epilogue(ds, da, 0.5)
-    inner = 4.5 - 0.1 * ds - 0.0309 * da
-    torch.testing.assert_close(mos, 0.999 + 4 / (1 + torch.exp(-1.3669 * inner + 3.8224)))
-    torch.testing.assert_close(loss, 0.5 * (0.1 * ds + 0.0309 * da))
-    assert float(mos[0]) < 4.999 and float(mos[2]) > 1.0
+    want = [4.643888749336258439, 1.012035949416599897, 3.115872494896440961,
+            4.365381103103138429]
+    torch.testing.assert_close(mos, torch.tensor(want, dtype=torch.float64), rtol=1e-14, atol=0)
+    # the loss is factor times the raw score's deficit, 4.5 - x
+    torch.testing.assert_close(loss, 0.5 * torch.tensor([0.0, 5.8905, 1.618, 0.48175],
+                                                        dtype=torch.float64), rtol=1e-14, atol=0)
+
+
+# -- the formula constants against the reference's text ----------------------------------
+
+
+def test_formula_constants_match_the_reference_text():
+    """Every constant the oracle's formulas use equals the literal at the
+    reference's line (``tables.json`` holds what ``make_tables.py`` parsed
+    from the source with ``ast``); the two copies of the chain in the
+    reference (``loss.py`` and ``triton_ops/reference.py``) were checked to
+    agree when the table was written."""
+
+    parsed = TABLES["formula_constants"]
+    assert set(O.FORMULA) == set(parsed)
+    for name, value in parsed.items():
+        assert O.FORMULA[name] == value, (name, O.FORMULA[name], value,
+                                          TABLES["formula_constant_sources"][name])
+    # the chain's sl (reference.py:322) is the loudness table's Sl_16k (loudness.py:26)
+    assert O.SL == parsed["sl"] == TABLES["Sl_16k"]
+    assert (O.WINDOW, O.STRIDE) == (TABLES["psqm_window"], TABLES["psqm_stride"])
+
+
+def test_oracle_formulas_take_their_constants_from_the_table():
+    """No constant is typed inside the oracle's formula functions: every
+    numeric literal left there is structural (0, 1, 2 as indices, dims,
+    the 1 of a logistic or of ``1 / p``)."""
+
+    import ast
+    import inspect
+
+    names = ["total_audible", "silent_frames", "band_means", "band_ratio", "frame_ratio",
+             "loudness", "disturbance", "weighted_norm", "asymmetry_factor", "frame_weight",
+             "frame_distances", "overlapping_sums", "epilogue", "align_level", "edge_ramp",
+             "n_frames", "stft_bark"]
+    for name in names:
+        tree = ast.parse(inspect.getsource(getattr(O, name)))
+        body = tree.body[0].body[1:]  # past the docstring
+        for stmt in body:
+            for node in ast.walk(stmt):
+                if isinstance(node, ast.Constant) and isinstance(node.value, (int, float)):
+                    assert node.value in (0, 1, 2), (name, node.value, ast.unparse(stmt))
+
+
+# -- closed-form consequences of each chain step --------------------------------------------
+#
+# Each test below evaluates one step of the oracle's chain on inputs whose answer
+# follows from the mathematics, and also checks that a plausible misreading
+# (a constant changed in ``O.FORMULA``, a mistake planted in the oracle) fails.
+
+
+def _planted(monkeypatch, **changes):
+    for key, value in changes.items():
+        monkeypatch.setitem(O.FORMULA, key, value)
+
+
+def _loudness_laws_hold():
+    c = O.constants()
+    th, ex = c["threshs"].reshape(1, 1, -1), c["exp"].reshape(1, 1, -1)
+    ok = True
+    # zero at and below the threshold
+    zero = O.loudness(torch.cat([th, 0.5 * th, 0 * th], dim=1), th, ex, O.SL)
+    ok &= bool((zero == 0).all())
+    # far above the threshold the law tends to sl x^e
+    x = th * 1e40
+    ok &= bool(((O.loudness(x, th, ex, O.SL) / (O.SL * x**ex)) - 1).abs().max() < 1e-9)
+    # just above it, its slope: L(th (1 + 2 d)) ~ sl (2 th)^e e d
+    d = 1e-6
+    near = O.loudness(th * (1 + 2 * d), th, ex, O.SL) / (O.SL * (2 * th) ** ex * ex * d)
+    ok &= bool((near - 1).abs().max() < 1e-5)
+    return ok
+
+
+def test_loudness_laws(monkeypatch):
+    assert _loudness_laws_hold()
+    for change in ({"loudness_half": 1.0}, {"loudness_threshold_scale": 1.0},
+                   {"loudness_one": 0}):
+        with monkeypatch.context() as m:
+            _planted(m, **change)
+            assert not _loudness_laws_hold(), change
+
+
+def _disturbance_answers(l_ref):
+    l_ref = torch.tensor(l_ref, dtype=torch.float64)
+    got = [O.disturbance(k * l_ref, l_ref) for k in (2.0, 1.2, 0.5, 1.0, 0.0)]
+    want = [0.75 * l_ref, 0 * l_ref, -0.375 * l_ref, 0 * l_ref, -l_ref]
+    return all(bool(torch.allclose(g, w, rtol=1e-14, atol=0)) for g, w in zip(got, want))
+
+
+def test_disturbance_deadzone(monkeypatch):
+    """``L_deg = 2 L_ref`` leaves 0.75 L_ref, ``1.2 L_ref`` falls in the dead
+    zone, ``0.5 L_ref`` leaves -0.375 L_ref, a silent deg leaves -L_ref; the
+    rule is antisymmetric."""
+
+    l_ref = [1.0, 3.5, 1e-3]
+    assert _disturbance_answers(l_ref)
+    a = torch.tensor([0.3, 2.0, 5.0], dtype=torch.float64)
+    b = torch.tensor([1.0, 1.1, 0.2], dtype=torch.float64)
+    assert torch.equal(O.disturbance(a, b), -O.disturbance(b, a))
+    with monkeypatch.context() as m:
+        _planted(m, deadzone=0.2)
+        assert not _disturbance_answers(l_ref)
+
+
+def _psqm_answers():
+    v = 3.0
+    root = 0.6069622310029172  # 20^(-1/6)
+    ok = True
+    for frames, t, windows_in, nwin in ((50, 15, 2, 4), (50, 5, 1, 4), (50, 45, 1, 4),
+                                        (49, 45, 0, 3), (40, 20, 2, 3), (40, 9, 1, 3)):
+        x = torch.zeros(1, frames, dtype=torch.float64)
+        x[0, t] = v
+        want = v * root * math.sqrt(windows_in / nwin)
+        ok &= abs(float(O.overlapping_sums(x)) - want) <= 1e-14 * v
+    const = torch.full((1, 57), 7.25, dtype=torch.float64)
+    ok &= abs(float(O.overlapping_sums(const)) - 7.25) <= 1e-13
+    return ok
+
+
+def test_overlapping_sums_single_frame(monkeypatch):
+    """One non-zero frame v: each window holding it has the 6th power mean
+    ``v 20^(-1/6)``, the others 0, so the RMS over ``nwin`` windows is
+    ``v 20^(-1/6) sqrt(m / nwin)`` for a frame inside m windows (windows of 20
+    frames at stride 10: frame 15 is in two, frame 5 in one, frame 45 of 49
+    in none); a constant sequence gives the constant."""
+
+    assert _psqm_answers()
+    for change in ({"psqm_power": 4}, {"psqm_stride": 5}, {"psqm_window": 10}):
+        with monkeypatch.context() as m:
+            _planted(m, **change)
+            monkeypatch.setattr(O, "WINDOW", O.FORMULA["psqm_window"])
+            monkeypatch.setattr(O, "STRIDE", O.FORMULA["psqm_stride"])
+            assert not _psqm_answers(), change
+            monkeypatch.setattr(O, "WINDOW", 20)
+            monkeypatch.setattr(O, "STRIDE", 10)
+
+
+def _silence_and_means_answers():
+    c = O.constants()
+    th = c["threshs"]
+    T = 8
+    spec = torch.zeros(1, T, 49, dtype=torch.float64)
+    spec[0, :, 30] = 2e7          # frames of 2e7 above 100 th: not silent
+    spec[0, 4:, 30] = 0.5e7       # half of them at 0.5e7: silent
+    spec[0, :, 20] = 50 * th[20]  # audible, but below 100 th: never in a mean
+    spec[0, 1, 0] = 99 * th[0]    # 5e9 of energy below 100 th_0: does not count
+    silent = O.silent_frames(spec, th)
+    ok = silent.tolist() == [[False] * 4 + [True] * 4]
+    # a frame whose only energy is band 0 at 99 th_0 (about 5.1e9) is silent
+    lone = torch.zeros(1, 2, 49, dtype=torch.float64)
+    lone[0, 0, 0] = 99 * th[0]
+    lone[0, 1, 0] = 101 * th[0]
+    ok &= O.silent_frames(lone, th).tolist() == [[True, False]]
+    means = O.band_means(spec, th, silent)
+    # the mean over all 8 frames of the 4 non-silent frames' 2e7: 1e7
+    ok &= abs(float(means[0, 30]) - 1e7) <= 1e-6
+    ok &= float(means[0, 20]) == 0.0 and float(means[0, 0]) == 0.0
+    return ok
+
+
+def test_silent_frames_and_band_means(monkeypatch):
+    """A frame is silent when its reference energy in bands above 100 times
+    their threshold is below 1e7; the band means sum the non-silent frames'
+    powers above 100 th and divide by all frames."""
+
+    assert _silence_and_means_answers()
+    for change in ({"silent_energy": 1e6}, {"mean_threshold_factor": 1.0},
+                   {"silent_threshold_factor": 1.0}):
+        with monkeypatch.context() as m:
+            _planted(m, **change)
+            assert not _silence_and_means_answers(), change
+
+
+def _band_ratio_answers():
+    t = lambda v: torch.tensor([v], dtype=torch.float64)  # noqa: E731
+    got = [float(O.band_ratio(t(mr), t(md))) for mr, md in
+           ((0.0, 0.0), (1000.0, 3000.0), (1e9, 0.0), (0.0, 1e9), (9000.0, 0.0))]
+    return got == [1.0, 2.0, 0.01, 100.0, 0.1]
+
+
+def test_band_ratio_known_answers(monkeypatch):
+    assert _band_ratio_answers()
+    for change in ({"band_ratio_offset": 100}, {"band_ratio_min": 0.001},
+                   {"band_ratio_max": 1000.0}):
+        with monkeypatch.context() as m:
+            _planted(m, **change)
+            assert not _band_ratio_answers(), change
+
+
+def _frame_ratio_answers():
+    # raw ratios (taer + 5e3) / (tad + 5e3): 2, 1, 0.25, 1e-8, 1e-8, 100
+    taer = torch.tensor([[5e3, 7e3, 0.0, 0.0, 0.0, 4.95e5]], dtype=torch.float64)
+    tad = torch.tensor([[0.0, 7e3, 15e3, 5e11 - 5e3, 5e11 - 5e3, 0.0]], dtype=torch.float64)
+    # smoothed 0.8 f_t + 0.2 f_(t-1) for t > 0, clamped to [3e-4, 5]
+    want = torch.tensor([[2.0, 1.2, 0.4, 0.05 + 0.8e-8, 3e-4, 5.0]], dtype=torch.float64)
+    return bool(torch.allclose(O.frame_ratio(taer, tad), want, rtol=1e-12, atol=0))
+
+
+def test_frame_ratio_known_answers(monkeypatch):
+    assert _frame_ratio_answers()
+    for change in ({"frame_smooth_current": 0.2, "frame_smooth_previous": 0.8},
+                   {"frame_ratio_offset": 1e3}, {"frame_ratio_min": 3e-3},
+                   {"frame_ratio_max": 10.0}):
+        with monkeypatch.context() as m:
+            _planted(m, **change)
+            assert not _frame_ratio_answers(), change
+
+
+def _asymmetry_answers():
+    er = torch.zeros(5, dtype=torch.float64)
+    ed = torch.tensor([75.0, 74.0, 350.0, 0.0, 200.0], dtype=torch.float64)
+    want = torch.tensor([3.002811084953578,  # 2.5^1.2, above the cut of 3
+                         0.0,                # 2.48^1.2 = 2.974, below it
+                         12.0,               # 8^1.2 = 12.126, capped
+                         0.0,                # 1
+                         6.898648307306074], dtype=torch.float64)  # 5^1.2
+    return bool(torch.allclose(O.asymmetry_factor(ed, er), want, rtol=1e-14, atol=0))
+
+
+def test_asymmetry_factor_known_answers(monkeypatch):
+    assert _asymmetry_answers()
+    for change in ({"asymm_exponent": 1.0}, {"asymm_offset": 5.0}, {"asymm_cut": 2.9},
+                   {"asymm_cap": 20.0}):
+        with monkeypatch.context() as m:
+            _planted(m, **change)
+            assert not _asymmetry_answers(), change
+
+
+def _frame_weight_answers():
+    taer = torch.tensor([0.0, 9.9e6, 1e7 * 2**25 - 1e5], dtype=torch.float64)
+    # h(0) = 0.01^0.04: the 0.83175 of the identical-input floor at
+    # test_triton_chain.py:725-750; h(9.9e6) = 1; h(2^25 1e7 - 1e5) = 2
+    want = torch.tensor([0.8317637711026710, 1.0, 2.0], dtype=torch.float64)
+    return bool(torch.allclose(O.frame_weight(taer), want, rtol=1e-14, atol=0))
+
+
+def test_frame_weight_known_answers(monkeypatch):
+    assert _frame_weight_answers()
+    for change in ({"h_offset": 1e4}, {"h_scale": 1e6}, {"h_exponent": 0.4}):
+        with monkeypatch.context() as m:
+            _planted(m, **change)
+            assert not _frame_weight_answers(), change
+
+
+def _norm_answers():
+    c = O.constants()
+    wb, tw = c["width_bark"], float(c["total_width"])
+    ok = abs(tw - sum(TABLES["width_of_band_bark_16k"][1:])) <= 1e-12 * tw
+    d = torch.zeros(1, 1, 49, dtype=torch.float64)
+    d[0, 0, 17] = -2.5
+    # one band: sqrt(W) w_k |d| for p = 2, w_k |d| for p = 1
+    ok &= abs(float(O.weighted_norm(d, wb, tw, 2)) - math.sqrt(tw) * float(wb[17]) * 2.5) <= 1e-12
+    ok &= abs(float(O.weighted_norm(d, wb, tw, 1)) - float(wb[17]) * 2.5) <= 1e-12
+    d[0, 0, 30] = 1.5
+    two = math.sqrt(tw) * math.hypot(float(wb[17]) * 2.5, float(wb[30]) * 1.5)
+    ok &= abs(float(O.weighted_norm(d, wb, tw, 2)) - two) <= 1e-12
+    # band 0 is left out of both norms
+    z = torch.zeros(1, 1, 49, dtype=torch.float64)
+    z[0, 0, 0] = 9.0
+    ok &= float(O.weighted_norm(z, wb, tw, 2)) == 0.0 and float(O.weighted_norm(z, wb, tw, 1)) == 0.0
+    return ok
+
+
+def test_weighted_norms_absolute_scale(monkeypatch):
+    """``W ||w d / W^(1/p)||_p`` over bands 1..48: a single band k gives
+    ``sqrt(W) w_k |d|`` (p = 2) and ``w_k |d|`` (p = 1); band 0 is excluded;
+    W is the sum of the widths of bands 1..48."""
+
+    assert _norm_answers()
+    with monkeypatch.context() as m:
+        _planted(m, norm_first_band=0)
+        assert not _norm_answers()
+
+
+def _single_band_distances(k, ref_level, deg_level, frames=40):
+    ref = torch.zeros(1, frames, 49, dtype=torch.float64)
+    deg = torch.zeros(1, frames, 49, dtype=torch.float64)
+    ref[:, :, k] = ref_level
+    deg[:, :, k] = deg_level
+    return [float(v) for v in O.chain(ref, deg)]
+
+
+@pytest.mark.parametrize("k", [10, 25, 40])
+def test_chain_single_band_absolute_distances(k):
+    """Constant single-band spectra through the whole chain (every frame the
+    same, so the overlapping sums return the frame value):
+
+    * ref = A >= 1e7 in band k, deg = 0: the band ratio is
+      ``max(1000 / (A + 1000), 0.01)``, equ_ref = ratio A, the disturbance is
+      ``-L(equ_ref)``, so ``d_symm = sqrt(W) w_k L(equ_ref) / h(equ_ref)`` and
+      the asymmetry factor ``(50 / (equ_ref + 50))^1.2 < 3`` leaves
+      ``d_asymm = 1e-20 / h(equ_ref)``;
+    * ref = 0 (every frame silent, band ratio 1), deg = B in band k: the frame
+      ratio is ``5e3 / (B + 5e3)``, equ_deg = that times B, h = h(0), and
+      ``d_symm = sqrt(W) w_k L(equ_deg) / h(0)``,
+      ``d_asymm = w_k L(equ_deg) ((equ_deg + 50) / 50)^1.2 / h(0)``.
+    """
+
+    c = O.constants()
+    th, ex = c["threshs"][k], c["exp"][k]
+    wk, tw = float(c["width_bark"][k]), float(c["total_width"])
+    loud = lambda x: float(O.loudness(torch.tensor(x, dtype=torch.float64), th, ex, O.SL))  # noqa: E731
+    h = lambda taer: (taer + 1e5) / 1e7  # noqa: E731
+
+    a = 3e7
+    equ_ref = max(1000.0 / (a + 1000.0), 0.01) * a
+    ds, da = _single_band_distances(k, a, 0.0)
+    assert abs(ds - math.sqrt(tw) * wk * loud(equ_ref) / h(equ_ref) ** 0.04) <= 1e-12 * ds
+    assert abs(da - 1e-20 / h(equ_ref) ** 0.04) <= 1e-12 * da
+
+    b = 5000.0 * 200.0 / 4800.0  # equ_deg = 200: an asymmetry factor of 5^1.2
+    equ_deg = 5e3 / (b + 5e3) * b
+    ds, da = _single_band_distances(k, 0.0, b)
+    h0 = h(0.0) ** 0.04
+    assert abs(ds - math.sqrt(tw) * wk * loud(equ_deg) / h0) <= 1e-12 * ds
+    asc = ((equ_deg + 50.0) / 50.0) ** 1.2
+    assert 3.0 < asc < 12.0
+    assert abs(da - wk * loud(equ_deg) * asc / h0) <= 1e-12 * da
 
 
 def _signals(batch, n, seed):
