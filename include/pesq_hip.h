@@ -140,7 +140,8 @@ int pesq_pipeline_backward_workspace(int64_t batch, int64_t len, int grad_mask, 
  * workspace's "p" and "f" hold the pre-emphasised and band-passed signals in
  * the units of the input.  grad_mask (PESQ_GRAD_*) selects which inputs
  * the backward will need; it must match the backward call.  Requires
- * len >= 15 and at least 20 frames (1 + (len + len % 256 - 512) / 256). */
+ * len >= 15 and at least 20 frames (1 + (len + len % 256 - 512) / 256).
+ * batch == 0 is a no-op (no pointer is read), as is the backward's. */
 int pesq_pipeline_forward(const float *ref, const float *deg, int64_t batch, int64_t len,
                           const void *model_table, double factor, int grad_mask,
                           float *d_symm, float *d_asymm, float *mos, float *loss,
@@ -370,6 +371,8 @@ int pesq_chain_backward_workspace(int64_t batch, int64_t frames, int nbands, siz
 
 /* (d_symm, d_asymm)[batch] of two Bark spectrograms [batch, frames, nbands]
  * (nbands 1 .. 128, as packed in model_table); needs at least 20 frames.
+ * batch == 0 is a no-op, as in the reference (test_triton_chain.py:799-806),
+ * and so is the backward's.
  * Replaces the 7 forward kernels of _ChainFunction.forward (chain.py:768-940). */
 int pesq_chain_forward(const float *ref_bark, const float *deg_bark, int64_t batch,
                        int64_t frames, int nbands, const void *model_table, float *d_symm,

@@ -25,7 +25,7 @@ Tolerances:
 import pytest
 import torch
 
-from bench import synthetic_config
+from bench import speech_like_pair, synthetic_config
 from kernel_trace import launched_kernels, library_kernels
 from oracle import pesq_oracle as O
 from torch_pesq import PesqLossTriton, _lib
@@ -70,6 +70,7 @@ def _compare_with_oracle(ref_np, deg_np, fs, weights, outputs, g_deg, items):
         mos, loss = O.epilogue(ds, da, 0.5)
         (want_g,) = torch.autograd.grad(loss.sum() * float(weights[i]), d)
         for name, got, want in zip(worst, outputs, (ds, da, mos, loss)):
+            want = want.detach()
             err = abs(float(got[i]) - float(want)) / abs(float(want))
             worst[name] = max(worst[name], err)
         grad_num = max(grad_num, float((g_deg[i] - want_g[0]).abs().max()))
@@ -151,3 +152,36 @@ def test_config3_full_batch_forward_and_backward():
     }, resamplers
     _compare_with_oracle(ref_np, deg_np, fs, weights, outputs, g_deg, range(batch))
 
+
+
+def test_config4_length_unsaturated_items():
+    """Three 60 s items of the speech-like pair at a moderate noise level: the
+    c4 row length (prefix kernels in both scan passes, the band totals kernel)
+    and the four-frame chain variants (705 chain tiles), with both distances
+    inside their clamps, so the asymmetric path of 60 s rows (its fifth root
+    asymmetry factor, the band totals feeding it) is compared with float64."""
+
+    ref_np, deg_np = speech_like_pair(3, 960000, seed=44, noise=0.1)
+    fs = 16000
+    model = PesqLossTriton(0.5, sample_rate=fs).cuda()
+    ref = torch.from_numpy(ref_np).cuda()
+    deg = torch.from_numpy(deg_np).cuda().requires_grad_(True)
+    weights = torch.linspace(0.5, 1.5, 3, dtype=torch.float64)
+    upstream = weights.float().cuda()
+
+    def step():
+        out = model._run(ref, deg)
+        (g_deg,) = torch.autograd.grad(out[3], deg, grad_outputs=upstream)
+        return out, g_deg
+
+    step()
+    (outputs, g_deg), kernels = launched_kernels(step)
+    _assert_pipeline_variants(kernels, 3, 960000)
+    for name in ("iir_prefix_kernel<6>", "chain_fwd_kernel<4,1>", "chain_bwd_kernel<4,1>"):
+        assert name in kernels, name
+    assert any(k.startswith("band_totals_kernel<") for k in kernels)
+    outputs = [o.detach().double().cpu() for o in outputs]
+    saturated = _compare_with_oracle(ref_np, deg_np, fs, weights, outputs, g_deg.double().cpu(),
+                                     range(3))
+    assert saturated == 0, outputs[1]
+    assert all(0.0 < float(v) < 44.0 for v in outputs[1]), outputs[1]

@@ -363,3 +363,140 @@ def test_chain_exact_threshold_values(chain, deg_scale):
     _check(errs, deg_scale)
     ds, da = chain(ref.cuda(), deg.cuda())
     assert math.isfinite(float(ds.sum())) and math.isfinite(float(da.sum()))
+
+
+# -- chain: the rest of the reference's chain contract ------------------------------
+
+
+def _grad_pair(chain, ref, deg, weights, oracle=False):
+    """Gradients of ``sum(w0 d_symm + w1 d_asymm)`` w.r.t. both spectra."""
+
+    if oracle:
+        r, d = ref.double().requires_grad_(True), deg.double().requires_grad_(True)
+        ds, da = O.chain(r, d)
+        w = [x.double() for x in weights]
+    else:
+        r, d = ref.cuda().requires_grad_(True), deg.cuda().requires_grad_(True)
+        ds, da = chain(r, d)
+        w = [x.float().cuda() for x in weights]
+    total = (ds * w[0]).sum() + (da * w[1]).sum()
+    grads = torch.autograd.grad(total, [r, d])
+    return [g.detach().double().cpu() for g in grads]
+
+
+@pytest.mark.parametrize("u", [1e-2, 1e-3])
+def test_chain_near_threshold_bands(chain, u):
+    """``test_triton_chain.py:455-495``: every band a relative ``u`` above its
+    hearing threshold, where ``(0.5 + 0.5 x / th)^e - 1`` cancels to the last
+    digits unless the loudness is formed as ``expm1(e log1p(.))``.  The
+    reference's float32 chain is held to 1e-5 / 5e-5 (u = 1e-2) and
+    1.2e-4 / 6e-4 (u = 1e-3) there; the kernels here keep the chain in float64
+    and are held to the fuzz budgets of this file (1e-6 forward, 1e-5
+    gradients), which the reference's float32 spelling would fail."""
+
+    th = O.constants()["threshs"].float().reshape(1, 1, -1)
+    g = torch.Generator().manual_seed(7)
+    shape = (3, 63, 49)
+    ref = th * (1.0 + u * (0.5 + torch.rand(shape, generator=g)))
+    deg = th * (1.0 + u * (0.5 + torch.rand(shape, generator=g)))
+    # every band is audible: the loudness of every (frame, band) is formed
+    assert bool((ref.double() > th.double()).all()) and bool((deg.double() > th.double()).all())
+    errs = _chain_errors(chain, ref.contiguous(), deg.contiguous(), seed=1)
+    print(f"\nnear threshold u={u:g}: " + " ".join(f"{k}={v:.2e}" for k, v in errs.items()))
+    _check(errs, u)
+
+
+def test_chain_many_silent_frames(chain):
+    """``test_triton_chain.py:314-329``: most frames below the 1e7 total audible
+    energy of the silence test (they drop out of the band means)."""
+
+    ref, deg = _spectra(4, 71, seed=11)
+    g = torch.Generator().manual_seed(12)
+    silent = torch.rand((4, 71, 1), generator=g) < 0.8
+    ref = torch.where(silent, ref * 1e-7, ref).contiguous()
+    deg = torch.where(silent, deg * 1e-7, deg).contiguous()
+    th = O.constants()["threshs"]
+    is_silent = (ref.double() * (ref.double() > th * 1e2)).sum(dim=2) < 1e7
+    assert 0.5 < is_silent.double().mean().item() < 1.0
+    _check(_chain_errors(chain, ref, deg, seed=13), "silent")
+
+
+def test_chain_frames_outside_windows(chain):
+    """``test_triton_chain.py:774-796``: with 29 frames there is one window
+    (frames 0..19); frames 20..28 reach the distances only through the band
+    means, and their gradient is that path's, non-zero, and the oracle's."""
+
+    ref, deg = _spectra(2, 29, seed=61)
+    weights = [torch.ones(2, dtype=torch.float64)] * 2
+    got = _grad_pair(chain, ref, deg, weights)
+    want = _grad_pair(chain, ref, deg, weights, oracle=True)
+    scale = max(float(w.abs().max()) for w in want)
+    for mine, oracle in zip(got, want):
+        assert torch.isfinite(mine).all()
+        assert float((mine[:, 20:] - oracle[:, 20:]).abs().max()) <= CHAIN_GRAD * scale
+        assert float((mine - oracle).abs().max()) <= CHAIN_GRAD * scale
+        assert float(mine[:, 20:].abs().max()) > 0.0
+
+
+@pytest.mark.parametrize("which", [0, 1])
+def test_chain_single_output_gradient(chain, which):
+    """``test_triton_chain.py:405-425``: only d_symm (or only d_asymm) carries
+    an upstream gradient; the other output's backward is absent, not zero."""
+
+    ref, deg = _spectra(2, 62, seed=109)
+    up = torch.randn(2, generator=torch.Generator().manual_seed(4), dtype=torch.float64)
+    r, d = ref.cuda().requires_grad_(True), deg.cuda().requires_grad_(True)
+    out = chain(r, d)[which]
+    got = torch.autograd.grad((out * up.float().cuda()).sum(), [r, d])
+    ro, do = ref.double().requires_grad_(True), deg.double().requires_grad_(True)
+    want = torch.autograd.grad((O.chain(ro, do)[which] * up).sum(), [ro, do])
+    scale = max(float(w.abs().max()) for w in want)
+    for mine, oracle in zip(got, want):
+        mine = mine.double().cpu()
+        assert torch.isfinite(mine).all()
+        assert float((mine - oracle).abs().max()) <= CHAIN_GRAD * scale
+
+
+def test_chain_aliased_inputs(chain):
+    """``test_triton_chain.py:386-403``: one tensor passed as both spectra;
+    autograd adds the two paths' gradients."""
+
+    ref, _ = _spectra(2, 62, seed=401)
+    both = ref.cuda().requires_grad_(True)
+    ds, da = chain(both, both)
+    (got,) = torch.autograd.grad(ds.sum() + da.sum(), both)
+    both64 = ref.double().requires_grad_(True)
+    wds, wda = O.chain(both64, both64)
+    (want,) = torch.autograd.grad(wds.sum() + wda.sum(), both64)
+    got = got.double().cpu()
+    assert torch.isfinite(got).all()
+    assert float((got - want).abs().max()) <= CHAIN_GRAD * float(want.abs().max())
+    ds, wds = ds.detach().double().cpu(), wds.detach()
+    assert float((ds - wds).abs().max()) <= CHAIN_FWD * float(wds.abs().max())
+
+
+def test_chain_empty_batch(chain):
+    """``test_triton_chain.py:799-806``: a zero sized batch is a no-op that
+    returns empty distances (and an empty gradient), not a launch failure."""
+
+    empty = torch.zeros(0, 62, 49, device="cuda", requires_grad=True)
+    ds, da = chain(empty, empty)
+    assert ds.shape == (0,) and da.shape == (0,)
+    (g,) = torch.autograd.grad(ds.sum() + da.sum(), empty)
+    assert g.shape == empty.shape
+
+
+@pytest.mark.parametrize("rate,samples", [(16000, 24000), (48000, 72000)])
+def test_loss_empty_batch(model, rate, samples):
+    """The whole loss of an empty batch: empty outputs and gradients."""
+
+    m = model if rate == 16000 else PesqLossTriton(0.5, sample_rate=rate).cuda()
+    r = torch.zeros(0, samples, device="cuda")
+    d = torch.zeros(0, samples, device="cuda", requires_grad=True)
+    loss = m(r, d)
+    assert loss.shape == (0,)
+    (g,) = torch.autograd.grad(loss.sum(), d)
+    assert g.shape == d.shape
+    assert m.mos(r, d.detach()).shape == (0,)
+    ds, da = m.raw(r, d.detach())
+    assert ds.shape == (0,) and da.shape == (0,)

@@ -382,8 +382,16 @@ struct GraphedLoss : torch::CustomClassHolder {
     at::Tensor ws, scratch;         // forward workspace, backward scratch
     at::Tensor g_loss;              // upstream gradient of the loss [batch]
     at::Tensor g_ref16, g_deg16, g_ref, g_deg;
-    hipGraphExec_t fwd = nullptr, bwd = nullptr;  // forward from the static inputs, backward
-    hipStream_t fwd_stream = nullptr, bwd_stream = nullptr;  // of the last replays
+
+    // An executable graph and an event recorded after each of its launches,
+    // on the stream of that launch: the graph, and the static buffers its
+    // replays use, are released only after the event of its last launch has
+    // completed, whichever stream (of several the caller may use) ran it.
+    struct Exec {
+        hipGraphExec_t exec = nullptr;
+        hipEvent_t done = nullptr;
+    };
+    Exec fwd, bwd;  // forward from the static inputs, backward
 
     // Forward graphs that read a caller's own input buffers, by address: a
     // caller passing the same (ref, deg) buffers on two calls in a row (a
@@ -391,7 +399,7 @@ struct GraphedLoss : torch::CustomClassHolder {
     // gets one captured for them and from then on skips the two input copies.
     struct Direct {
         const void *ref, *deg;
-        hipGraphExec_t exec;
+        Exec graph;
     };
     static constexpr size_t kDirectGraphs = 4;
     std::vector<Direct> direct;  // the most recent capture last
@@ -401,12 +409,24 @@ struct GraphedLoss : torch::CustomClassHolder {
     GraphedLoss(const GraphedLoss &) = delete;
     GraphedLoss &operator=(const GraphedLoss &) = delete;
     ~GraphedLoss() override {
-        // replays still running read the graphs and the static buffers
-        if (fwd_stream) (void)hipStreamSynchronize(fwd_stream);
-        if (bwd_stream) (void)hipStreamSynchronize(bwd_stream);
-        if (fwd) (void)hipGraphExecDestroy(fwd);
-        if (bwd) (void)hipGraphExecDestroy(bwd);
-        for (const Direct &d : direct) (void)hipGraphExecDestroy(d.exec);
+        // every graph's last replay has finished before the graphs and the
+        // static buffers (freed after this body) go
+        release(fwd);
+        release(bwd);
+        for (Direct &d : direct) release(d.graph);
+    }
+
+    static void launch(const Exec &e, hipStream_t stream) {
+        check_hip(hipGraphLaunch(e.exec, stream), "hipGraphLaunch");
+        check_hip(hipEventRecord(e.done, stream), "hipEventRecord");
+    }
+
+    // waits for the graph's last replay, then destroys it
+    static void release(Exec &e) {
+        if (e.done) (void)hipEventSynchronize(e.done);
+        if (e.exec) (void)hipGraphExecDestroy(e.exec);
+        if (e.done) (void)hipEventDestroy(e.done);
+        e = Exec{};
     }
 
     void enqueue_forward(const float *ref_in, const float *deg_in, hipStream_t stream) const {
@@ -425,7 +445,7 @@ struct GraphedLoss : torch::CustomClassHolder {
 
     // the forward graph for a call's inputs (copying them into the static
     // inputs when it is the static one)
-    hipGraphExec_t forward_graph(const at::Tensor &ref, const at::Tensor &deg, hipStream_t stream) {
+    const Exec &forward_graph(const at::Tensor &ref, const at::Tensor &deg, hipStream_t stream) {
         const void *rp = ref.data_ptr(), *dp = deg.data_ptr();
         const bool plain = ref.scalar_type() == at::kFloat && deg.scalar_type() == at::kFloat &&
                            ref.is_contiguous() && deg.is_contiguous() &&
@@ -435,17 +455,16 @@ struct GraphedLoss : torch::CustomClassHolder {
         last_deg = dp;
         if (plain) {
             for (const Direct &d : direct)
-                if (d.ref == rp && d.deg == dp) return d.exec;
+                if (d.ref == rp && d.deg == dp) return d.graph;
             if (repeated) {
                 if (direct.size() == kDirectGraphs) {
-                    if (fwd_stream) check_hip(hipStreamSynchronize(fwd_stream), "hipStreamSynchronize");
-                    check_hip(hipGraphExecDestroy(direct.front().exec), "hipGraphExecDestroy");
+                    release(direct.front().graph);
                     direct.erase(direct.begin());
                 }
                 const auto *r = static_cast<const float *>(rp);
                 const auto *d = static_cast<const float *>(dp);
                 direct.push_back({rp, dp, capture([&](hipStream_t s) { enqueue_forward(r, d, s); })});
-                return direct.back().exec;
+                return direct.back().graph;
             }
         }
         stage(ref, ref_s, stream);
@@ -472,7 +491,7 @@ struct GraphedLoss : torch::CustomClassHolder {
     // the calls of enqueue(stream) as an executable graph, captured on a
     // stream of its own (capture records, it does not run anything)
     template <class F>
-    hipGraphExec_t capture(F &&enqueue) {
+    Exec capture(F &&enqueue) {
         hipStream_t stream = nullptr;
         check_hip(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
         hipGraph_t graph = nullptr;
@@ -493,7 +512,13 @@ struct GraphedLoss : torch::CustomClassHolder {
         if (graph) (void)hipGraphDestroy(graph);
         (void)hipStreamDestroy(stream);
         check_hip(status, "capturing the graphed loss");
-        return exec;
+        Exec out{exec, nullptr};
+        status = hipEventCreateWithFlags(&out.done, hipEventDisableTiming);
+        if (status != hipSuccess) {
+            (void)hipGraphExecDestroy(exec);
+            check_hip(status, "hipEventCreateWithFlags");
+        }
+        return out;
     }
 
     // copies a call's input into its static buffer
@@ -521,8 +546,7 @@ struct GraphedCall : public torch::autograd::Function<GraphedCall> {
                     "graphed loss: the inputs must be on ", g->ref_s.device());
         const c10::DeviceGuard guard(g->ref_s.device());
         const hipStream_t stream = current_stream(g->ref_s);
-        check_hip(hipGraphLaunch(g->forward_graph(ref, deg, stream), stream), "hipGraphLaunch");
-        g->fwd_stream = stream;
+        GraphedLoss::launch(g->forward_graph(ref, deg, stream), stream);
         ctx->saved_data["graphed"] = c10::IValue::make_capsule(g);
         ctx->set_materialize_grads(false);
         return g->out[3].detach();
@@ -532,15 +556,14 @@ struct GraphedCall : public torch::autograd::Function<GraphedCall> {
         const auto g =
             c10::static_intrusive_pointer_cast<GraphedLoss>(ctx->saved_data["graphed"].toCapsule());
         variable_list result(3);  // ref, deg, the graphs
-        if (!grads[0].defined() || g->bwd == nullptr) return result;
+        if (!grads[0].defined() || g->bwd.exec == nullptr) return result;
         const c10::DeviceGuard guard(g->g_loss.device());
         const hipStream_t stream = current_stream(g->g_loss);
         if (grads[0].data_ptr() != g->g_loss.data_ptr()) {
             const at::NoGradGuard no_grad;
             g->g_loss.copy_(grads[0]);
         }
-        check_hip(hipGraphLaunch(g->bwd, stream), "hipGraphLaunch");
-        g->bwd_stream = stream;
+        GraphedLoss::launch(g->bwd, stream);
         if (g->g_ref.defined()) result[0] = g->g_ref.view(g->shape).detach();
         if (g->g_deg.defined()) result[1] = g->g_deg.view(g->shape).detach();
         if (torch::autograd::GradMode::is_enabled() && grads[0].requires_grad()) {
@@ -662,9 +685,7 @@ class GraphedStep {
     void replay() const {
         GraphedLoss &s = *graphed_;
         const c10::DeviceGuard guard(s.ref_s.device());
-        const hipStream_t stream = current_stream(s.ref_s);
-        check_hip(hipGraphLaunch(s.fwd, stream), "hipGraphLaunch");
-        s.fwd_stream = stream;
+        GraphedLoss::launch(s.fwd, current_stream(s.ref_s));
     }
 
     // the static inputs (ref, deg), shaped like the examples
