@@ -316,12 +316,14 @@ def _stage_times(model, ref, deg, repeats: int = 50):
     return times
 
 
-def cpu_baseline(ref_np, deg_np, gpu_outputs, budget_s: float = 12.0):
+def cpu_baseline(ref_np, deg_np, gpu_outputs, budget_s: float = 12.0, unsaturated=None):
     """Float32 CPU restatement of the reference PesqLoss (``oracle/pesq_port.py``).
 
     Timed on this host on the full c2 batch (forward + backward w.r.t. deg),
     repeated for about ``budget_s`` seconds; also the float64 oracle as the
-    accuracy checker of the GPU outputs and of the CPU port.
+    accuracy checker of the GPU outputs and of the CPU port.  ``unsaturated``:
+    ``(ref, deg, fs, outputs)`` of a second batch whose asymmetric distances
+    stay below their 45 clamp (c2's sit at it), checked the same way.
     """
 
     import platform
@@ -359,7 +361,22 @@ def cpu_baseline(ref_np, deg_np, gpu_outputs, budget_s: float = 12.0):
         "mos": rel(gpu_outputs[2], mos),
         "cpu_port_d_symm": rel(port_ds, ds),
         "cpu_port_d_asymm": rel(port_da, da),
+        "c2_d_asymm_at_clamp": int((da >= 45.0 - 1e-9).sum()),
     }
+    if unsaturated is not None:
+        u_ref, u_deg, u_fs, u_out = unsaturated
+        with torch.no_grad():
+            u_ds, u_da = pesq_oracle.pipeline(torch.from_numpy(u_ref), torch.from_numpy(u_deg),
+                                              sample_rate=u_fs)
+        u_mos, _ = pesq_oracle.epilogue(u_ds, u_da, 1.0)
+        errors["c3"] = {
+            "batch": f"BASELINE c3, {u_ref.shape[0]} x {u_ref.shape[1]} @ {u_fs} Hz",
+            "d_symm": rel(u_out[0], u_ds),
+            "d_asymm": rel(u_out[1], u_da),
+            "mos": rel(u_out[2], u_mos),
+            "d_asymm_at_clamp": int((u_da >= 45.0 - 1e-9).sum()),
+            "d_asymm_range": [round(float(u_da.min()), 3), round(float(u_da.max()), 3)],
+        }
     # BASELINE c1: PesqLoss(0.5) forward + mos on the CPU, one 1 s item
     c1_ref, c1_deg, _ = synthetic_config(1)
     r1, d1 = torch.from_numpy(c1_ref), torch.from_numpy(c1_deg)
@@ -505,6 +522,25 @@ def diagnose(config: int, steps: int, warmup: int, copy_calibration: bool = Fals
         "device_ms_per_step": round(dev, 4),
         "signals_per_s": round(count / (wall / 1e3), 1),
     }
+    # the graph modes: PesqLossTriton.graphed() replays (forward and backward
+    # graphs, the batch's own buffers read in place) and the whole step as one
+    # graph (graphed_step, on its static inputs)
+    graph_deg = deg.detach().clone().requires_grad_(True)
+    graphed = model.graphed(ref, graph_deg)
+
+    def graph_step():
+        loss = graphed(ref, graph_deg)
+        torch.autograd.grad(loss.sum(), graph_deg)
+
+    g_wall, g_dev = timed(graph_step, steps)
+    del graphed
+    whole = model.graphed_step(ref, deg)
+    s_wall, s_dev = timed(whole.replay, steps)
+    del whole
+    out["graph_ms_per_step"] = round(g_wall, 4)
+    out["graph_device_ms_per_step"] = round(g_dev, 4)
+    out["step_graph_ms_per_step"] = round(s_wall, 4)
+    out["step_graph_device_ms_per_step"] = round(s_dev, 4)
     with torch.no_grad():
         ref16 = model.resampler(ref) if fs != 16000 else ref
         deg16 = model.resampler(deg.detach()) if fs != 16000 else deg.detach()
@@ -699,7 +735,9 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f64",
+        "dtype": "f32/f64",
+        "dtype_detail": "float32 I/O, signals, Bark spectra and FFT passes; float64 IIR state, "
+                        "band sums, perceptual chain and reductions",
         "data": "synthetic",
         "config": {
             "workload": "BASELINE c2: 8 x 8 s @16 kHz, PESQ loss forward+backward w.r.t. deg (the pipeline entry points PesqLossTriton's autograd calls, upstream gradient ones), on the resident batch",
@@ -719,7 +757,14 @@ def main(argv=None):
         "stages": stages,
     }
     if not args.no_cpu_baseline:
-        baseline, errors = cpu_baseline(ref_np, deg_np, outputs, args.cpu_seconds)
+        # an unsaturated batch for the accuracy line: c3 (d_asymm 42-43 < 45)
+        c3_ref, c3_deg, c3_fs = synthetic_config(3)
+        c3_model = PesqLossTriton(1.0, sample_rate=c3_fs).to(device)
+        with torch.no_grad():
+            c3_out = [o.double().cpu() for o in c3_model._run(torch.from_numpy(c3_ref).to(device),
+                                                             torch.from_numpy(c3_deg).to(device))]
+        baseline, errors = cpu_baseline(ref_np, deg_np, outputs, args.cpu_seconds,
+                                        (c3_ref, c3_deg, c3_fs, c3_out))
         line["cpu_baseline"] = baseline
         line["err_vs_fp64"] = errors
     else:

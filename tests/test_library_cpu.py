@@ -383,7 +383,7 @@ VARIANTS = {
          "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
          "stft_fwd_kernel<float, false, 8>", "band_totals_kernel<16, 2>",
          "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
-        ["chain_bwd_kernel<16, 1>", "band_totals_kernel<9, 1>", "stft_bwd_kernel<float, 1, 9>",
+        ["chain_bwd_kernel<16, 1>", "band_totals_kernel<8, 1>", "stft_bwd_kernel<float, 1, 9>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, true>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
     ),

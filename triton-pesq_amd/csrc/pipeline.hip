@@ -99,10 +99,10 @@ struct PipeBwdMode {
 
     const float *f, *gp;      // [nrg, len] each
     const double *rowconst;   // [rows, 4]: -, E, scale, -
-    const double *spart;      // [nrg, nhoptile]
+    const double *spart;      // [nrg, nhop]
     float *g_ref, *g_deg;
     int64_t len;
-    int batch, row0, nhoptile;
+    int batch, row0, nhop;
 
     // filter A (power^T) runs on f, filter B (pre^T) on dL/dp
     __device__ __forceinline__ const float *src(int row, int q) const {
@@ -117,10 +117,10 @@ struct PipeBwdMode {
         xa = in[0];
         xb = in[1];
     }
-    // scale and scale S / E, S = sum of the per hop tile partials of dL/dp . p
+    // scale and scale S / E, S = sum of the per hop block partials of dL/dp . p
     __device__ __forceinline__ void setup(int row, double *sh, int lane) const {
-        const int nmine = lane < nhoptile ? (nhoptile - 1 - lane) / kWave + 1 : 0;
-        double s = nmine > 0 ? strided_sum(spart + int64_t(row) * nhoptile + lane, nmine, kWave)
+        const int nmine = lane < nhop ? (nhop - 1 - lane) / kWave + 1 : 0;
+        double s = nmine > 0 ? strided_sum(spart + int64_t(row) * nhop + lane, nmine, kWave)
                              : 0.0;
         s = wave_sum(s);
         const double *rc = rowconst + int64_t(row0 + row) * 4;
@@ -340,6 +340,7 @@ constexpr int kStftWaves = 8;
 // a rolled band sum) so that more wavefronts fit per SIMD.
 template <typename real, bool kLean, int kWaves = kStftWaves>
 __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(PipeArgs a) {
+#pragma clang fp contract(off)  // the same bits in both variants (spectral.hpp)
     constexpr int kSideWaves = kWaves / 2;            // wavefronts per side
     constexpr int kPerWave = 2 * kTile / kWaves;      // frames per wavefront
     static_assert(kSideWaves * kPerWave == kTile, "a tile per side");
@@ -447,7 +448,8 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int fbin = lane + 64 * r;
-            power_buf[fbin] = fbin == 0 ? real(0) : (x[r].re * x[r].re + x[r].im * x[r].im) * scale2;
+            power_buf[fbin] =
+                fbin == 0 ? real(0) : fmadd(x[r].re, x[r].re, x[r].im * x[r].im) * scale2;
         }
         wave_lds_fence();
         const double acc = band_power(power_buf, lane, band_lo, band_hi);
@@ -1140,18 +1142,23 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
 // per CU, where 576 of 8 do not: 10.2 against 11.4 us; 448 of 10, 10.7 us);
 // large ones two frames per wavefront and eight wavefronts,
 // which halves the per workgroup table staging and band sums per frame and
-// the frames shared by two workgroups.  The sums are taken in the same order
-// for every kFPW; kW sets the split of the band gradient totals and of the
-// partials of S.
+// the frames shared by two workgroups.  Every sum is taken in an order that
+// does not depend on the variant: the band gradient totals over kGradSlices
+// slices of tiles (the first kGradSlices wavefronts take one each), and the
+// partials of S = sum dL/dp . p per hop block (one wavefront's lanes over its
+// 256 samples), so an item gets the same bits in any batch.
+constexpr int kGradSlices = kBwdWaves;
+
 template <typename real, int kFPW, int kW>
 __global__ void __launch_bounds__(kWave *kW, 5) stft_bwd_kernel(PipeArgs a) {
+#pragma clang fp contract(off)  // the same bits in both variants (spectral.hpp)
+    static_assert(kW >= kGradSlices, "a wavefront per slice of the band gradient totals");
     constexpr int kFrames = kW * kFPW;  // frames per workgroup
     constexpr int kHops = kFrames - 1;         // output hop blocks per workgroup
     __shared__ cplx<real> fftbuf[kW][kHalf];
     __shared__ float contrib[kFrames][kNfft];
-    __shared__ double gpart[kW][kBands];
+    __shared__ double gpart[kGradSlices][kBands];
     __shared__ float gband[kW][kBands];
-    __shared__ double scratch[kW];
     // the twiddle tables, window and bin-to-band map, staged once per
     // workgroup (both FFTs of every frame read them)
     using T2 = typename Vec2<real>::type;
@@ -1186,11 +1193,11 @@ __global__ void __launch_bounds__(kWave *kW, 5) stft_bwd_kernel(PipeArgs a) {
     }
 
     // adjoint of the band power ratio and its clamp, then of the mean band
-    // powers: wavefront w sums the band partials of tiles w, w + kW, ...
-    // and every wavefront adds the partial sums in wavefront order
+    // powers: wavefront w < kGradSlices sums the band partials of tiles w,
+    // w + kGradSlices, ... and every wavefront adds the slices in order
     const double *grp = region<double>(a.bw, L.grpart) + int64_t(item) * L.ntile * kBands;
-    if (lane < kBands && !L.totals) {
-        gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kW, lane, kBands);
+    if (lane < kBands && !L.totals && wave < kGradSlices) {
+        gpart[wave][lane] = tile_partial(grp, L.ntile, wave, kGradSlices, lane, kBands);
     }
     for (int k = threadIdx.x; k < kNfft; k += kWave * kW) {
         if (k < kPassTwiddles) lds_pass[k] = StagedTwiddles<real>::pass(t)[k];
@@ -1207,7 +1214,7 @@ __global__ void __launch_bounds__(kWave *kW, 5) stft_bwd_kernel(PipeArgs a) {
         if (L.totals) {
             g = region<double>(a.bw, L.gradtot)[int64_t(item) * kBands + lane];
         } else {
-            for (int w = 0; w < kW; ++w) g += gpart[w][lane];
+            for (int w = 0; w < kGradSlices; ++w) g += gpart[w][lane];
         }
         const double ratio = band_array(a, kRatio)[item * kBands + lane];
         const double mref = band_array(a, kMref)[item * kBands + lane];
@@ -1273,14 +1280,18 @@ __global__ void __launch_bounds__(kWave *kW, 5) stft_bwd_kernel(PipeArgs a) {
 
     // overlap-add: hop block j0 + q receives frames j0 + q - 1 (second half) and
     // j0 + q; four consecutive samples per thread (16-byte LDS reads, global
-    // loads and stores), element by element at the end of the row
+    // loads and stores), element by element at the end of the row.  A hop
+    // block is one wavefront's pass (wavefront q mod kW, lane l its samples
+    // 4 l .. 4 l + 3), whose lane sum is the block's partial of S.
     float *gp_out = region<float>(a.bw, L.gp) + int64_t(i) * L.len;
-    double acc = 0.0;
+    double *s_part = region<double>(a.bw, L.spart) + int64_t(i) * L.nhop;
     for (int g4 = threadIdx.x; g4 < kHops * kHop / 4; g4 += blockDim.x) {
         const int k = 4 * g4;
         const int q = k / kHop, m = k % kHop;
-        const int64_t n = (j0 + q) * kHop + m;
-        if (n >= L.len) continue;
+        const int64_t hop = j0 + q;  // the same for the whole wavefront
+        if (hop >= L.nhop) break;
+        const int64_t n = hop * kHop + m;
+        double acc = 0.0;
         float lo[4], hi[4], pv[4], out[4];
         __builtin_memcpy(hi, &contrib[q][kHop + m], sizeof(hi));
         __builtin_memcpy(lo, &contrib[q + 1][m], sizeof(lo));
@@ -1290,24 +1301,18 @@ __global__ void __launch_bounds__(kWave *kW, 5) stft_bwd_kernel(PipeArgs a) {
             for (int e = 0; e < 4; ++e) {
                 const double g = static_cast<double>(hi[e]) + static_cast<double>(lo[e]);
                 out[e] = static_cast<float>(g);
-                acc += g * static_cast<double>(pv[e]);
+                acc = fma(g, static_cast<double>(pv[e]), acc);
             }
             __builtin_memcpy(gp_out + n, out, sizeof(out));
         } else {
             for (int e = 0; e < 4 && n + e < L.len; ++e) {
                 const double g = static_cast<double>(hi[e]) + static_cast<double>(lo[e]);
                 gp_out[n + e] = static_cast<float>(g);
-                acc += g * static_cast<double>(p[n + e]);
+                acc = fma(g, static_cast<double>(p[n + e]), acc);
             }
         }
-    }
-    acc = wave_sum(acc);
-    if (lane == 0) scratch[wave] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        double sum = 0.0;
-        for (int w = 0; w < kW; ++w) sum += scratch[w];
-        region<double>(a.bw, L.spart)[int64_t(i) * L.nhoptile + ht] = sum;
+        acc = wave_sum(acc);
+        if (lane == 0) s_part[hop] = acc;
     }
 }
 
@@ -1686,7 +1691,7 @@ extern "C" int pesq_pipeline_kernels(int64_t batch, int64_t len, int grad_mask, 
     } else {
         out += "chain_bwd_kernel<" + std::to_string(P.chain_bwd_waves) + ", " +
                std::to_string(P.chain_bpl) + ">;";
-        if (L.totals) out += "band_totals_kernel<" + std::to_string(L.bwd_waves) + ", 1>;";
+        if (L.totals) out += "band_totals_kernel<" + std::to_string(kGradSlices) + ", 1>;";
         out += std::string("stft_bwd_kernel<") + bwd_real + ", " + std::to_string(L.bwd_fpw) +
                ", " + std::to_string(L.bwd_waves) + ">;";
         scan_kernel_names(P.bwd_scan, "PipeBwdMode", out);
@@ -1819,13 +1824,9 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
     }
     if (stages & 2u) {
         if (L.totals) {
-            const dim3 tgrid(static_cast<unsigned>(batch)), tblock(kWave * L.bwd_waves);
-            if (L.bwd_waves == kBwdWaves) {
-                hipLaunchKernelGGL((band_totals_kernel<kBwdWaves, 1>), tgrid, tblock, 0, stream, a);
-            } else {
-                hipLaunchKernelGGL((band_totals_kernel<kBwdWavesSmall, 1>), tgrid, tblock, 0,
-                                   stream, a);
-            }
+            hipLaunchKernelGGL((band_totals_kernel<kGradSlices, 1>),
+                               dim3(static_cast<unsigned>(batch)), dim3(kWave * kGradSlices), 0,
+                               stream, a);
             PESQ_CHECK_LAUNCH("pipeline gradient totals");
         }
         const dim3 grid(static_cast<unsigned>(L.nrg * L.nhoptile));
@@ -1849,7 +1850,7 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
     m.len = len;
     m.batch = static_cast<int>(batch);
     m.row0 = static_cast<int>(L.row0);
-    m.nhoptile = static_cast<int>(L.nhoptile);
+    m.nhop = static_cast<int>(L.nhop);
     double *aggr = region<double>(a.bw, L.aggr_b);
     if (stages & 12u) {
         return launch_scan<kPowerSections, kPreSections>(m, iir, aggr, L.nrg, len, stages & 4u,

@@ -44,7 +44,7 @@ enum LoudArray { kLoudRef, kLoudDeg, kAscRaw, kLoudArrays };
 
 struct PipeLayout {
     int64_t batch = 0, len = 0, rows = 0, frames = 0;
-    int64_t nblk = 0, ntile = 0, nhoptile = 0, nwin = 0;
+    int64_t nblk = 0, ntile = 0, nhoptile = 0, nhop = 0, nwin = 0;
     int64_t row0 = 0, nrg = 0;  // stacked rows that receive gradients
     int grad_mask = 0;
     int nb = kBands;            // Bark bands (the stand-alone chain takes 1 .. 128)
@@ -81,7 +81,8 @@ struct PipeLayout {
         bwd_fpw = b * ntile > kWideTiles ? 2 : 1;
         totals = ntile > kTotalsTiles;
         bwd_waves = bwd_fpw == 2 ? kBwdWaves : kBwdWavesSmall;
-        nhoptile = cdiv(cdiv(n, kHop), bwd_waves * bwd_fpw - 1);
+        nhop = cdiv(n, kHop);
+        nhoptile = cdiv(nhop, bwd_waves * bwd_fpw - 1);
         nwin = frames >= kWin ? (frames - kWin) / kStride + 1 : 0;
         row0 = (mask & PESQ_GRAD_REF) ? 0 : b;
         nrg = mask == (PESQ_GRAD_REF | PESQ_GRAD_DEG) ? 2 * b : (mask ? b : 0);
@@ -113,7 +114,7 @@ struct PipeLayout {
         take(gbark, size_t(rows) * frames * nb * sizeof(float));
         take(grpart, size_t(batch) * ntile * nb * sizeof(double));
         take(gp, size_t(nrg) * len * sizeof(float));
-        take(spart, size_t(nrg) * nhoptile * sizeof(double));
+        take(spart, size_t(nrg) * nhop * sizeof(double));
         take(aggr_b, size_t(scan_workspace_doubles(nrg, nblk, kPipeSections)) * sizeof(double));
         take(gradtot, totals ? size_t(batch) * nb * sizeof(double) : 0);
         bwd_bytes = off;

@@ -11,6 +11,14 @@
 // obtained from the inverse of the same fold:
 //     Z'_f = (V_f + conj V_{256-f}) + i e^{+2 pi i f / 512} (V_f - conj V_{256-f}),
 //     z = IFFT256(Z') (unnormalised),  g_u_{2n} = Re z_n,  g_u_{2n+1} = Im z_n.
+//
+// Rounding.  Floating point contraction is off in every function here and in
+// the kernels that use them: each product that meets a sum is either an
+// explicit fused multiply-add (fmadd) or rounded on its own, as written.  The
+// compiler would otherwise choose which products to fuse per instantiation,
+// and the launch variants of one transform (registers or LDS twiddles, one or
+// two frames per wavefront) would round differently; written out, every
+// variant computes the same bits for a frame.
 #pragma once
 
 #include "common.hpp"
@@ -47,14 +55,19 @@ struct cplx {
     real re, im;
 };
 
+__device__ __forceinline__ float fmadd(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+__device__ __forceinline__ double fmadd(double a, double b, double c) { return __builtin_fma(a, b, c); }
+
 template <typename real>
 __device__ __forceinline__ cplx<real> cmul(cplx<real> a, cplx<real> b) {
-    return {a.re * b.re - a.im * b.im, a.re * b.im + a.im * b.re};
+#pragma clang fp contract(off)
+    return {fmadd(a.re, b.re, -(a.im * b.im)), fmadd(a.re, b.im, a.im * b.re)};
 }
 
 // radix-4 DFT of v[0..3]; forward uses e^{-2 pi i / 4} = -i
 template <typename real, bool kInverse>
 __device__ __forceinline__ void dft4(cplx<real> (&v)[4]) {
+#pragma clang fp contract(off)
     const cplx<real> a0 = {v[0].re + v[2].re, v[0].im + v[2].im};
     const cplx<real> a1 = {v[0].re - v[2].re, v[0].im - v[2].im};
     const cplx<real> a2 = {v[1].re + v[3].re, v[1].im + v[3].im};
@@ -83,6 +96,7 @@ __device__ __forceinline__ int slot(int i) { return i ^ (((i >> 4) & 3) * 5); }
 // doubles, which the frame buffer holds for float and double bins alike).
 template <typename real>
 __device__ __forceinline__ double band_power(real *p, int lane, int lo, int hi) {
+#pragma clang fp contract(off)
     real b[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) b[j] = p[4 * lane + j];
@@ -199,6 +213,7 @@ struct LdsTwiddles {
 template <typename real, bool kInverse, bool kStoreLast = true, class TW>
 __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, const TW &tw,
                                        int lane) {
+#pragma clang fp contract(off)
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
         const int ns = 1 << (2 * pass);
@@ -232,6 +247,7 @@ __device__ __forceinline__ void fft256(cplx<real> (&v)[4], cplx<real> *buf, cons
 template <typename real, bool kDoubled = false, class Load, class TW>
 __device__ __forceinline__ void frame_spectrum(Load u, cplx<real> (&x)[4], cplx<real> *buf,
                                                const TW &tw, int lane) {
+#pragma clang fp contract(off)
     cplx<real> v[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -262,6 +278,7 @@ template <typename real, class TW>
 __device__ __forceinline__ void frame_adjoint(const cplx<real> (&vf)[4], real (&even)[4],
                                               real (&odd)[4], cplx<real> *buf, const TW &tw,
                                               int lane) {
+#pragma clang fp contract(off)
 #pragma unroll
     for (int r = 0; r < 4; ++r) buf[slot(lane + 64 * r)] = vf[r];
     wave_lds_fence();
