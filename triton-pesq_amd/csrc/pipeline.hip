@@ -162,8 +162,26 @@ __device__ __forceinline__ double *frame_array(const PipeArgs &a, int which) {
     return region<double>(a.ws, a.L.frame) + int64_t(which) * a.L.batch * a.L.frames;
 }
 
-__device__ __forceinline__ double *loud_array(const PipeArgs &a, int which) {
-    return region<double>(a.ws, a.L.loud) + int64_t(which) * a.L.batch * a.L.frames * a.L.nb;
+// What the backward needs of a (frame, band) of the forward chain, stored in
+// float32 (16 bytes instead of the three float64 values it derives them from):
+//   dist   the clamped disturbance sign(u) max(|u| - 0.25 min(L_d, L_r), 0);
+//          its sign is sign(u) wherever it is non-zero, and where it is zero
+//          the band adds nothing to either norm's gradient, so the backward
+//          takes every decision of the dead zone (sign, zone, which loudness
+//          is the smaller) from it and none from rounded loudnesses
+//   asc    the raw asymmetry factor where it lies in [3, 12] (the factor and
+//          its log-derivative both count), -12 where it is capped, 0 where
+//          it is cut: the clamp decisions are the forward's
+//   sr, sd d L_r / d equ_ref and d L_d / d equ_deg at this (frame, band)
+// Each is the float64 value rounded once, so a gradient term carries float32
+// rounding of itself, not of a difference of loudnesses.
+struct alignas(16) ChainTerms {
+    float dist, asc, sr, sd;
+};
+static_assert(sizeof(ChainTerms) == kChainTermBytes, "float4 layout");
+
+__device__ __forceinline__ ChainTerms *chain_terms(const PipeArgs &a) {
+    return region<ChainTerms>(a.ws, a.L.loud);
 }
 
 __device__ __forceinline__ double *band_array(const PipeArgs &a, int which) {
@@ -298,10 +316,14 @@ __device__ __forceinline__ double loudness(double x, double th, double inv2th, d
 }
 
 // d loudness / dx from the loudness l itself: with 1 + u = (x + th) / (2 th),
-// l = ls ((1 + u)^e - 1) gives ls e (1 + u)^(e - 1) / (2 th) = e (l + ls) / (x + th)
-__device__ __forceinline__ double loudness_slope(double x, double l, double th, double e,
-                                                 double ls) {
-    return x > th ? e * (l + ls) / (x + th) : 0.0;
+// l = ls ((1 + u)^e - 1) gives ls e (1 + u)^(e - 1) / (2 th) = e (l + ls) / (x + th);
+// to float32 accuracy (the precision it is stored in): the quotient through
+// the hardware reciprocal (1 ulp)
+__device__ __forceinline__ float loudness_slope(double x, double l, double th, double e,
+                                                double ls) {
+    return x > th ? static_cast<float>(e * (l + ls)) *
+                        __builtin_amdgcn_rcpf(static_cast<float>(x + th))
+                  : 0.0f;
 }
 
 // raw asymmetry factor ((ed + 50) / (er + 50))^1.2 = z^6 with z the fifth
@@ -748,9 +770,10 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
                 const double asc = asc_raw < 3.0 ? 0.0 : fmin(asc_raw, 12.0);
                 if (L.loud_store) {
                     const int64_t o = (int64_t(item) * L.frames + frame) * nb + lane + kWave * k;
-                    loud_array(a, kLoudRef)[o] = lr;
-                    loud_array(a, kLoudDeg)[o] = ld;
-                    loud_array(a, kAscRaw)[o] = asc_raw;
+                    const double asc_s = asc_raw < 3.0 ? 0.0 : (asc_raw <= 12.0 ? asc_raw : -12.0);
+                    chain_terms(a)[o] = {static_cast<float>(dist), static_cast<float>(asc_s),
+                                         loudness_slope(er, lr, ck.th, ck.e, ck.ls),
+                                         loudness_slope(ed, ld, ck.th, ck.e, ck.ls)};
                 }
                 if (lane + kWave * k >= 1) {
                     const double v = ck.w * dist * inv_sqrt_w;
@@ -1019,18 +1042,11 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
                 const BandConsts &ck = c[k];
                 const double Rq = R[k][q], Gq = G[k][q];
                 const double er = r[k] * Rq, ed = fpr * Gq;
-                // the forward's loudnesses and asymmetry factor of this (frame, band)
-                const int64_t o = (fo + frame) * nb + lane + kWave * k;
-                const double lr = loud_array(a, kLoudRef)[o];
-                const double ld = loud_array(a, kLoudDeg)[o];
-                const double asc_raw = loud_array(a, kAscRaw)[o];
-                const double slope_r = loudness_slope(er, lr, ck.th, ck.e, ck.ls);
-                const double slope_d = loudness_slope(ed, ld, ck.th, ck.e, ck.ls);
-                const double u = ld - lr;
-                const double z = fabs(u) - 0.25 * fmin(ld, lr);
-                const double su = sgn(u);
-                const double dst = su * fmax(z, 0.0);
-                const double asc = asc_raw < 3.0 ? 0.0 : fmin(asc_raw, 12.0);
+                // the forward's terms of this (frame, band) (ChainTerms)
+                const ChainTerms ct = chain_terms(a)[(fo + frame) * nb + lane + kWave * k];
+                const double dst = ct.dist;
+                const double asc = fabs(static_cast<double>(ct.asc));
+                const double su = sgn(dst);
 
                 double g_dist = 0.0, g_asc = 0.0;
                 if (lane + kWave * k >= 1) {
@@ -1039,17 +1055,17 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
                     g_dist += gy * asc;
                     g_asc = gy * dst;
                 }
-                const bool inzone = z >= 0.0;
-                const double g_u = inzone ? g_dist * su * su : 0.0;
-                const double g_min = inzone ? -0.25 * g_dist * su : 0.0;
-                const double wd = ld < lr ? 1.0 : (ld == lr ? 0.5 : 0.0);
-                const double wr = lr < ld ? 1.0 : (ld == lr ? 0.5 : 0.0);
-                const double g_ld = g_u + g_min * wd;
-                const double g_lr = -g_u + g_min * wr;
-                my_er = g_lr * slope_r;
-                my_ed = g_ld * slope_d;
-                if (asc_raw >= 3.0 && asc_raw <= 12.0) {
-                    const double g_log = g_asc * 1.2 * asc_raw;  // d asc / d log(ratio)
+                // outside the dead zone (dst != 0) the smaller loudness is the
+                // reference's where u > 0 and the degraded one's where u < 0;
+                // inside it g_dist is 0 and so are g_u and g_min
+                const double g_u = g_dist * su * su;
+                const double g_min = -0.25 * g_dist * su;
+                const double g_ld = g_u + (su < 0.0 ? g_min : 0.0);
+                const double g_lr = -g_u + (su > 0.0 ? g_min : 0.0);
+                my_er = g_lr * static_cast<double>(ct.sr);
+                my_ed = g_ld * static_cast<double>(ct.sd);
+                if (ct.asc > 0.0f) {
+                    const double g_log = g_asc * 1.2 * asc;  // d asc / d log(ratio)
                     my_ed += g_log / (ed + 50.0);
                     my_er -= g_log / (er + 50.0);
                 }
@@ -1150,7 +1166,7 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
 constexpr int kGradSlices = kBwdWaves;
 
 template <typename real, int kFPW, int kW>
-__global__ void __launch_bounds__(kWave *kW, 5) stft_bwd_kernel(PipeArgs a) {
+__global__ void __launch_bounds__(kWave *kW, kFPW == 2 ? 4 : 5) stft_bwd_kernel(PipeArgs a) {
 #pragma clang fp contract(off)  // the same bits in both variants (spectral.hpp)
     static_assert(kW >= kGradSlices, "a wavefront per slice of the band gradient totals");
     constexpr int kFrames = kW * kFPW;  // frames per workgroup

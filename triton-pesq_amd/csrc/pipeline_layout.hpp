@@ -38,9 +38,11 @@ constexpr int kStride = 10;        // PSQM stride (frames)
 enum FrameArray { kTaer, kTad, kFpr0, kFpr1, kH, kSymmRaw, kAsymmRaw, kSymm, kAsymm, kFrameArrays };
 // per band chain arrays, [batch, bands] each
 enum BandArray { kR, kRatio, kMref, kBandArrays };
-// per (frame, band) values of the forward chain that the backward reads,
-// [batch, frames, bands] each: the two loudnesses and the raw asymmetry factor
-enum LoudArray { kLoudRef, kLoudDeg, kAscRaw, kLoudArrays };
+// per (frame, band) terms of the forward chain that the backward reads,
+// [batch, frames, bands] of float4 (ChainTerms in pipeline.hip): the clamped
+// disturbance, the asymmetry factor with its clamp state, and the slopes of
+// both loudnesses
+constexpr size_t kChainTermBytes = 16;
 
 struct PipeLayout {
     int64_t batch = 0, len = 0, rows = 0, frames = 0;
@@ -106,7 +108,7 @@ struct PipeLayout {
         take(psqm, size_t(2) * batch * nwin * sizeof(double));
         take(dist, size_t(batch) * 2 * sizeof(double));
         loud_store = mask != 0;
-        take(loud, loud_store ? size_t(kLoudArrays) * batch * frames * nb * sizeof(double) : 0);
+        take(loud, loud_store ? kChainTermBytes * batch * frames * nb : 0);
         take(bandtot, totals ? size_t(2) * batch * nb * sizeof(double) : 0);
         fwd_bytes = off;
 
@@ -143,7 +145,7 @@ struct PipeLayout {
         take(psqm, size_t(2) * batch * nwin * sizeof(double));
         take(dist, size_t(batch) * 2 * sizeof(double));
         loud_store = 1;
-        take(loud, size_t(kLoudArrays) * batch * frames * nb * sizeof(double));
+        take(loud, kChainTermBytes * batch * frames * nb);
         fwd_bytes = off;
         off = 0;
         take(grpart, size_t(batch) * ntile * nb * sizeof(double));
