@@ -125,9 +125,9 @@ def test_config5_full_batch_forward_and_backward():
     batch = ref_np.shape[0]
     length = O.resample_length(ref_np.shape[1], fs, 16000)
     _assert_pipeline_variants(kernels, batch, length)
-    for name in ("iir_aggregate_kernel<5,1,PipeFwdMode,false>",
+    for name in ("iir_aggregate_kernel<5,1,PipeFwdMode,false,0,6>",
                  "iir_output_kernel<5,1,PipeFwdMode,false,false>",
-                 "iir_aggregate_kernel<5,1,PipeBwdMode,false>",
+                 "iir_aggregate_kernel<5,1,PipeBwdMode,false,0,6>",
                  "iir_output_kernel<5,1,PipeBwdMode,false,false>",
                  "chain_bwd_kernel<4,1>", "resample_fwd_window<3>", "resample_bwd_window<3>"):
         assert name in kernels, name

@@ -316,7 +316,10 @@ __device__ __forceinline__ void block_start_reduce(const IirTable &t, const Pair
     wave_lds_fence();
 }
 
-template <int NA, int NB>
+// The states of NA sections of filter A and NB of filter B, which are the
+// table's sections kBase .. kBase + NA - 1 and kBase + NA .. kBase + NA + NB - 1
+// (kBase 0: all sections of both filters; a pass may also run a subset).
+template <int NA, int NB, int kBase = 0>
 struct BankPair {
     Bank<NA> a;
     Bank<NB> b;
@@ -326,18 +329,18 @@ struct BankPair {
         b.zero();
     }
     __device__ __forceinline__ void scan(const IirTable &t, int level0, int lane) {
-        if constexpr (NA > 0) scan_wave<0, NA>(t, level0, a, lane);
-        if constexpr (NB > 0) scan_wave<NA, NB>(t, level0, b, lane);
+        if constexpr (NA > 0) scan_wave<kBase, NA>(t, level0, a, lane);
+        if constexpr (NB > 0) scan_wave<kBase + NA, NB>(t, level0, b, lane);
     }
     // the in-wave chunk scan (level0 = 0) with DPP moves
     template <class Powers>
     __device__ __forceinline__ void scan_chunks(const Powers &t, int lane) {
-        if constexpr (NA > 0) scan_wave_dpp<0, NA>(t, a, lane);
-        if constexpr (NB > 0) scan_wave_dpp<NA, NB>(t, b, lane);
+        if constexpr (NA > 0) scan_wave_dpp<kBase, NA>(t, a, lane);
+        if constexpr (NB > 0) scan_wave_dpp<kBase + NA, NB>(t, b, lane);
     }
     __device__ __forceinline__ void power(const IirTable &t, int level, const BankPair &add) {
-        if constexpr (NA > 0) apply_power<0, NA>(t, level, a, add.a);
-        if constexpr (NB > 0) apply_power<NA, NB>(t, level, b, add.b);
+        if constexpr (NA > 0) apply_power<kBase, NA>(t, level, a, add.a);
+        if constexpr (NB > 0) apply_power<kBase + NA, NB>(t, level, b, add.b);
     }
     // section k (0 .. NA + NB - 1) as (u, v) references
     __device__ __forceinline__ double &u(int k) { return k < NA ? a.u[k] : b.u[k - NA]; }
@@ -500,13 +503,13 @@ __device__ __forceinline__ void chunk_end_state(const IirTable &t, const double 
 // 1 us to the weights' scalar loads and keep the recursion.  Chunks at a row
 // end always run the recursion, with the ramp weights and bounds of
 // element_inputs.
-template <bool kGeneral, bool kWeighted, int NA, int NB, class Mode>
+template <bool kGeneral, bool kWeighted, int NA, int NB, class Mode, int kBase = 0>
 __device__ __forceinline__ void zero_run(const Mode &m, const IirTable &t,
-                                         const Coeffs<0, NA, Mode::kB2> &ca,
-                                         const Coeffs<NA, NB, Mode::kB2> &cb,
+                                         const Coeffs<kBase, NA, Mode::kB2> &ca,
+                                         const Coeffs<kBase + NA, NB, Mode::kB2> &cb,
                                          const typename Mode::In (&in)[kChunk][Mode::kInputs],
                                          int64_t j0,
-                                         int64_t len, BankPair<NA, NB> &s) {
+                                         int64_t len, BankPair<NA, NB, kBase> &s) {
     if constexpr (kGeneral || !kWeighted) {
 #pragma unroll
         for (int i = 0; i < kChunk; ++i) {
@@ -522,8 +525,8 @@ __device__ __forceinline__ void zero_run(const Mode &m, const IirTable &t,
             double w;
             element_inputs<false>(m, in[i], j0 + i, len, w, xa[i], xb[i]);
         }
-        if constexpr (NA > 0) chunk_end_state<0, NA>(t, xa, s.a);
-        if constexpr (NB > 0) chunk_end_state<NA, NB>(t, xb, s.b);
+        if constexpr (NA > 0) chunk_end_state<kBase, NA>(t, xa, s.a);
+        if constexpr (NB > 0) chunk_end_state<kBase + NA, NB>(t, xb, s.b);
     }
 }
 
@@ -581,51 +584,84 @@ __device__ __forceinline__ void block_end_state(const IirTable &t, BP &s, double
     if (lane % 4 == 0 && comp < kComps) dst[int64_t(comp / 2) * nblk * 2 + comp % 2] = sum;
 }
 
-template <int NA, int NB, class Mode, bool kLaneStates>
-__global__ void __launch_bounds__(kWave)
-    iir_aggregate_kernel(Mode m, const IirTable *__restrict__ table, double *__restrict__ aggr,
-                         double *__restrict__ lanes, int64_t len, int nblk) {
+// The aggregate pass of one block (row, blk) by one wavefront, lane states
+// stored: sections kBase .. kBase + NA + NB - 1 of a workspace laid out for
+// kLayout sections (the aggregates [row][section][block][2], the lane states
+// [row][block][section][lane][2]).  Every section is an independent
+// recursion, so a pass over a subset of the sections writes the same bits for
+// them as a pass over all (the pipeline runs the backward's level alignment
+// filter on its own, inside an earlier kernel, and the pre-emphasis filter in
+// the aggregate launch).
+template <int NA, int NB, int kBase, int kLayout, class Mode>
+__device__ __forceinline__ void aggregate_block(const Mode &m, const IirTable &t, double *aggr,
+                                                double *lanes, int64_t len, int nblk, int row,
+                                                int blk, int lane) {
     constexpr int NS = NA + NB;
-    const IirTable &t = *table;
-    const int row = blockIdx.x / nblk;
-    const int blk = blockIdx.x - row * nblk;
-    const int lane = threadIdx.x;
+    static_assert(kBase + NS <= kLayout, "sections inside the layout");
     const int64_t j0 = int64_t(blk) * kSpan + int64_t(lane) * kChunk;
-    Coeffs<0, NA, Mode::kB2> ca;
-    Coeffs<NA, NB, Mode::kB2> cb;
+    Coeffs<kBase, NA, Mode::kB2> ca;
+    Coeffs<kBase + NA, NB, Mode::kB2> cb;
     ca.load(t, t.c0a);
     cb.load(t, t.c0b);
 
     typename Mode::In in[kChunk][Mode::kInputs];
     load_chunk(m, row, j0, len, in);
 
-    BankPair<NA, NB> s;
+    BankPair<NA, NB, kBase> s;
     s.zero();
     if (general_chunk(j0, len)) {
-        zero_run<true, !kLaneStates>(m, t, ca, cb, in, j0, len, s);
+        zero_run<true, false>(m, t, ca, cb, in, j0, len, s);
     } else {
-        zero_run<false, !kLaneStates>(m, t, ca, cb, in, j0, len, s);
-    }
-    if constexpr (!kLaneStates) {
-        block_end_state<NS>(t, s, aggr + (int64_t(row) * NS * nblk + blk) * 2, nblk, lane);
-        return;
+        zero_run<false, false>(m, t, ca, cb, in, j0, len, s);
     }
     s.scan_chunks(t, lane);
     if (lane == kWave - 1) {
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
-            double *dst = aggr + ((int64_t(row) * NS + k) * nblk + blk) * 2;
+            double *dst = aggr + ((int64_t(row) * kLayout + kBase + k) * nblk + blk) * 2;
             dst[0] = s.u(k);
             dst[1] = s.v(k);
         }
     }
     // start state of every lane's chunk (the end state of the chunk before it)
-    double2 *dst = reinterpret_cast<double2 *>(lanes) + (int64_t(row) * nblk + blk) * NS * kWave;
+    double2 *dst = reinterpret_cast<double2 *>(lanes) +
+                   ((int64_t(row) * nblk + blk) * kLayout + kBase) * kWave;
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
         // wave_shr:1 (lane 0 reads 0)
         const double u = dpp_move<0x138, 0xF>(s.u(k)), v = dpp_move<0x138, 0xF>(s.v(k));
         dst[k * kWave + lane] = make_double2(u, v);
+    }
+}
+
+template <int NA, int NB, class Mode, bool kLaneStates, int kBase = 0, int kLayout = NA + NB>
+__global__ void __launch_bounds__(kWave)
+    iir_aggregate_kernel(Mode m, const IirTable *__restrict__ table, double *__restrict__ aggr,
+                         double *__restrict__ lanes, int64_t len, int nblk) {
+    const IirTable &t = *table;
+    const int row = blockIdx.x / nblk;
+    const int blk = blockIdx.x - row * nblk;
+    const int lane = threadIdx.x;
+    if constexpr (kLaneStates) {
+        aggregate_block<NA, NB, kBase, kLayout>(m, t, aggr, lanes, len, nblk, row, blk, lane);
+    } else {
+        static_assert(kBase == 0 && kLayout == NA + NB, "all sections without lane states");
+        constexpr int NS = NA + NB;
+        const int64_t j0 = int64_t(blk) * kSpan + int64_t(lane) * kChunk;
+        Coeffs<0, NA, Mode::kB2> ca;
+        Coeffs<NA, NB, Mode::kB2> cb;
+        ca.load(t, t.c0a);
+        cb.load(t, t.c0b);
+        typename Mode::In in[kChunk][Mode::kInputs];
+        load_chunk(m, row, j0, len, in);
+        BankPair<NA, NB> s;
+        s.zero();
+        if (general_chunk(j0, len)) {
+            zero_run<true, true>(m, t, ca, cb, in, j0, len, s);
+        } else {
+            zero_run<false, true>(m, t, ca, cb, in, j0, len, s);
+        }
+        block_end_state<NS>(t, s, aggr + (int64_t(row) * NS * nblk + blk) * 2, nblk, lane);
     }
 }
 

@@ -134,6 +134,51 @@ struct PipeBwdMode {
     __device__ __forceinline__ void finish(int, int, double) const {}
 };
 
+// The two filters of the backward scan one at a time, for aggregate passes
+// over a subset of its sections (iir.hpp aggregate_block): the level
+// alignment filter (power^T) on f, run inside the forward's chain kernel, and
+// the pre-emphasis filter (pre^T) on dL/dp.  Same inputs and time order as
+// PipeBwdMode; they produce no outputs.
+struct PipeBwdPowerMode {
+    static constexpr int kInputs = 1;
+    static constexpr int kOutputs = 1;
+    static constexpr bool kRamp = false;
+    static constexpr bool kReverse = true;
+    static constexpr bool kAccumulates = false;
+    static constexpr bool kB2 = false;
+    using In = float;
+    using Out = float;
+
+    const float *f;  // [nrg, len]
+    int64_t len;
+
+    __device__ __forceinline__ const float *src(int row, int) const { return f + int64_t(row) * len; }
+    __device__ __forceinline__ void inputs(double, const float *in, double &xa, double &xb) const {
+        xa = in[0];
+        xb = 0.0;
+    }
+};
+
+struct PipeBwdPreMode {
+    static constexpr int kInputs = 1;
+    static constexpr int kOutputs = 1;
+    static constexpr bool kRamp = false;
+    static constexpr bool kReverse = true;
+    static constexpr bool kAccumulates = false;
+    static constexpr bool kB2 = false;
+    using In = float;
+    using Out = float;
+
+    const float *gp;  // [nrg, len]
+    int64_t len;
+
+    __device__ __forceinline__ const float *src(int row, int) const { return gp + int64_t(row) * len; }
+    __device__ __forceinline__ void inputs(double, const float *in, double &xa, double &xb) const {
+        xa = 0.0;
+        xb = in[0];
+    }
+};
+
 // ---------------------------------------------------------------------------
 // shared chain helpers
 // ---------------------------------------------------------------------------
@@ -602,12 +647,27 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
 
     const ModelTable &t = *a.tab;
     const PipeLayout &L = a.L;
+    const int wave = wave_index();
+    const int lane = threadIdx.x % kWave;
+    if (L.host_power && blockIdx.x >= L.batch * L.ntile) {
+        // workgroups past the chain's: the aggregate pass of the backward's
+        // level alignment filter on f, a block of a gradient row per wavefront
+        const int64_t g = int64_t(blockIdx.x - L.batch * L.ntile) * kWaves + wave;
+        if (g < L.nrg * L.nblk) {
+            const int row = static_cast<int>(g / L.nblk);
+            const int blk = static_cast<int>(g - int64_t(row) * L.nblk);
+            double *aggr = region<double>(a.ws, L.aggr_b);
+            double *lanes = aggr + scan_aggr_doubles(L.nrg, L.nblk, kPipeSections);
+            const PipeBwdPowerMode m{region<float>(a.ws, L.f), L.len};
+            aggregate_block<kPowerSections, 0, 0, kPipeSections>(
+                m, t.iir, aggr, lanes, L.len, static_cast<int>(L.nblk), row, blk, lane);
+        }
+        return;
+    }
     const int nb = L.nb;  // bands: band lane + kWave k is slot k of a lane
     const int item = blockIdx.x / L.ntile;
     const int tile = blockIdx.x - item * L.ntile;
     const int t0 = tile * kTile;
-    const int wave = wave_index();
-    const int lane = threadIdx.x % kWave;
     const double frames_f = static_cast<double>(L.frames);
     const int64_t f0 = t0 + wave * kPer;  // first frame of this wavefront
 
@@ -1612,6 +1672,10 @@ static PipePlan pipe_plan(const PipeLayout &L) {
 
 static void launch_chain_fwd(const PipeArgs &a, unsigned grid, hipStream_t stream) {
     const PipePlan P = pipe_plan(a.L);
+    if (a.L.host_power) {
+        // and the backward's level alignment aggregate blocks, a wavefront each
+        grid += static_cast<unsigned>(cdiv(a.L.nrg * a.L.nblk, P.chain_fwd_waves));
+    }
     if (P.chain_bpl == 2) {
         hipLaunchKernelGGL((chain_fwd_kernel<4, 2>), dim3(grid), dim3(kWave * 4), 0, stream, a);
     } else if (P.chain_fwd_waves == 8) {
@@ -1632,10 +1696,16 @@ static void launch_chain_bwd(const PipeArgs &a, unsigned grid, hipStream_t strea
     }
 }
 
-// Names of the kernels of one scan pass, in launch order.
-static void scan_kernel_names(const ScanPlan &S, const char *mode, std::string &out) {
+// Names of the kernels of one scan pass, in launch order (host_power: the
+// backward's aggregate launch runs the pre-emphasis filter alone).
+static void scan_kernel_names(const ScanPlan &S, const char *mode, std::string &out,
+                              bool host_power = false) {
     const char *lanes = S.lane_states ? "true" : "false";
-    out += std::string("iir_aggregate_kernel<5, 1, ") + mode + ", " + lanes + ">;";
+    if (host_power) {
+        out += "iir_aggregate_kernel<0, 1, PipeBwdPreMode, true, 5, 6>;";
+    } else {
+        out += std::string("iir_aggregate_kernel<5, 1, ") + mode + ", " + lanes + ", 0, 6>;";
+    }
     if (!S.fused_prefix) out += "iir_prefix_kernel<6>;";
     out += std::string("iir_output_kernel<5, 1, ") + mode + ", " + lanes + ", " +
            (S.fused_prefix ? "true" : "false") + ">;";
@@ -1710,7 +1780,7 @@ extern "C" int pesq_pipeline_kernels(int64_t batch, int64_t len, int grad_mask, 
         if (L.totals) out += "band_totals_kernel<" + std::to_string(kGradSlices) + ", 1>;";
         out += std::string("stft_bwd_kernel<") + bwd_real + ", " + std::to_string(L.bwd_fpw) +
                ", " + std::to_string(L.bwd_waves) + ">;";
-        scan_kernel_names(P.bwd_scan, "PipeBwdMode", out);
+        scan_kernel_names(P.bwd_scan, "PipeBwdMode", out, L.host_power);
     }
     out.pop_back();  // the last ';'
     if (needed != nullptr) *needed = out.size() + 1;
@@ -1867,6 +1937,27 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
     m.batch = static_cast<int>(batch);
     m.row0 = static_cast<int>(L.row0);
     m.nhop = static_cast<int>(L.nhop);
+    if (L.host_power) {
+        // the level alignment filter's aggregates came from the forward's
+        // chain kernel (sections 0..4); the pre-emphasis filter's (section 5)
+        // complete them, then the output pass runs both filters
+        double *aggr = region<double>(a.ws, L.aggr_b);
+        const int nblk = static_cast<int>(L.nblk);
+        if (stages & 4u) {
+            const PipeBwdPreMode pm{m.gp, len};
+            hipLaunchKernelGGL((iir_aggregate_kernel<0, kPreSections, PipeBwdPreMode, true,
+                                                     kPowerSections, kPipeSections>),
+                               dim3(static_cast<unsigned>(L.nrg * L.nblk)), dim3(kWave), 0, stream,
+                               pm, iir, aggr, aggr + scan_aggr_doubles(L.nrg, nblk, kPipeSections),
+                               len, nblk);
+            PESQ_CHECK_LAUNCH("iir aggregate");
+        }
+        if (stages & 8u) {
+            return launch_scan<kPowerSections, kPreSections>(m, iir, aggr, L.nrg, len, false,
+                                                             true, stream);
+        }
+        return PESQ_OK;
+    }
     double *aggr = region<double>(a.bw, L.aggr_b);
     if (stages & 12u) {
         return launch_scan<kPowerSections, kPreSections>(m, iir, aggr, L.nrg, len, stages & 4u,

@@ -54,6 +54,12 @@ struct PipeLayout {
     int bwd_fpw = 1;            // frames per wavefront of the fused STFT backward (1 or 2)
     int bwd_waves = kBwdWaves;  // wavefronts per workgroup of the fused STFT backward
     int totals = 0;             // per item band totals (items of more than kTotalsTiles tiles)
+    // The forward's chain kernel also runs the aggregate pass of the backward's
+    // level alignment filter (power^T on f, which only needs forward data), on
+    // grids whose backward scan stores lane states and fuses its block prefix;
+    // the backward's aggregate launch then runs the pre-emphasis filter alone.
+    // The backward scan's workspace (aggr_b) then lies in the forward workspace.
+    int host_power = 0;
 
     // forward workspace
     size_t aggr = 0, energy = 0, p = 0, f = 0, rowconst = 0, bark = 0, keep = 0;
@@ -110,6 +116,12 @@ struct PipeLayout {
         loud_store = mask != 0;
         take(loud, loud_store ? kChainTermBytes * batch * frames * nb : 0);
         take(bandtot, totals ? size_t(2) * batch * nb * sizeof(double) : 0);
+        const ScanPlan bwd_scan = scan_plan(nrg, nblk);
+        host_power = nrg > 0 && bwd_scan.lane_states && bwd_scan.fused_prefix;
+        const size_t bwd_scan_bytes =
+            size_t(scan_workspace_doubles(nrg, nblk, kPipeSections)) * sizeof(double);
+        size_t aggr_f = 0;
+        take(aggr_f, host_power ? bwd_scan_bytes : 0);
         fwd_bytes = off;
 
         off = 0;
@@ -117,9 +129,10 @@ struct PipeLayout {
         take(grpart, size_t(batch) * ntile * nb * sizeof(double));
         take(gp, size_t(nrg) * len * sizeof(float));
         take(spart, size_t(nrg) * nhop * sizeof(double));
-        take(aggr_b, size_t(scan_workspace_doubles(nrg, nblk, kPipeSections)) * sizeof(double));
+        take(aggr_b, host_power ? 0 : bwd_scan_bytes);
         take(gradtot, totals ? size_t(batch) * nb * sizeof(double) : 0);
         bwd_bytes = off;
+        if (host_power) aggr_b = aggr_f;  // an offset into the forward workspace
     }
 
     // Regions of the stand-alone perceptual chain over given Bark spectra:
