@@ -665,6 +665,29 @@ __global__ void __launch_bounds__(kWave)
     }
 }
 
+// The aggregate pass with lane states by two wavefronts per block, each on
+// its own sections: the first runs filter A's sections 0 .. kSplit - 1, the
+// second A's others and filter B's.  The sections are independent recursions,
+// so this writes the same bits as iir_aggregate_kernel, with about half the
+// serial work per wavefront (both read the block's inputs).
+template <int NA, int NB, int kSplit, class Mode>
+__global__ void __launch_bounds__(2 * kWave)
+    iir_aggregate_split_kernel(Mode m, const IirTable *__restrict__ table,
+                               double *__restrict__ aggr, double *__restrict__ lanes, int64_t len,
+                               int nblk) {
+    static_assert(kSplit > 0 && kSplit < NA, "both wavefronts take sections of filter A");
+    const IirTable &t = *table;
+    const int row = blockIdx.x / nblk;
+    const int blk = blockIdx.x - row * nblk;
+    const int lane = threadIdx.x % kWave;
+    if (wave_index() == 0) {
+        aggregate_block<kSplit, 0, 0, NA + NB>(m, t, aggr, lanes, len, nblk, row, blk, lane);
+    } else {
+        aggregate_block<NA - kSplit, NB, kSplit, NA + NB>(m, t, aggr, lanes, len, nblk, row, blk,
+                                                          lane);
+    }
+}
+
 // Exclusive scan of the block aggregates, one (row, section) sequence per
 // wavefront; aggr[b] is replaced by the state at the start of block b
 // (s_{b+1} = M s_b + e_b, M = A^1024 the block transfer, e_b the aggregate).
@@ -880,9 +903,11 @@ __global__ void __launch_bounds__(kWave)
 
 // Host side: aggregate, prefix and output launches of one scan pass over
 // `rows` rows; `ws` holds scan_workspace_doubles(rows, nblk, NA + NB).
+// split: the aggregate pass of lane-state grids by two wavefronts per block
+// (iir_aggregate_split_kernel, A's first NA / 2 sections in one of them).
 template <int NA, int NB, class Mode>
 int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, int64_t len,
-                bool aggregate, bool output, hipStream_t stream) {
+                bool aggregate, bool output, hipStream_t stream, bool split = false) {
     constexpr int NS = NA + NB;
     static_assert(NS <= kMaxSections, "too many sections");
     const int64_t nblk = cdiv(len, kBlockSpan);
@@ -894,7 +919,17 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
     const bool lane_states = plan.lane_states;
     const bool fused = plan.fused_prefix;
     if (aggregate) {
-        if (lane_states) {
+        bool launched = false;
+        if constexpr (NA >= 2) {
+            if (lane_states && split) {
+                hipLaunchKernelGGL((iir_aggregate_split_kernel<NA, NB, NA / 2, Mode>), dim3(grid),
+                                   dim3(2 * kWave), 0, stream, m, table, aggr, lanes, len,
+                                   static_cast<int>(nblk));
+                launched = true;
+            }
+        }
+        if (launched) {
+        } else if (lane_states) {
             hipLaunchKernelGGL((iir_aggregate_kernel<NA, NB, Mode, true>), dim3(grid), dim3(kWave),
                                0, stream, m, table, aggr, lanes, len, static_cast<int>(nblk));
         } else {

@@ -1696,6 +1696,12 @@ static void launch_chain_bwd(const PipeArgs &a, unsigned grid, hipStream_t strea
     }
 }
 
+#ifndef PESQ_SPLIT_AGGREGATE
+#define PESQ_SPLIT_AGGREGATE 1
+#endif
+// the scans' aggregate pass of lane-state grids by two wavefronts per block
+constexpr bool kSplitAggregate = PESQ_SPLIT_AGGREGATE != 0;
+
 // Names of the kernels of one scan pass, in launch order (host_power: the
 // backward's aggregate launch runs the pre-emphasis filter alone).
 static void scan_kernel_names(const ScanPlan &S, const char *mode, std::string &out,
@@ -1703,6 +1709,8 @@ static void scan_kernel_names(const ScanPlan &S, const char *mode, std::string &
     const char *lanes = S.lane_states ? "true" : "false";
     if (host_power) {
         out += "iir_aggregate_kernel<0, 1, PipeBwdPreMode, true, 5, 6>;";
+    } else if (kSplitAggregate && S.lane_states) {
+        out += std::string("iir_aggregate_split_kernel<5, 1, 2, ") + mode + ">;";
     } else {
         out += std::string("iir_aggregate_kernel<5, 1, ") + mode + ", " + lanes + ", 0, 6>;";
     }
@@ -1833,7 +1841,8 @@ extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, 
 
     if (stages & 3u) {
         if (int st = launch_scan<kPowerSections, kPreSections>(m, iir, aggr, L.rows, len,
-                                                               stages & 1u, stages & 2u, stream)) {
+                                                               stages & 1u, stages & 2u, stream,
+                                                               kSplitAggregate)) {
             return st;
         }
     }
@@ -1961,7 +1970,7 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
     double *aggr = region<double>(a.bw, L.aggr_b);
     if (stages & 12u) {
         return launch_scan<kPowerSections, kPreSections>(m, iir, aggr, L.nrg, len, stages & 4u,
-                                                         stages & 8u, stream);
+                                                         stages & 8u, stream, kSplitAggregate);
     }
     return PESQ_OK;
 }
