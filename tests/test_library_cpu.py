@@ -363,7 +363,7 @@ def test_graft_entry_exposes_build_and_smoke():
 VARIANTS = {
     # BASELINE c2: 16 rows x 125 blocks, 8 x 32 tiles
     (8, 128000, 2): (
-        ["iir_aggregate_split_kernel<5, 1, 2, PipeFwdMode>",
+        ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, true>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
@@ -373,32 +373,32 @@ VARIANTS = {
     # BASELINE c4: 938 blocks per row (prefix kernel), 4 x 235 = 940 tiles, items
     # of 235 tiles (per item band totals)
     (4, 960000, 2): (
-        ["iir_aggregate_split_kernel<5, 1, 2, PipeFwdMode>", "iir_prefix_kernel<6>",
+        ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
          "stft_fwd_kernel<float, true, 8>", "band_totals_kernel<16, 2>",
          "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<4, 1>", "band_totals_kernel<8, 1>", "stft_bwd_kernel<float, 2, 8>",
-         "iir_aggregate_split_kernel<5, 1, 2, PipeBwdMode>", "iir_prefix_kernel<6>",
+         "iir_aggregate_split_kernel<5, 1, 3, PipeBwdMode>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
     ),
     # one item of 65 tiles (1033 frames): just past the band totals threshold
     # (259 blocks per row: the prefix kernel)
     (1, 264704, 1): (
-        ["iir_aggregate_split_kernel<5, 1, 2, PipeFwdMode>", "iir_prefix_kernel<6>",
+        ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
          "stft_fwd_kernel<float, false, 8>", "band_totals_kernel<16, 2>",
          "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "band_totals_kernel<8, 1>", "stft_bwd_kernel<float, 1, 9>",
-         "iir_aggregate_split_kernel<5, 1, 2, PipeBwdMode>", "iir_prefix_kernel<6>",
+         "iir_aggregate_split_kernel<5, 1, 3, PipeBwdMode>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
     ),
     # one item of 64 tiles (1023 frames): the largest without band totals
     (1, 262144, 1): (
-        ["iir_aggregate_split_kernel<5, 1, 2, PipeFwdMode>", "iir_prefix_kernel<6>",
+        ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
-         "iir_aggregate_split_kernel<5, 1, 2, PipeBwdMode>", "iir_prefix_kernel<6>",
+         "iir_aggregate_split_kernel<5, 1, 3, PipeBwdMode>", "iir_prefix_kernel<6>",
          "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
     ),
     # BASELINE c5 after the 3:1 resampler: 512 x 63 = 32256 forward scan
@@ -413,7 +413,7 @@ VARIANTS = {
     ),
     # BASELINE c3 after the 441:160 resampler: a small grid like c2
     (16, 64000, 2): (
-        ["iir_aggregate_split_kernel<5, 1, 2, PipeFwdMode>",
+        ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>",
          "iir_output_kernel<5, 1, PipeFwdMode, true, true>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
@@ -514,7 +514,7 @@ def test_kernel_trace_normalises_library_names():
         == "iir_prefix_kernel<6>"
     mangled = "_ZN4pesq20iir_aggregate_kernelILi5ELi1ENS_11PipeFwdModeELb1ELi0ELi6EEEvT1_PKNS_8IirTableEPdS6_li"
     assert normalise(mangled) == "iir_aggregate_kernel<5,1,PipeFwdMode,true,0,6>"
-    assert library_kernels(8, 128000, 2, False)[0] == "iir_aggregate_split_kernel<5,1,2,PipeFwdMode>"
+    assert library_kernels(8, 128000, 2, False)[0] == "iir_aggregate_split_kernel<5,1,3,PipeFwdMode>"
     assert all(" " not in k for k in library_kernels(4, 960000, 2, True))
 
 

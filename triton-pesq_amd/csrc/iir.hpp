@@ -904,7 +904,7 @@ __global__ void __launch_bounds__(kWave)
 // Host side: aggregate, prefix and output launches of one scan pass over
 // `rows` rows; `ws` holds scan_workspace_doubles(rows, nblk, NA + NB).
 // split: the aggregate pass of lane-state grids by two wavefronts per block
-// (iir_aggregate_split_kernel, A's first NA / 2 sections in one of them).
+// (iir_aggregate_split_kernel, A's first (NA + NB) / 2 sections in one of them).
 template <int NA, int NB, class Mode>
 int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, int64_t len,
                 bool aggregate, bool output, hipStream_t stream, bool split = false) {
@@ -922,7 +922,9 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
         bool launched = false;
         if constexpr (NA >= 2) {
             if (lane_states && split) {
-                hipLaunchKernelGGL((iir_aggregate_split_kernel<NA, NB, NA / 2, Mode>), dim3(grid),
+                // as many sections in each wavefront as the filters allow
+                constexpr int kSplit = (NA + NB) / 2 < NA ? (NA + NB) / 2 : NA - 1;
+                hipLaunchKernelGGL((iir_aggregate_split_kernel<NA, NB, kSplit, Mode>), dim3(grid),
                                    dim3(2 * kWave), 0, stream, m, table, aggr, lanes, len,
                                    static_cast<int>(nblk));
                 launched = true;
