@@ -269,6 +269,35 @@ def test_chain_batch_independence_and_errors(chain):
         chain(ref, deg)
 
 
+@pytest.mark.parametrize("batch,frames", [(8, 63), (8, 1100)])
+def test_chain_batch_independence_with_gradients(chain, batch, frames):
+    """Every row of a batched call, outputs and both input gradients under
+    per-row upstream gradients, equals the same row computed on its own, bit
+    for bit (``test_triton_chain.py:568-598``, whose shape is the first case).
+    In the second the batch (552 chain tiles) runs the wide kernel variants
+    (four frames per wavefront) and each row alone (69 tiles) the narrow
+    ones."""
+
+    ref, deg = _spectra(batch, frames, 999)
+    g = torch.Generator().manual_seed(5)
+    up_s = torch.randn(batch, generator=g).cuda()
+    up_a = torch.randn(batch, generator=g).cuda()
+    r, d = ref.cuda().requires_grad_(True), deg.cuda().requires_grad_(True)
+    symm, asymm = chain(r, d)
+    grads = torch.autograd.grad((symm * up_s).sum() + (asymm * up_a).sum(), (r, d))
+    for b in range(batch):
+        rb = ref[b : b + 1].cuda().requires_grad_(True)
+        db = deg[b : b + 1].cuda().requires_grad_(True)
+        symm_b, asymm_b = chain(rb, db)
+        grads_b = torch.autograd.grad(
+            (symm_b * up_s[b : b + 1]).sum() + (asymm_b * up_a[b : b + 1]).sum(), (rb, db)
+        )
+        assert torch.equal(symm[b : b + 1], symm_b), b
+        assert torch.equal(asymm[b : b + 1], asymm_b), b
+        assert torch.equal(grads[0][b : b + 1], grads_b[0]), b
+        assert torch.equal(grads[1][b : b + 1], grads_b[1]), b
+
+
 @pytest.mark.parametrize("nband", [17, 33, 64, 65, 100, 128])
 def test_chain_other_band_counts(nband):
     """Band counts other than 49 (``test_triton_chain.py:668-717``): random

@@ -54,6 +54,11 @@ constexpr int kChunk = PESQ_CHUNK;                         // samples per lane
 constexpr int64_t kLaneStateWaves = 8192;
 constexpr int kSpan = kWave * kChunk;                      // samples per block
 constexpr int64_t kBlockSpan = kSpan;
+#ifndef PESQ_SPLIT_WAVES
+#define PESQ_SPLIT_WAVES 3
+#endif
+// wavefronts per block of the split aggregate pass (each on its own sections)
+constexpr int kSplitWaves = PESQ_SPLIT_WAVES;
 constexpr int kMaxSections = PESQ_IIR_MAX_SECTIONS;
 // power levels: A^(kChunk 2^j); j = 0..5 in-wave, 6 = one block, 6..11 the
 // block level scan over 64 blocks
@@ -665,27 +670,40 @@ __global__ void __launch_bounds__(kWave)
     }
 }
 
-// The aggregate pass with lane states by two wavefronts per block, each on
-// its own sections: the first runs filter A's sections 0 .. kSplit - 1, the
-// second A's others and filter B's.  The sections are independent recursions,
-// so this writes the same bits as iir_aggregate_kernel, with about half the
-// serial work per wavefront (both read the block's inputs).
-template <int NA, int NB, int kSplit, class Mode>
-__global__ void __launch_bounds__(2 * kWave)
+// The aggregate pass with lane states by kWaves wavefronts per block, each on
+// its own sections: wavefront w runs sections [w NS / kWaves, (w + 1) NS /
+// kWaves) of the NS = NA + NB (A's sections first, then B's).  The sections
+// are independent recursions, so this writes the same bits as
+// iir_aggregate_kernel, with 1 / kWaves of the serial work per wavefront (all
+// of them read the block's inputs).
+template <int NA, int NB, int kWaves, int W, class Mode>
+__device__ __forceinline__ void aggregate_split_wave(const Mode &m, const IirTable &t, double *aggr,
+                                                     double *lanes, int64_t len, int nblk, int row,
+                                                     int blk, int lane, int w) {
+    constexpr int NS = NA + NB;
+    constexpr int lo = W * NS / kWaves, hi = (W + 1) * NS / kWaves;
+    constexpr int na = (hi < NA ? hi : NA) - (lo < NA ? lo : NA);  // A's sections in [lo, hi)
+    constexpr int nb = hi - lo - na;
+    if (w == W) {
+        aggregate_block<na, nb, lo, NS>(m, t, aggr, lanes, len, nblk, row, blk, lane);
+    } else if constexpr (W + 1 < kWaves) {
+        aggregate_split_wave<NA, NB, kWaves, W + 1>(m, t, aggr, lanes, len, nblk, row, blk, lane,
+                                                     w);
+    }
+}
+
+template <int NA, int NB, int kWaves, class Mode>
+__global__ void __launch_bounds__(kWaves * kWave)
     iir_aggregate_split_kernel(Mode m, const IirTable *__restrict__ table,
                                double *__restrict__ aggr, double *__restrict__ lanes, int64_t len,
                                int nblk) {
-    static_assert(kSplit > 0 && kSplit < NA, "both wavefronts take sections of filter A");
+    static_assert(kWaves >= 2 && kWaves <= NA + NB, "one section per wavefront at least");
     const IirTable &t = *table;
     const int row = blockIdx.x / nblk;
     const int blk = blockIdx.x - row * nblk;
     const int lane = threadIdx.x % kWave;
-    if (wave_index() == 0) {
-        aggregate_block<kSplit, 0, 0, NA + NB>(m, t, aggr, lanes, len, nblk, row, blk, lane);
-    } else {
-        aggregate_block<NA - kSplit, NB, kSplit, NA + NB>(m, t, aggr, lanes, len, nblk, row, blk,
-                                                          lane);
-    }
+    aggregate_split_wave<NA, NB, kWaves, 0>(m, t, aggr, lanes, len, nblk, row, blk, lane,
+                                            wave_index());
 }
 
 // Exclusive scan of the block aggregates, one (row, section) sequence per
@@ -903,8 +921,8 @@ __global__ void __launch_bounds__(kWave)
 
 // Host side: aggregate, prefix and output launches of one scan pass over
 // `rows` rows; `ws` holds scan_workspace_doubles(rows, nblk, NA + NB).
-// split: the aggregate pass of lane-state grids by two wavefronts per block
-// (iir_aggregate_split_kernel, A's first (NA + NB) / 2 sections in one of them).
+// split: the aggregate pass of lane-state grids by kSplitWaves wavefronts per
+// block (iir_aggregate_split_kernel).
 template <int NA, int NB, class Mode>
 int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, int64_t len,
                 bool aggregate, bool output, hipStream_t stream, bool split = false) {
@@ -920,13 +938,11 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
     const bool fused = plan.fused_prefix;
     if (aggregate) {
         bool launched = false;
-        if constexpr (NA >= 2) {
+        if constexpr (NA + NB >= kSplitWaves) {
             if (lane_states && split) {
-                // as many sections in each wavefront as the filters allow
-                constexpr int kSplit = (NA + NB) / 2 < NA ? (NA + NB) / 2 : NA - 1;
-                hipLaunchKernelGGL((iir_aggregate_split_kernel<NA, NB, kSplit, Mode>), dim3(grid),
-                                   dim3(2 * kWave), 0, stream, m, table, aggr, lanes, len,
-                                   static_cast<int>(nblk));
+                hipLaunchKernelGGL((iir_aggregate_split_kernel<NA, NB, kSplitWaves, Mode>),
+                                   dim3(grid), dim3(kSplitWaves * kWave), 0, stream, m, table,
+                                   aggr, lanes, len, static_cast<int>(nblk));
                 launched = true;
             }
         }

@@ -1710,7 +1710,8 @@ static void scan_kernel_names(const ScanPlan &S, const char *mode, std::string &
     if (host_power) {
         out += "iir_aggregate_kernel<0, 1, PipeBwdPreMode, true, 5, 6>;";
     } else if (kSplitAggregate && S.lane_states) {
-        out += std::string("iir_aggregate_split_kernel<5, 1, 3, ") + mode + ">;";
+        out += "iir_aggregate_split_kernel<5, 1, " + std::to_string(kSplitWaves) + ", " + mode +
+               ">;";
     } else {
         out += std::string("iir_aggregate_kernel<5, 1, ") + mode + ", " + lanes + ", 0, 6>;";
     }
