@@ -35,6 +35,8 @@
 // pre-emphasis filter together.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace pesq {
@@ -280,6 +282,14 @@ __device__ __forceinline__ void block_start_load(const double *row_aggr, int nbl
     }
 }
 
+// Modes whose output pass reads per row constants from memory (Mode::Pre,
+// m.prefetch(row, lane, pre) issuing the loads, m.setup(row, sh, lane, pre)
+// using them): the output kernel requests them before its raw inputs.
+template <class M, class = void>
+struct HasPre : std::false_type {};
+template <class M>
+struct HasPre<M, std::void_t<typename M::Pre>> : std::true_type {};
+
 // the lane's pair power M^(2 (63 - lane)) of every section, loaded with the
 // block end states (block_start_load) so that its latency overlaps theirs
 template <int NS>
@@ -408,6 +418,9 @@ __device__ __forceinline__ void store16(double *p, const double *src) {
     *reinterpret_cast<double2 *>(p) = make_double2(src[0], src[1]);
 }
 
+// One path for all inputs (16-byte vectors when every input's chunk is full
+// and aligned, else elements), so that the loads of all inputs are issued
+// before the first wait for one of them.
 template <class Mode>
 __device__ __forceinline__ void load_chunk(const Mode &m, int row, int64_t j0, int64_t len,
                                            typename Mode::In (&in)[kChunk][Mode::kInputs]) {
@@ -415,16 +428,28 @@ __device__ __forceinline__ void load_chunk(const Mode &m, int row, int64_t j0, i
     constexpr int kVec = 16 / sizeof(T);
     const bool full = j0 + kChunk <= len;
     const int64_t lo = chunk_lo<Mode::kReverse>(j0, len);
+    bool vec = full;
 #pragma unroll
     for (int q = 0; q < Mode::kInputs; ++q) {
-        const T *base = m.src(row, q);
-        T buf[kChunk];
-        if (full && (reinterpret_cast<uintptr_t>(base + lo) & 15) == 0) {
+        vec = vec && (reinterpret_cast<uintptr_t>(m.src(row, q) + lo) & 15) == 0;
+    }
+    if (vec) {
+        T buf[Mode::kInputs][kChunk];
 #pragma unroll
-            for (int r = 0; r < kChunk / kVec; ++r) load16(base + lo + kVec * r, buf + kVec * r);
+        for (int q = 0; q < Mode::kInputs; ++q) {
+            const T *base = m.src(row, q);
 #pragma unroll
-            for (int i = 0; i < kChunk; ++i) in[i][q] = buf[Mode::kReverse ? kChunk - 1 - i : i];
-        } else {
+            for (int r = 0; r < kChunk / kVec; ++r) load16(base + lo + kVec * r, buf[q] + kVec * r);
+        }
+#pragma unroll
+        for (int q = 0; q < Mode::kInputs; ++q) {
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i) in[i][q] = buf[q][Mode::kReverse ? kChunk - 1 - i : i];
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < Mode::kInputs; ++q) {
+            const T *base = m.src(row, q);
 #pragma unroll
             for (int i = 0; i < kChunk; ++i) {
                 const int64_t j = j0 + i;
@@ -852,10 +877,20 @@ __global__ void __launch_bounds__(kWave)
             s.v(k) = w.y;
         }
     }
-    double sh[4];
-    m.setup(row, sh, lane);
+    // the row constants' loads (Modes with Pre) go out before the raw
+    // inputs', whose placement waits for every load issued before it: one
+    // wait for all of them
     typename Mode::In in[kChunk][Mode::kInputs];
-    load_chunk(m, row, j0, len, in);
+    double sh[4];
+    if constexpr (HasPre<Mode>::value) {
+        typename Mode::Pre pre;
+        m.prefetch(row, lane, pre);
+        load_chunk(m, row, j0, len, in);
+        m.setup(row, sh, lane, pre);
+    } else {
+        load_chunk(m, row, j0, len, in);
+        m.setup(row, sh, lane);
+    }
     const IirTable &t2 = *table;
     if constexpr (kFusedPrefix) {
         __shared__ double red[wave_sums_lds_doubles<2 * NS>()];

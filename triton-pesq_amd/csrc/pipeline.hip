@@ -118,10 +118,43 @@ struct PipeBwdMode {
         xb = in[1];
     }
     // scale and scale S / E, S = sum of the per hop block partials of dL/dp . p
-    __device__ __forceinline__ void setup(int row, double *sh, int lane) const {
-        const int nmine = lane < nhop ? (nhop - 1 - lane) / kWave + 1 : 0;
-        double s = nmine > 0 ? strided_sum(spart + int64_t(row) * nhop + lane, nmine, kWave)
-                             : 0.0;
+    // (lane l sums partials l, l + 64, ...: the first 8 are requested by
+    // prefetch, any further ones here, in the order of strided_sum)
+    struct Pre {
+        double v[8];
+    };
+    __device__ __forceinline__ int mine(int lane) const {
+        return lane < nhop ? (nhop - 1 - lane) / kWave + 1 : 0;
+    }
+    __device__ __forceinline__ void prefetch(int row, int lane, Pre &pre) const {
+        const int n = mine(lane);
+        const double *src = spart + int64_t(row) * nhop + (lane < nhop ? lane : 0);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            pre.v[u] = src[int64_t(u < n ? u : (n > 0 ? n - 1 : 0)) * kWave];
+        }
+    }
+    __device__ __forceinline__ void setup(int row, double *sh, int lane, const Pre &pre) const {
+        const int n = mine(lane);
+        double s = 0.0;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            if (u < n) s += pre.v[u];
+        }
+        if (n > 8) {
+            const double *src = spart + int64_t(row) * nhop + lane;
+            for (int i0 = 8; i0 < n; i0 += 8) {
+                double v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    v[u] = src[int64_t(i0 + u < n ? i0 + u : n - 1) * kWave];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    if (i0 + u < n) s += v[u];
+                }
+            }
+        }
         s = wave_sum(s);
         const double *rc = rowconst + int64_t(row0 + row) * 4;
         sh[1] = rc[2];
