@@ -502,7 +502,7 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
         __syncthreads();
         tw = TW{lds_pass, lds_tw512, lane};
     } else {
-        tw.load(t.tw256, t.tw512, lane);
+        tw.load_staged(StagedTwiddles<real>::pass(t), StagedTwiddles<real>::fold(t), lane);
     }
     float win[8];
     if constexpr (!kLean) {

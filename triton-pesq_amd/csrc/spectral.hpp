@@ -134,6 +134,16 @@ __device__ __forceinline__ typename Vec2<real>::type to_vec2(double2 w) {
     return {static_cast<real>(w.x), static_cast<real>(w.y)};
 }
 
+// The pass twiddles laid out per (pass, r, k) with k = lane mod ns running
+// fastest, for tables staged in LDS: the reads of one pass are unit stride
+// (pass 1 reads 4 entries, a broadcast), so they do not conflict on the banks.
+//   pass[pass_offset(p) + (r - 1) ns + k] = e^{-2 pi i k r / (4 ns)}, ns = 4^p
+//   fold[f]                               = e^{-2 pi i f / 512}
+constexpr int kPassTwiddles = 3 * (4 + 16 + 64);
+__host__ __device__ __forceinline__ constexpr int pass_offset(int p) {
+    return p == 1 ? 0 : (p == 2 ? 3 * 4 : 3 * (4 + 16));
+}
+
 // Per lane twiddles of every FFT pass and of the real-FFT fold, loaded once
 // per kernel so that no pass waits on a memory load:
 //   pass[p][r - 1] = e^{-2 pi i k r / (4 ns)}, ns = 4^p (p = 1..3), k = lane mod ns
@@ -157,6 +167,20 @@ struct Twiddles {
 #pragma unroll
         for (int r = 0; r < 4; ++r) fold[r] = to_vec2<real>(tw512[lane + 64 * r]);
     }
+    // the same values from the tables kept in the arithmetic's precision
+    // (the per pass layout of LdsTwiddles, and the fold's): no conversions
+    // for the compiler to place inside the frame loop
+    __device__ __forceinline__ void load_staged(const T2 *pass_tab, const T2 *fold_tab, int lane) {
+#pragma unroll
+        for (int p = 1; p < 4; ++p) {
+            const int ns = 1 << (2 * p);
+#pragma unroll
+            for (int r = 1; r < 4; ++r)
+                pass[p - 1][r - 1] = pass_tab[pass_offset(p) + (r - 1) * ns + (lane & (ns - 1))];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) fold[r] = fold_tab[lane + 64 * r];
+    }
     __device__ __forceinline__ T2 pass_tw(int p, int r) const { return pass[p - 1][r - 1]; }
     __device__ __forceinline__ T2 fold_tw(int r) const { return fold[r]; }
 };
@@ -174,16 +198,6 @@ struct LazyTwiddles {
     }
     __device__ __forceinline__ double2 fold_tw(int r) const { return tw512[lane + 64 * r]; }
 };
-
-// The pass twiddles laid out per (pass, r, k) with k = lane mod ns running
-// fastest, for tables staged in LDS: the reads of one pass are unit stride
-// (pass 1 reads 4 entries, a broadcast), so they do not conflict on the banks.
-//   pass[pass_offset(p) + (r - 1) ns + k] = e^{-2 pi i k r / (4 ns)}, ns = 4^p
-//   fold[f]                               = e^{-2 pi i f / 512}
-constexpr int kPassTwiddles = 3 * (4 + 16 + 64);
-__host__ __device__ __forceinline__ constexpr int pass_offset(int p) {
-    return p == 1 ? 0 : (p == 2 ? 3 * 4 : 3 * (4 + 16));
-}
 
 // entry i (0 <= i < kPassTwiddles) of the per pass table, from the 256-point table
 __host__ __device__ __forceinline__ double2 pass_twiddle_entry(const double2 *tw256, int i) {
