@@ -105,6 +105,26 @@ def test_strided_and_deterministic():
     assert torch.equal(mod(x)[2:3], mod(x[2:3]))
 
 
+def test_nan_does_not_cross_rows():
+    """A poisoned row does not contaminate its neighbours, forward and adjoint
+    (``test_triton_iir.py:574-586``): every scan block belongs to one row."""
+
+    b, a = FILTERS["power"]
+    mod = HipIIR(b, a).cuda()
+    x = torch.randn(3, 5000, device="cuda")
+    x[1, 2500] = float("nan")
+    xg = x.clone().requires_grad_(True)
+    y = mod(xg)
+    assert torch.isfinite(y[0]).all() and torch.isfinite(y[2]).all()
+    assert torch.isnan(y[1, 2500:]).any() and torch.isfinite(y[1, :2500]).all()
+    g = torch.randn_like(y)
+    g[1, 1000] = float("nan")
+    (gx,) = torch.autograd.grad(y, xg, grad_outputs=g)
+    assert torch.isfinite(gx[0]).all() and torch.isfinite(gx[2]).all()
+    # the adjoint runs back in time: the poisoned upstream reaches samples before it
+    assert torch.isnan(gx[1, :1001]).any() and torch.isfinite(gx[1, 1001:]).all()
+
+
 def test_errors():
     mod = HipIIR(*FILTERS["pre"]).cuda()
     with pytest.raises(RuntimeError):

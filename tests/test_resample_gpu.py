@@ -129,6 +129,29 @@ def test_identity_and_shapes():
     assert m48(torch.randn(2, 3, 1000, device="cuda")).shape == (2, 3, 334)
 
 
+@pytest.mark.parametrize("orig,new", [(48000, 16000), (44100, 16000), (8000, 16000)])
+@pytest.mark.parametrize("shape", [(5001,), (2, 3, 5001), (2, 1, 2, 777)])
+def test_leading_dimensions(orig, new, shape):
+    """Any number of leading dimensions is packed and unpacked like torchaudio
+    (``test_triton_resample.py:556-572``): values and gradients of a
+    ``[..., sample]`` input against the float64 oracle on its rows."""
+
+    mod = HipResample(orig, new).cuda()
+    x = torch.randn(*shape, generator=torch.Generator().manual_seed(sum(shape)))
+    xg = x.cuda().requires_grad_(True)
+    y = mod(xg)
+    n_out = O.resample_length(shape[-1], orig, new)
+    assert y.shape == shape[:-1] + (n_out,)
+    rows = x.reshape(-1, shape[-1]).double().requires_grad_(True)
+    want = O.resample(rows, orig, new)
+    assert _close(y.reshape(-1, n_out), want.detach())
+    g = torch.randn(*y.shape, generator=torch.Generator().manual_seed(3))
+    (gx,) = torch.autograd.grad(y, xg, grad_outputs=g.cuda())
+    (want_g,) = torch.autograd.grad(want, rows, grad_outputs=g.reshape(-1, n_out).double())
+    assert gx.shape == shape
+    assert _close(gx.reshape(-1, shape[-1]), want_g)
+
+
 @pytest.mark.parametrize("config,items,samples", [(3, 2, 44100), (5, 3, 48000)])
 def test_resampled_pipeline_matches_float64(config, items, samples):
     ref, deg, fs = synthetic_config(config, items=items, samples=samples)
