@@ -209,6 +209,35 @@ def test_batch_independence(model):
     assert torch.equal(batched, single)
 
 
+def test_nan_item_stays_in_its_item(model):
+    """A NaN in one item's degraded signal leaves the other items' losses and
+    gradients (w.r.t. both signals) bitwise as they are without it: every
+    reduction of the fused kernels (row energies, band means, PSQM windows,
+    block prefixes) stays inside its item, as the reference's row isolation
+    test asks of its filter (``test_triton_iir.py:574-586``)."""
+
+    ref, deg = speech_like_pair(3, 24000, seed=19, noise=0.1)
+    r, d = torch.from_numpy(ref).cuda(), torch.from_numpy(deg).cuda()
+
+    def step(deg_t):
+        rr = r.clone().requires_grad_(True)
+        dd = deg_t.clone().requires_grad_(True)
+        loss = model(rr, dd)
+        gr, gd = torch.autograd.grad(loss.sum(), (rr, dd))
+        return loss, gr, gd
+
+    clean = step(d)
+    poisoned_deg = d.clone()
+    poisoned_deg[1, 12000] = float("nan")
+    poisoned = step(poisoned_deg)
+    # the poisoned item itself is not pinned to NaN: the chain's clamps take
+    # the non-NaN operand, as the reference's Triton chain does
+    # (tl.minimum / tl.maximum, ``triton_ops/chain.py:174,325,347-348``)
+    assert not torch.equal(clean[0][1], poisoned[0][1])
+    for want, got in zip(clean, poisoned):
+        assert torch.equal(want[0], got[0]) and torch.equal(want[2], got[2])
+
+
 def test_graph_replay_is_bit_exact(model):
     ref, deg = speech_like_pair(2, 16000, seed=10, noise=0.1)
     r = torch.from_numpy(ref).cuda().requires_grad_(True)
