@@ -104,8 +104,8 @@ def test_config4_full_batch_forward_and_backward():
     ref_np, deg_np, fs, weights, outputs, g_deg, kernels = _run_step(4)
     batch, length = ref_np.shape
     _assert_pipeline_variants(kernels, batch, length)
-    for name in ("iir_prefix_kernel<6>", "iir_output_kernel<5,1,PipeBwdMode,true,false>",
-                 "iir_output_kernel<5,1,PipeFwdMode,true,false>", "chain_bwd_kernel<4,1>",
+    for name in ("iir_prefix_kernel<6>", "iir_output_kernel<5,1,PipeBwdMode,true,false,false>",
+                 "iir_output_kernel<5,1,PipeFwdMode,true,false,false>", "chain_bwd_kernel<4,1>",
                  "chain_fwd_kernel<4,1>"):
         assert name in kernels, name
     # the STFT variant for large grids (its arithmetic type is the library's choice)
@@ -126,9 +126,9 @@ def test_config5_full_batch_forward_and_backward():
     length = O.resample_length(ref_np.shape[1], fs, 16000)
     _assert_pipeline_variants(kernels, batch, length)
     for name in ("iir_aggregate_kernel<5,1,PipeFwdMode,false,0,6>",
-                 "iir_output_kernel<5,1,PipeFwdMode,false,false>",
+                 "iir_output_kernel<5,1,PipeFwdMode,false,false,false>",
                  "iir_aggregate_kernel<5,1,PipeBwdMode,false,0,6>",
-                 "iir_output_kernel<5,1,PipeBwdMode,false,false>",
+                 "iir_output_kernel<5,1,PipeBwdMode,false,false,false>",
                  "chain_bwd_kernel<4,1>", "resample_fwd_window<3>", "resample_bwd_window<3>"):
         assert name in kernels, name
     _compare_with_oracle(ref_np, deg_np, fs, weights, outputs, g_deg, range(batch))

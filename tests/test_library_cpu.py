@@ -326,6 +326,30 @@ def test_model_table_pack_rejects_bad_bands():
                          m.loudness.exp, m.fbank.width_bark, m.fbank.total_width, 0.1866055)
 
 
+def test_pre_emphasis_decays_within_the_warm_up():
+    """The backward's output pass starts the pre-emphasis filter 2048 samples
+    before each block from a zero state: the standard filter's state keeps at
+    most 3e-24 of itself over that span (largest entry of A^2048; pole radius
+    0.973; the pack requires at most 1e-20), and a filter decaying more
+    slowly is refused where the table is packed."""
+
+    from torch_pesq.hip_ops.pipeline import pack_model_table
+
+    m = PesqLoss(1.0, sample_rate=16000)
+    a = m.pre_filter[1].double().numpy()
+    comp = np.array([[-a[1] / a[0], 1.0], [-a[2] / a[0], 0.0]])
+    decay = np.abs(np.linalg.matrix_power(comp, 2048)).max()
+    assert decay < 3e-24
+    assert abs(np.abs(np.roots(a)).max() - 0.9726) < 1e-3
+
+    slow_a = torch.tensor([1.0, -1.98 * np.cos(0.1), 0.99 ** 2], dtype=torch.float64)
+    with pytest.raises((RuntimeError, ValueError), match="decays too slowly"):
+        pack_model_table(m.power_filter[0], m.power_filter[1], m.pre_filter[0], slow_a,
+                         m.to_spec.window, m.fbank.fbank, m.fbank.pow_dens_correction,
+                         m.loudness.threshs, m.loudness.exp, m.fbank.width_bark,
+                         m.fbank.total_width, 0.1866055)
+
+
 def test_cpu_inputs_and_bad_shapes_raise():
     m = PesqLoss(1.0, sample_rate=16000)
     ref = torch.zeros(2, 16000)
@@ -356,69 +380,68 @@ def test_graft_entry_exposes_build_and_smoke():
 #: chain kernels of grids above 512 chain tiles take four frames per wavefront
 #: (the STFT backward two).  Where the backward scan stores lane states and
 #: fuses its block prefix (c2, c3), the forward's chain kernel also runs the
-#: backward's level alignment aggregate and the backward's aggregate launch
-#: runs the pre-emphasis filter alone (PipeBwdPreMode, sections 5 of 6).  The
-#: aggregate pass of lane-state grids runs two wavefronts per block, each on
-#: its own sections (iir_aggregate_split_kernel).
+#: backward's level alignment aggregate and the backward's output pass warms
+#: the pre-emphasis filter up itself, so the backward has no aggregate launch
+#: (the output kernel's third flag).  The aggregate pass of lane-state grids
+#: runs three wavefronts per block, each on its own sections
+#: (iir_aggregate_split_kernel).
 VARIANTS = {
     # BASELINE c2: 16 rows x 125 blocks, 8 x 32 tiles
     (8, 128000, 2): (
         ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>",
-         "iir_output_kernel<5, 1, PipeFwdMode, true, true>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, true, false>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
-         "iir_aggregate_kernel<0, 1, PipeBwdPreMode, true, 5, 6>",
-         "iir_output_kernel<5, 1, PipeBwdMode, true, true>"],
+         "iir_output_kernel<5, 1, PipeBwdMode, true, true, true>"],
     ),
     # BASELINE c4: 938 blocks per row (prefix kernel), 4 x 235 = 940 tiles, items
     # of 235 tiles (per item band totals)
     (4, 960000, 2): (
         ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, false, false>",
          "stft_fwd_kernel<float, true, 8>", "band_totals_kernel<16, 2>",
          "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<4, 1>", "band_totals_kernel<8, 1>", "stft_bwd_kernel<float, 2, 8>",
          "iir_aggregate_split_kernel<5, 1, 3, PipeBwdMode>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
+         "iir_output_kernel<5, 1, PipeBwdMode, true, false, false>"],
     ),
     # one item of 65 tiles (1033 frames): just past the band totals threshold
     # (259 blocks per row: the prefix kernel)
     (1, 264704, 1): (
         ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, false, false>",
          "stft_fwd_kernel<float, false, 8>", "band_totals_kernel<16, 2>",
          "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "band_totals_kernel<8, 1>", "stft_bwd_kernel<float, 1, 9>",
          "iir_aggregate_split_kernel<5, 1, 3, PipeBwdMode>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
+         "iir_output_kernel<5, 1, PipeBwdMode, true, false, false>"],
     ),
     # one item of 64 tiles (1023 frames): the largest without band totals
     (1, 262144, 1): (
         ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeFwdMode, true, false>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, false, false>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
          "iir_aggregate_split_kernel<5, 1, 3, PipeBwdMode>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeBwdMode, true, false>"],
+         "iir_output_kernel<5, 1, PipeBwdMode, true, false, false>"],
     ),
     # BASELINE c5 after the 3:1 resampler: 512 x 63 = 32256 forward scan
     # wavefronts, 256 x 63 = 16128 backward ones (both above 8192)
     (256, 64000, 2): (
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, false, 0, 6>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeFwdMode, false, false>",
+         "iir_output_kernel<5, 1, PipeFwdMode, false, false, false>",
          "stft_fwd_kernel<float, true, 8>", "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float, 2, 8>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, false, 0, 6>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeBwdMode, false, false>"],
+         "iir_output_kernel<5, 1, PipeBwdMode, false, false, false>"],
     ),
     # BASELINE c3 after the 441:160 resampler: a small grid like c2
     (16, 64000, 2): (
         ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>",
-         "iir_output_kernel<5, 1, PipeFwdMode, true, true>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, true, false>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
-         "iir_aggregate_kernel<0, 1, PipeBwdPreMode, true, 5, 6>",
-         "iir_output_kernel<5, 1, PipeBwdMode, true, true>"],
+         "iir_output_kernel<5, 1, PipeBwdMode, true, true, true>"],
     ),
 }
 

@@ -75,7 +75,7 @@ def test_only_library_kernels_touch_the_data(model, batch, samples):
 def test_sum_and_implicit_gradient_add_only_pytorch_glue(model):
     """``grad(loss.sum(), deg)``: PyTorch's own reduction, the ones fill of the
     implicit gradient and the contiguous copy of its broadcast (three [B]
-    sized kernels) join the library's nine."""
+    sized kernels) join the library's eight."""
 
     ref, deg = speech_like_pair(8, 128000, seed=22, noise=0.1)
     r = torch.from_numpy(ref).cuda()

@@ -57,12 +57,12 @@ def test_large_grid_variants_match_small_grid_ones():
     # the batch and the single items take different variants of every stage
     assert "stft_fwd_kernel<float, true, 8>" in wide and "stft_fwd_kernel<float, false, 8>" in narrow
     assert "chain_fwd_kernel<4, 1>" in wide and "chain_fwd_kernel<8, 1>" in narrow
-    assert "iir_output_kernel<5, 1, PipeFwdMode, false, false>" in wide
-    assert "iir_output_kernel<5, 1, PipeFwdMode, true, false>" in narrow
+    assert "iir_output_kernel<5, 1, PipeFwdMode, false, false, false>" in wide
+    assert "iir_output_kernel<5, 1, PipeFwdMode, true, false, false>" in narrow
     assert "stft_bwd_kernel<float, 2, 8>" in wide_b and "stft_bwd_kernel<float, 1, 9>" in narrow_b
     assert "chain_bwd_kernel<4, 1>" in wide_b and "chain_bwd_kernel<16, 1>" in narrow_b
-    assert "iir_output_kernel<5, 1, PipeBwdMode, false, false>" in wide_b
-    assert "iir_output_kernel<5, 1, PipeBwdMode, true, false>" in narrow_b
+    assert "iir_output_kernel<5, 1, PipeBwdMode, false, false, false>" in wide_b
+    assert "iir_output_kernel<5, 1, PipeBwdMode, true, false, false>" in narrow_b
 
     ref_np, deg_np = speech_like_pair(ITEMS, SAMPLES, seed=21, noise=0.15)
     ref = torch.from_numpy(ref_np).cuda()

@@ -202,6 +202,21 @@ extern "C" int pesq_model_table_pack(const pesq_model_constants *c, void *out) {
             delete t;
             return st;
         }
+        // the backward's output pass starts the pre-emphasis filter kWarmBlocks
+        // blocks early from a zero state (iir.hpp, kWarmB): its state must
+        // have decayed below kWindowDecay over that span
+        const int q = t->iir.na;
+        double m[4] = {1.0, 0.0, 0.0, 1.0};
+        for (int w = 0; w < kWarmBlocks; ++w) mat_mul(t->iir.pw[kLevelBlock][q], m, m);
+        double mx = 0.0;
+        for (double v : m) mx = std::fmax(mx, std::fabs(v));
+        if (!(mx <= kWindowDecay)) {
+            delete t;
+            set_error("the pre-emphasis filter decays too slowly for the pipeline: its state "
+                      "keeps %.3g of itself over %d samples (at most %.0e)",
+                      mx, kWarmBlocks * kSpan, kWindowDecay);
+            return PESQ_ERR_ARGUMENT;
+        }
     }
 
     const double two_pi = 6.283185307179586476925286766559;

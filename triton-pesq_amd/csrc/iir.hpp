@@ -97,6 +97,18 @@ struct IirTable {
 constexpr int kFusedPrefixBlocks = PESQ_FUSED_PREFIX_BLOCKS;
 static_assert(kFusedPrefixBlocks <= 2 * kWave, "two blocks per lane");
 
+// Warm-up of filter B.  A block's start state differs from the end state of
+// the kWarmBlocks blocks before it, run from a zero state, by
+// A^(kWarmBlocks kSpan) applied to the state there, i.e. by at most twice
+// kWindowDecay of the state's largest component when every entry of that
+// matrix power is below kWindowDecay (checked where the pipeline's table is
+// packed).  For the pre-emphasis filter (pole radius 0.973) the largest entry
+// of A^2048 is 3e-24, far below the float64 rounding of the recursion, so the backward's output
+// pass forms filter B's block start states itself (kWarmB) and needs no
+// aggregate pass for it.
+constexpr int kWarmBlocks = 2;
+constexpr double kWindowDecay = 1e-20;
+
 // Launch plan of a scan over `rows` rows of nblk blocks (one wavefront each):
 // whether the aggregate pass stores the lane states, and whether the output
 // pass derives the block start states itself (no prefix launch).  The
@@ -265,13 +277,16 @@ __device__ __forceinline__ void scan_wave_dpp(const Powers &t, Bank<NS> &z, int 
 // start with M^(2 (63 - i)) (blk_pw2); the 64 lanes' terms are then summed in
 // LDS (wave_sums_lds, `red`) and every lane reads the sums back.  The loads are
 // issued first so that they overlap the kernel's other loads.
-template <int NS>
+template <int NS, int NL = NS>
 __device__ __forceinline__ void block_start_load(const double *row_aggr, int nblk, int blk,
                                                  int lane, Bank<NS> &e0, Bank<NS> &e1) {
+    // sections NL .. NS - 1 (none by default) take no aggregates: zero
+#pragma unroll
+    for (int k = NL; k < NS; ++k) e0.u[k] = e0.v[k] = e1.u[k] = e1.v[k] = 0.0;
     const int j0 = blk - 2 * kWave + 2 * lane;
     const int c0 = j0 >= 0 ? j0 : 0, c1 = j0 + 1 >= 0 ? j0 + 1 : 0;
 #pragma unroll
-    for (int k = 0; k < NS; ++k) {
+    for (int k = 0; k < NL; ++k) {
         const double *sec = row_aggr + int64_t(k) * nblk * 2;
         const double2 a = *reinterpret_cast<const double2 *>(sec + 2 * c0);
         const double2 b = *reinterpret_cast<const double2 *>(sec + 2 * c1);
@@ -837,13 +852,15 @@ __global__ void __launch_bounds__(kWave *kPrefixWaves)
     }
 }
 
-template <int NA, int NB, class Mode, bool kLaneStates, bool kFusedPrefix>
+template <int NA, int NB, class Mode, bool kLaneStates, bool kFusedPrefix, bool kWarmB = false>
 __global__ void __launch_bounds__(kWave)
     iir_output_kernel(Mode m, const IirTable *__restrict__ table,
                       const double *__restrict__ aggr, const double *__restrict__ lanes,
                       int64_t len, int nblk) {
     constexpr int NS = NA + NB;
     static_assert(kLaneStates || !kFusedPrefix, "the fused prefix is for small grids");
+    static_assert(!kWarmB || (kLaneStates && kFusedPrefix && NB == 1),
+                  "filter B warms up beside stored lane states of A and the fused prefix");
     const int row = blockIdx.x / nblk;
     const int blk = blockIdx.x - row * nblk;
     const int lane = threadIdx.x;
@@ -856,7 +873,7 @@ __global__ void __launch_bounds__(kWave)
     Bank<NS> e0, e1;  // kFusedPrefix: the block aggregates this block starts from
     PairPowers<NS> pp;
     if constexpr (kFusedPrefix) {
-        block_start_load<NS>(row_aggr, nblk, blk, lane, e0, e1);
+        block_start_load<NS, kWarmB ? NA : NS>(row_aggr, nblk, blk, lane, e0, e1);
         pp.load(*table, lane);
     } else {
 #pragma unroll
@@ -871,10 +888,34 @@ __global__ void __launch_bounds__(kWave)
         const double2 *src =
             reinterpret_cast<const double2 *>(lanes) + (int64_t(row) * nblk + blk) * NS * kWave;
 #pragma unroll
-        for (int k = 0; k < NS; ++k) {
+        for (int k = 0; k < (kWarmB ? NA : NS); ++k) {
             const double2 w = src[k * kWave + lane];
             s.u(k) = w.x;
             s.v(k) = w.y;
+        }
+    }
+    // kWarmB: filter B's inputs of this lane's chunks in the kWarmBlocks
+    // blocks before this one (warm[w - 1] is block blk - w; before the row
+    // start block 0 is read and not used), requested with the other loads
+    typename Mode::In warm[kWarmB ? kWarmBlocks : 1][kChunk][Mode::kInputs];
+    if constexpr (kWarmB) {
+        // (B's filter input is the Mode's input 1 as it is: PipeBwdMode)
+        static_assert(Mode::kInputs == 2, "filter B reads input 1");
+        const typename Mode::In *b_src = m.src(row, 1);
+#pragma unroll
+        for (int w = 1; w <= kWarmBlocks; ++w) {
+            const int64_t jw = blk - w >= 0 ? j0 - int64_t(w) * kSpan : int64_t(lane) * kChunk;
+            const int64_t lo = chunk_lo<Mode::kReverse>(jw, len);  // full chunks
+            typename Mode::In buf[kChunk];
+#pragma unroll
+            for (int r = 0; r < kChunk / 4; ++r) {
+                __builtin_memcpy(buf + 4 * r, b_src + lo + 4 * r, 4 * sizeof(typename Mode::In));
+            }
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i) {
+                warm[w - 1][i][0] = typename Mode::In(0);
+                warm[w - 1][i][1] = buf[Mode::kReverse ? kChunk - 1 - i : i];
+            }
         }
     }
     // the row constants' loads (Modes with Pre) go out before the raw
@@ -900,6 +941,49 @@ __global__ void __launch_bounds__(kWave)
             p.u(k) = e0.u[k];
             p.v(k) = e0.v[k];
         }
+    }
+    if constexpr (kWarmB) {
+        // filter B's block start state: its chunk end states from zero in
+        // the previous blocks (weighted sums), v = sum_w M^(w - 1) e_(blk - w)
+        // per lane (oldest block first), carried to the block end by
+        // A^(kChunk (63 - lane)) and summed over the lanes in LDS
+        Coeffs<NA, 0, Mode::kB2> none;
+        Coeffs<NA, NB, Mode::kB2> wb;
+        wb.load(t2, t2.c0b);
+        const double *mk = t2.pw[kLevelBlock][NA];
+        double vu = 0.0, vv = 0.0;
+#pragma unroll
+        for (int w = kWarmBlocks; w >= 1; --w) {
+            if (blk - w < 0) continue;  // wave uniform
+            const double u = vu, v = vv;
+            vu = fma(mk[0], u, mk[1] * v);
+            vv = fma(mk[2], u, mk[3] * v);
+            BankPair<0, NB, NA> e;
+            e.zero();
+            zero_run<false, true>(m, t2, none, wb, warm[w - 1], j0 - int64_t(w) * kSpan, len, e);
+            vu += e.b.u[0];
+            vv += e.b.v[0];
+        }
+        __shared__ double red_b[wave_sums_lds_doubles<2>()];
+        const double *lp = t2.lane_pw[NA][kWave - 1 - lane];
+        const double wsum[2] = {fma(lp[0], vu, lp[1] * vv), fma(lp[2], vu, lp[3] * vv)};
+        const double sum = wave_sums_lds(wsum, red_b, lane);  // component j in lane 4 j
+        if (lane % 4 == 0 && lane / 4 < 2) red_b[lane / 4] = sum;
+        wave_lds_fence();
+        p.b.u[0] = red_b[0];
+        p.b.v[0] = red_b[1];
+        wave_lds_fence();
+        // and its in-block lane start states, as the aggregate pass forms them
+        BankPair<0, NB, NA> sb;
+        sb.zero();
+        if (general_chunk(j0, len)) {
+            zero_run<true, false>(m, t2, none, wb, in, j0, len, sb);
+        } else {
+            zero_run<false, false>(m, t2, none, wb, in, j0, len, sb);
+        }
+        sb.scan_chunks(t2, lane);
+        s.b.u[0] = dpp_move<0x138, 0xF>(sb.b.u[0]);  // wave_shr:1 (lane 0 reads 0)
+        s.b.v[0] = dpp_move<0x138, 0xF>(sb.b.v[0]);
     }
     if constexpr (!kLaneStates) {
         // the in-block start states again: zero state run, scan, shift by a lane
@@ -960,7 +1044,8 @@ __global__ void __launch_bounds__(kWave)
 // block (iir_aggregate_split_kernel).
 template <int NA, int NB, class Mode>
 int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, int64_t len,
-                bool aggregate, bool output, hipStream_t stream, bool split = false) {
+                bool aggregate, bool output, hipStream_t stream, bool split = false,
+                bool warm_b = false) {
     constexpr int NS = NA + NB;
     static_assert(NS <= kMaxSections, "too many sections");
     const int64_t nblk = cdiv(len, kBlockSpan);
@@ -1004,7 +1089,17 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
         const double *ca = aggr;
         const double *cl = lanes;
         const int nb = static_cast<int>(nblk);
-        if (fused) {
+        bool launched = false;
+        if constexpr (NB == 1 && Mode::kInputs == 2) {
+            if (fused && warm_b) {
+                // filter B's block starts from its own warm-up (no aggregates of B)
+                hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, true, true>),
+                                   dim3(grid), dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
+                launched = true;
+            }
+        }
+        if (launched) {
+        } else if (fused) {
             hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, true>), dim3(grid),
                                dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
         } else if (lane_states) {

@@ -167,11 +167,10 @@ struct PipeBwdMode {
     __device__ __forceinline__ void finish(int, int, double) const {}
 };
 
-// The two filters of the backward scan one at a time, for aggregate passes
-// over a subset of its sections (iir.hpp aggregate_block): the level
-// alignment filter (power^T) on f, run inside the forward's chain kernel, and
-// the pre-emphasis filter (pre^T) on dL/dp.  Same inputs and time order as
-// PipeBwdMode; they produce no outputs.
+// The level alignment filter (power^T on f) of the backward scan alone, for
+// its aggregate pass inside the forward's chain kernel (iir.hpp
+// aggregate_block over sections 0 .. 4); same input and time order as
+// PipeBwdMode, no outputs.
 struct PipeBwdPowerMode {
     static constexpr int kInputs = 1;
     static constexpr int kOutputs = 1;
@@ -189,26 +188,6 @@ struct PipeBwdPowerMode {
     __device__ __forceinline__ void inputs(double, const float *in, double &xa, double &xb) const {
         xa = in[0];
         xb = 0.0;
-    }
-};
-
-struct PipeBwdPreMode {
-    static constexpr int kInputs = 1;
-    static constexpr int kOutputs = 1;
-    static constexpr bool kRamp = false;
-    static constexpr bool kReverse = true;
-    static constexpr bool kAccumulates = false;
-    static constexpr bool kB2 = false;
-    using In = float;
-    using Out = float;
-
-    const float *gp;  // [nrg, len]
-    int64_t len;
-
-    __device__ __forceinline__ const float *src(int row, int) const { return gp + int64_t(row) * len; }
-    __device__ __forceinline__ void inputs(double, const float *in, double &xa, double &xb) const {
-        xa = 0.0;
-        xb = in[0];
     }
 };
 
@@ -1732,16 +1711,19 @@ static void launch_chain_bwd(const PipeArgs &a, unsigned grid, hipStream_t strea
 #ifndef PESQ_SPLIT_AGGREGATE
 #define PESQ_SPLIT_AGGREGATE 1
 #endif
-// the scans' aggregate pass of lane-state grids by two wavefronts per block
+// the scans' aggregate pass of lane-state grids by kSplitWaves wavefronts per block
 constexpr bool kSplitAggregate = PESQ_SPLIT_AGGREGATE != 0;
 
 // Names of the kernels of one scan pass, in launch order (host_power: the
-// backward's aggregate launch runs the pre-emphasis filter alone).
+// backward scan is its output launch alone).
 static void scan_kernel_names(const ScanPlan &S, const char *mode, std::string &out,
                               bool host_power = false) {
     const char *lanes = S.lane_states ? "true" : "false";
     if (host_power) {
-        out += "iir_aggregate_kernel<0, 1, PipeBwdPreMode, true, 5, 6>;";
+        // no aggregate launch: the level alignment filter's ran in the forward's
+        // chain kernel, the pre-emphasis filter warms up in the output pass
+        out += std::string("iir_output_kernel<5, 1, ") + mode + ", true, true, true>;";
+        return;
     } else if (kSplitAggregate && S.lane_states) {
         out += "iir_aggregate_split_kernel<5, 1, " + std::to_string(kSplitWaves) + ", " + mode +
                ">;";
@@ -1750,7 +1732,7 @@ static void scan_kernel_names(const ScanPlan &S, const char *mode, std::string &
     }
     if (!S.fused_prefix) out += "iir_prefix_kernel<6>;";
     out += std::string("iir_output_kernel<5, 1, ") + mode + ", " + lanes + ", " +
-           (S.fused_prefix ? "true" : "false") + ">;";
+           (S.fused_prefix ? "true" : "false") + ", false>;";
 }
 
 static int check_sizes(int64_t batch, int64_t len, const PipeLayout &L) {
@@ -1982,22 +1964,12 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
     m.nhop = static_cast<int>(L.nhop);
     if (L.host_power) {
         // the level alignment filter's aggregates came from the forward's
-        // chain kernel (sections 0..4); the pre-emphasis filter's (section 5)
-        // complete them, then the output pass runs both filters
+        // chain kernel (sections 0..4); the output pass warms the
+        // pre-emphasis filter (section 5) up itself and runs both filters
         double *aggr = region<double>(a.ws, L.aggr_b);
-        const int nblk = static_cast<int>(L.nblk);
-        if (stages & 4u) {
-            const PipeBwdPreMode pm{m.gp, len};
-            hipLaunchKernelGGL((iir_aggregate_kernel<0, kPreSections, PipeBwdPreMode, true,
-                                                     kPowerSections, kPipeSections>),
-                               dim3(static_cast<unsigned>(L.nrg * L.nblk)), dim3(kWave), 0, stream,
-                               pm, iir, aggr, aggr + scan_aggr_doubles(L.nrg, nblk, kPipeSections),
-                               len, nblk);
-            PESQ_CHECK_LAUNCH("iir aggregate");
-        }
         if (stages & 8u) {
             return launch_scan<kPowerSections, kPreSections>(m, iir, aggr, L.nrg, len, false,
-                                                             true, stream);
+                                                             true, stream, false, true);
         }
         return PESQ_OK;
     }

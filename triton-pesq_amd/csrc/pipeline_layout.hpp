@@ -57,7 +57,8 @@ struct PipeLayout {
     // The forward's chain kernel also runs the aggregate pass of the backward's
     // level alignment filter (power^T on f, which only needs forward data), on
     // grids whose backward scan stores lane states and fuses its block prefix;
-    // the backward's aggregate launch then runs the pre-emphasis filter alone.
+    // the backward's output launch then warms the pre-emphasis filter's block
+    // start states up from the two previous blocks, and there is no aggregate launch.
     // The backward scan's workspace (aggr_b) then lies in the forward workspace.
     int host_power = 0;
 
