@@ -116,7 +116,11 @@ size_t pesq_model_table_bytes(void);
 /* Pack the model constants into `out` (host memory, pesq_model_table_bytes()).
  * Replaces the buffers registered by PesqLossTriton.__init__
  * (torch_pesq/triton_ops/loss.py:60-92), TritonStftBark.__init__
- * (spectral.py:634-734) and TritonPesqChain.__init__ (chain.py:1057-1078). */
+ * (spectral.py:634-734) and TritonPesqChain.__init__ (chain.py:1057-1078).
+ * The pipeline's scans start each 1024-sample block from the two blocks
+ * before it, so every filter section's state must decay below 1e-20 of
+ * itself over 2048 samples (largest entry of A^2048); tables whose filters
+ * decay more slowly are refused with PESQ_ERR_ARGUMENT. */
 int pesq_model_table_pack(const pesq_model_constants *constants, void *out);
 
 /* ----------------------------------------------------------------------- */

@@ -5,7 +5,7 @@ the data" checks (``tests/test_triton_iir.py:528-554``): the code runs once
 under the profiler and every kernel with device time is listed.  Names are
 normalised to the library's own spelling (``pesq_pipeline_kernels``):
 demangled, without the return type, the namespace and the argument list, and
-with no spaces, e.g. ``iir_output_kernel<5,1,PipeFwdMode,true,true,false>``.
+with no spaces, e.g. ``iir_output_kernel<5,1,PipeFwdMode,true,2,false>``.
 """
 
 import ctypes

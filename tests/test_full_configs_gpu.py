@@ -1,10 +1,11 @@
 """GPU parity at the full BASELINE shapes c3, c4 and c5, forward and backward.
 
 The pipeline chooses kernel variants by grid size (``pesq_pipeline_kernels``
-names them): rows of more than 128 scan blocks launch the block prefix
-kernel (c4: 938 blocks per row), grids of more than 8192 scan wavefronts
-recompute the lane states instead of storing them (c5: 32256 forward, 16128
-backward), and grids of more than 512 frame tiles run four frames per
+names them): grids of more than 8192 scan wavefronts recompute the lane
+states instead of storing them and launch the block prefix kernel (c5: 32256
+forward, 16128 backward), smaller ones take their block starts from the two
+previous blocks' aggregates (c4: 938 blocks per row, whose backward keeps
+its aggregate launch for both filters), and grids of more than 512 frame tiles run four frames per
 wavefront in the STFT and chain kernels (c4: 940 tiles, c5: 4096).  Those
 variants only run at these shapes, so these tests run the whole batch of each
 config, record the kernels the step launches (``torch.profiler``), check that
@@ -99,15 +100,18 @@ def _assert_pipeline_variants(kernels, batch, length):
 
 
 def test_config4_full_batch_forward_and_backward():
-    """4 x 60 s: prefix kernels in both scan passes, four frames per wavefront."""
+    """4 x 60 s: windowed block starts over rows of 938 blocks in both scan
+    passes, four frames per wavefront."""
 
     ref_np, deg_np, fs, weights, outputs, g_deg, kernels = _run_step(4)
     batch, length = ref_np.shape
     _assert_pipeline_variants(kernels, batch, length)
-    for name in ("iir_prefix_kernel<6>", "iir_output_kernel<5,1,PipeBwdMode,true,false,false>",
-                 "iir_output_kernel<5,1,PipeFwdMode,true,false,false>", "chain_bwd_kernel<4,1>",
+    for name in ("iir_aggregate_split_kernel<5,1,3,PipeBwdMode>",
+                 "iir_output_kernel<5,1,PipeBwdMode,true,2,false>",
+                 "iir_output_kernel<5,1,PipeFwdMode,true,2,false>", "chain_bwd_kernel<4,1>",
                  "chain_fwd_kernel<4,1>"):
         assert name in kernels, name
+    assert "iir_prefix_kernel<6>" not in kernels
     # the STFT variant for large grids (its arithmetic type is the library's choice)
     assert any(k.startswith("stft_fwd_kernel<") and k.endswith(",true,8>") for k in kernels)
     saturated = _compare_with_oracle(ref_np, deg_np, fs, weights, outputs, g_deg, range(batch))
@@ -125,10 +129,10 @@ def test_config5_full_batch_forward_and_backward():
     batch = ref_np.shape[0]
     length = O.resample_length(ref_np.shape[1], fs, 16000)
     _assert_pipeline_variants(kernels, batch, length)
-    for name in ("iir_aggregate_kernel<5,1,PipeFwdMode,false,0,6>",
-                 "iir_output_kernel<5,1,PipeFwdMode,false,false,false>",
+    for name in ("iir_aggregate_kernel<5,1,PipeFwdMode,false,0,6>", "iir_prefix_kernel<6>",
+                 "iir_output_kernel<5,1,PipeFwdMode,false,0,false>",
                  "iir_aggregate_kernel<5,1,PipeBwdMode,false,0,6>",
-                 "iir_output_kernel<5,1,PipeBwdMode,false,false,false>",
+                 "iir_output_kernel<5,1,PipeBwdMode,false,0,false>",
                  "chain_bwd_kernel<4,1>", "resample_fwd_window<3>", "resample_bwd_window<3>"):
         assert name in kernels, name
     _compare_with_oracle(ref_np, deg_np, fs, weights, outputs, g_deg, range(batch))
@@ -156,7 +160,7 @@ def test_config3_full_batch_forward_and_backward():
 
 def test_config4_length_unsaturated_items():
     """Three 60 s items of the speech-like pair at a moderate noise level: the
-    c4 row length (prefix kernels in both scan passes, the band totals kernel)
+    c4 row length (windowed block starts in both scan passes, the band totals kernel)
     and the four-frame chain variants (705 chain tiles), with both distances
     inside their clamps, so the asymmetric path of 60 s rows (its fifth root
     asymmetry factor, the band totals feeding it) is compared with float64."""
@@ -177,7 +181,8 @@ def test_config4_length_unsaturated_items():
     step()
     (outputs, g_deg), kernels = launched_kernels(step)
     _assert_pipeline_variants(kernels, 3, 960000)
-    for name in ("iir_prefix_kernel<6>", "chain_fwd_kernel<4,1>", "chain_bwd_kernel<4,1>"):
+    for name in ("iir_output_kernel<5,1,PipeFwdMode,true,2,false>", "chain_fwd_kernel<4,1>",
+                 "chain_bwd_kernel<4,1>"):
         assert name in kernels, name
     assert any(k.startswith("band_totals_kernel<") for k in kernels)
     outputs = [o.detach().double().cpu() for o in outputs]

@@ -326,28 +326,62 @@ def test_model_table_pack_rejects_bad_bands():
                          m.loudness.exp, m.fbank.width_bark, m.fbank.total_width, 0.1866055)
 
 
-def test_pre_emphasis_decays_within_the_warm_up():
-    """The backward's output pass starts the pre-emphasis filter 2048 samples
-    before each block from a zero state: the standard filter's state keeps at
-    most 3e-24 of itself over that span (largest entry of A^2048; pole radius
-    0.973; the pack requires at most 1e-20), and a filter decaying more
-    slowly is refused where the table is packed."""
+def _pair_decay(poles, n=2048):
+    """Largest entry of A^n for the 2x2 companion block of each pole pair
+    (z^2 + a1 z + a2 with the pair's roots), over the pairs."""
 
+    poles = sorted(poles, key=lambda p: (abs(p.imag), p.real))
+    worst = 0.0
+    for i in range(0, len(poles), 2):
+        a1 = -(poles[i] + poles[i + 1]).real
+        a2 = (poles[i] * poles[i + 1]).real
+        comp = np.array([[-a1, 1.0], [-a2, 0.0]])
+        worst = max(worst, np.abs(np.linalg.matrix_power(comp, n)).max())
+    return worst
+
+
+def _pack(m, power_a=None, pre_a=None):
     from torch_pesq.hip_ops.pipeline import pack_model_table
 
-    m = PesqLoss(1.0, sample_rate=16000)
-    a = m.pre_filter[1].double().numpy()
-    comp = np.array([[-a[1] / a[0], 1.0], [-a[2] / a[0], 0.0]])
-    decay = np.abs(np.linalg.matrix_power(comp, 2048)).max()
-    assert decay < 3e-24
-    assert abs(np.abs(np.roots(a)).max() - 0.9726) < 1e-3
+    return pack_model_table(
+        m.power_filter[0], m.power_filter[1] if power_a is None else power_a,
+        m.pre_filter[0], m.pre_filter[1] if pre_a is None else pre_a,
+        m.to_spec.window, m.fbank.fbank, m.fbank.pow_dens_correction, m.loudness.threshs,
+        m.loudness.exp, m.fbank.width_bark, m.fbank.total_width, 0.1866055)
 
-    slow_a = torch.tensor([1.0, -1.98 * np.cos(0.1), 0.99 ** 2], dtype=torch.float64)
-    with pytest.raises((RuntimeError, ValueError), match="decays too slowly"):
-        pack_model_table(m.power_filter[0], m.power_filter[1], m.pre_filter[0], slow_a,
-                         m.to_spec.window, m.fbank.fbank, m.fbank.pow_dens_correction,
-                         m.loudness.threshs, m.loudness.exp, m.fbank.width_bark,
-                         m.fbank.total_width, 0.1866055)
+
+def test_filters_decay_within_the_window():
+    """The scans start each block from the two blocks before it run from a
+    zero state (and the backward's output pass starts the pre-emphasis
+    filter 2048 samples early): every section's state must keep at most 1e-20
+    of itself over 2048 samples, which the pack checks.  The standard filters
+    keep at most 3e-24 (largest entry of A^2048 over the pole pairs; pole
+    radii 0.968 for the level alignment filter, 0.973 for the pre-emphasis
+    filter), and filters decaying more slowly are refused where the table is
+    packed."""
+
+    m = PesqLoss(1.0, sample_rate=16000)
+    pre_poles = np.roots(m.pre_filter[1].double().numpy())
+    power_poles = np.roots(m.power_filter[1].double().numpy())
+    assert abs(np.abs(pre_poles).max() - 0.9726) < 1e-3
+    assert abs(np.abs(power_poles).max() - 0.968) < 2e-3
+    assert _pair_decay(pre_poles) < 3e-24
+    assert _pair_decay(power_poles) < 3e-24
+    _pack(m)
+
+    slow_pre = torch.tensor([1.0, -1.98 * np.cos(0.1), 0.99 ** 2], dtype=torch.float64)
+    assert _pair_decay(np.roots(slow_pre.numpy())) > 1e-20
+    with pytest.raises((RuntimeError, ValueError), match="pre-emphasis filter decays too slowly"):
+        _pack(m, pre_a=slow_pre)
+    # a level alignment filter of the same order with well separated poles
+    # at radius 0.995
+    angles = np.array([0.3, 0.9, 1.5, 2.1, 2.7])
+    slow_poles = 0.995 * np.exp(1j * np.concatenate([angles, -angles]))
+    slow_power = torch.from_numpy(np.poly(slow_poles).real.copy())
+    assert _pair_decay(slow_poles) > 1e-20
+    with pytest.raises((RuntimeError, ValueError),
+                       match="level alignment filter decays too slowly"):
+        _pack(m, power_a=slow_power)
 
 
 def test_cpu_inputs_and_bad_shapes_raise():
@@ -375,73 +409,74 @@ def test_graft_entry_exposes_build_and_smoke():
 
 #: (batch, 16 kHz length, grad mask) -> kernels of the forward and the backward
 #: pass.  The variants are chosen by grid size: lane states are stored for
-#: grids of up to 8192 scan wavefronts and recomputed above; the block prefix
-#: is fused into the output pass for rows of up to 128 blocks; the STFT and
-#: chain kernels of grids above 512 chain tiles take four frames per wavefront
-#: (the STFT backward two).  Where the backward scan stores lane states and
-#: fuses its block prefix (c2, c3), the forward's chain kernel also runs the
+#: grids of up to 8192 scan wavefronts and recomputed above; grids that store
+#: them take windowed block starts in the output pass (the output kernel's
+#: fifth argument 2, kWindowStarts: the two previous blocks' aggregates), the
+#: others a prefix kernel (0, kStoredStarts); the STFT and chain kernels of
+#: grids above 512 chain tiles take four frames per wavefront (the STFT
+#: backward two).  Where the backward scan stores lane states and has rows of
+#: up to 128 blocks (c2, c3), the forward's chain kernel also runs the
 #: backward's level alignment aggregate and the backward's output pass warms
 #: the pre-emphasis filter up itself, so the backward has no aggregate launch
-#: (the output kernel's third flag).  The aggregate pass of lane-state grids
+#: (the output kernel's last flag).  The aggregate pass of lane-state grids
 #: runs three wavefronts per block, each on its own sections
 #: (iir_aggregate_split_kernel).
 VARIANTS = {
     # BASELINE c2: 16 rows x 125 blocks, 8 x 32 tiles
     (8, 128000, 2): (
         ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>",
-         "iir_output_kernel<5, 1, PipeFwdMode, true, true, false>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, 2, false>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
-         "iir_output_kernel<5, 1, PipeBwdMode, true, true, true>"],
+         "iir_output_kernel<5, 1, PipeBwdMode, true, 2, true>"],
     ),
-    # BASELINE c4: 938 blocks per row (prefix kernel), 4 x 235 = 940 tiles, items
+    # BASELINE c4: 938 blocks per row, 4 x 235 = 940 tiles, items
     # of 235 tiles (per item band totals)
     (4, 960000, 2): (
-        ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeFwdMode, true, false, false>",
+        ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, 2, false>",
          "stft_fwd_kernel<float, true, 8>", "band_totals_kernel<16, 2>",
          "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<4, 1>", "band_totals_kernel<8, 1>", "stft_bwd_kernel<float, 2, 8>",
-         "iir_aggregate_split_kernel<5, 1, 3, PipeBwdMode>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeBwdMode, true, false, false>"],
+         "iir_aggregate_split_kernel<5, 1, 3, PipeBwdMode>",
+         "iir_output_kernel<5, 1, PipeBwdMode, true, 2, false>"],
     ),
     # one item of 65 tiles (1033 frames): just past the band totals threshold
-    # (259 blocks per row: the prefix kernel)
     (1, 264704, 1): (
-        ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeFwdMode, true, false, false>",
+        ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, 2, false>",
          "stft_fwd_kernel<float, false, 8>", "band_totals_kernel<16, 2>",
          "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "band_totals_kernel<8, 1>", "stft_bwd_kernel<float, 1, 9>",
-         "iir_aggregate_split_kernel<5, 1, 3, PipeBwdMode>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeBwdMode, true, false, false>"],
+         "iir_aggregate_split_kernel<5, 1, 3, PipeBwdMode>",
+         "iir_output_kernel<5, 1, PipeBwdMode, true, 2, false>"],
     ),
     # one item of 64 tiles (1023 frames): the largest without band totals
     (1, 262144, 1): (
-        ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeFwdMode, true, false, false>",
+        ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, 2, false>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
-         "iir_aggregate_split_kernel<5, 1, 3, PipeBwdMode>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeBwdMode, true, false, false>"],
+         "iir_aggregate_split_kernel<5, 1, 3, PipeBwdMode>",
+         "iir_output_kernel<5, 1, PipeBwdMode, true, 2, false>"],
     ),
     # BASELINE c5 after the 3:1 resampler: 512 x 63 = 32256 forward scan
     # wavefronts, 256 x 63 = 16128 backward ones (both above 8192)
     (256, 64000, 2): (
         ["iir_aggregate_kernel<5, 1, PipeFwdMode, false, 0, 6>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeFwdMode, false, false, false>",
+         "iir_output_kernel<5, 1, PipeFwdMode, false, 0, false>",
          "stft_fwd_kernel<float, true, 8>", "chain_fwd_kernel<4, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<4, 1>", "stft_bwd_kernel<float, 2, 8>",
          "iir_aggregate_kernel<5, 1, PipeBwdMode, false, 0, 6>", "iir_prefix_kernel<6>",
-         "iir_output_kernel<5, 1, PipeBwdMode, false, false, false>"],
+         "iir_output_kernel<5, 1, PipeBwdMode, false, 0, false>"],
     ),
     # BASELINE c3 after the 441:160 resampler: a small grid like c2
     (16, 64000, 2): (
         ["iir_aggregate_split_kernel<5, 1, 3, PipeFwdMode>",
-         "iir_output_kernel<5, 1, PipeFwdMode, true, true, false>",
+         "iir_output_kernel<5, 1, PipeFwdMode, true, 2, false>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
-         "iir_output_kernel<5, 1, PipeBwdMode, true, true, true>"],
+         "iir_output_kernel<5, 1, PipeBwdMode, true, 2, true>"],
     ),
 }
 

@@ -115,9 +115,11 @@ def _generic_sizes():
 @pytest.mark.parametrize("poison", [float("nan"), -1e30])
 @pytest.mark.parametrize(
     "batch,samples",
-    # small grid (fused block prefix, lane states); 293 blocks per row (prefix
-    # kernel); 320 x 63 forward and 160 x 63 backward scan wavefronts (lane
-    # states recomputed) with 2560 frame tiles (four frames per wavefront)
+    # small grid (lane states, windowed block starts, the backward's level
+    # alignment aggregate in the chain forward); 293 blocks per row (windowed
+    # block starts, the backward's own aggregate launch); 320 x 63 forward and
+    # 160 x 63 backward scan wavefronts (lane states recomputed, prefix
+    # kernel) with 2560 frame tiles (four frames per wavefront)
     [(2, 24000), (3, 300000), (160, 64000)],
 )
 def test_no_uninitialised_reads_pipeline(model, poison, batch, samples):

@@ -14,8 +14,9 @@ compiler-chosen contraction) and every sum of the chain and the STFT is taken
 in an order that does not depend on the variant, so those stages give the
 same bits for an item in any batch.  What remains are the scans: the variant
 that stores the lane states runs the zero-state recursion and an in-wave
-scan, the one that recomputes them uses weighted sums of the chunk's inputs
-and an LDS sum for the block end state.  Both evaluate the same recursion in
+scan and takes its block start states from the two previous blocks'
+aggregates, the one that recomputes them uses weighted sums of the chunk's
+inputs and an LDS sum for the block end state, and a prefix kernel.  Both evaluate the same recursion in
 float64 and differ by float64 rounding (the parallel form's sections are
 larger than their sum, so that is about 1e-11 of a sample); rounded to the
 float32 signals of the forward, a few samples land on the other side of a
@@ -57,12 +58,12 @@ def test_large_grid_variants_match_small_grid_ones():
     # the batch and the single items take different variants of every stage
     assert "stft_fwd_kernel<float, true, 8>" in wide and "stft_fwd_kernel<float, false, 8>" in narrow
     assert "chain_fwd_kernel<4, 1>" in wide and "chain_fwd_kernel<8, 1>" in narrow
-    assert "iir_output_kernel<5, 1, PipeFwdMode, false, false, false>" in wide
-    assert "iir_output_kernel<5, 1, PipeFwdMode, true, false, false>" in narrow
+    assert "iir_output_kernel<5, 1, PipeFwdMode, false, 0, false>" in wide
+    assert "iir_output_kernel<5, 1, PipeFwdMode, true, 2, false>" in narrow
     assert "stft_bwd_kernel<float, 2, 8>" in wide_b and "stft_bwd_kernel<float, 1, 9>" in narrow_b
     assert "chain_bwd_kernel<4, 1>" in wide_b and "chain_bwd_kernel<16, 1>" in narrow_b
-    assert "iir_output_kernel<5, 1, PipeBwdMode, false, false, false>" in wide_b
-    assert "iir_output_kernel<5, 1, PipeBwdMode, true, false, false>" in narrow_b
+    assert "iir_output_kernel<5, 1, PipeBwdMode, false, 0, false>" in wide_b
+    assert "iir_output_kernel<5, 1, PipeBwdMode, true, 2, false>" in narrow_b
 
     ref_np, deg_np = speech_like_pair(ITEMS, SAMPLES, seed=21, noise=0.15)
     ref = torch.from_numpy(ref_np).cuda()

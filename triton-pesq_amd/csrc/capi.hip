@@ -202,20 +202,22 @@ extern "C" int pesq_model_table_pack(const pesq_model_constants *c, void *out) {
             delete t;
             return st;
         }
-        // the backward's output pass starts the pre-emphasis filter kWarmBlocks
-        // blocks early from a zero state (iir.hpp, kWarmB): its state must
-        // have decayed below kWindowDecay over that span
-        const int q = t->iir.na;
-        double m[4] = {1.0, 0.0, 0.0, 1.0};
-        for (int w = 0; w < kWarmBlocks; ++w) mat_mul(t->iir.pw[kLevelBlock][q], m, m);
-        double mx = 0.0;
-        for (double v : m) mx = std::fmax(mx, std::fabs(v));
-        if (!(mx <= kWindowDecay)) {
-            delete t;
-            set_error("the pre-emphasis filter decays too slowly for the pipeline: its state "
-                      "keeps %.3g of itself over %d samples (at most %.0e)",
-                      mx, kWarmBlocks * kSpan, kWindowDecay);
-            return PESQ_ERR_ARGUMENT;
+        // the pipeline's scans start every block from the two blocks before
+        // it, run from a zero state (iir.hpp, windowed block starts): every
+        // section's state must have decayed below kWindowDecay over that span
+        for (int q = 0; q < t->iir.na + t->iir.nb; ++q) {
+            double m[4] = {1.0, 0.0, 0.0, 1.0};
+            for (int w = 0; w < kWarmBlocks; ++w) mat_mul(t->iir.pw[kLevelBlock][q], m, m);
+            double mx = 0.0;
+            for (double v : m) mx = std::fmax(mx, std::fabs(v));
+            if (!(mx <= kWindowDecay)) {
+                const char *name = q < t->iir.na ? "level alignment" : "pre-emphasis";
+                set_error("the %s filter decays too slowly for the pipeline: section %d keeps "
+                          "%.3g of its state over %d samples (at most %.0e)",
+                          name, q, mx, kWarmBlocks * kSpan, kWindowDecay);
+                delete t;
+                return PESQ_ERR_ARGUMENT;
+            }
         }
     }
 

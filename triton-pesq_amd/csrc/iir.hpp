@@ -86,26 +86,43 @@ struct IirTable {
     double blk_pw2[kWave][kMaxSections][4];
 };
 
-// Small grids (those that keep lane states) of rows of up to
-// kFusedPrefixBlocks blocks skip the prefix pass: every output wavefront
-// derives its block's start state from the block aggregates itself
-// (block_start_load, block_start_reduce).  Large grids keep the separate
-// prefix kernel, whose work is not repeated per block.
+// How an output wavefront obtains its block's start state (the kPrefix
+// argument of iir_output_kernel):
+//   kStoredStarts  the prefix kernel has replaced the block aggregates by
+//                  the block start states (large grids of general filters);
+//   kFusedSums     the exact prefix sum over all earlier blocks' aggregates,
+//                  formed by the wavefront itself (block_start_load,
+//                  block_start_reduce): small grids (those that keep lane
+//                  states) of rows of up to kFusedPrefixBlocks blocks;
+//   kWindowStarts  the aggregates of the kWarmBlocks blocks before it only
+//                  (block_window_load): filters whose state decays below
+//                  kWindowDecay over that span (the pipeline's), grids that
+//                  keep lane states.  Where the output pass recomputes the
+//                  lane states, the window's uniform values would join the
+//                  recomputation's coefficients in scalar registers, which
+//                  then spill into vector lanes: the prefix pass costs less.
+constexpr int kStoredStarts = 0;
+constexpr int kFusedSums = 1;
+constexpr int kWindowStarts = 2;
 #ifndef PESQ_FUSED_PREFIX_BLOCKS
 #define PESQ_FUSED_PREFIX_BLOCKS 128
 #endif
 constexpr int kFusedPrefixBlocks = PESQ_FUSED_PREFIX_BLOCKS;
 static_assert(kFusedPrefixBlocks <= 2 * kWave, "two blocks per lane");
 
-// Warm-up of filter B.  A block's start state differs from the end state of
-// the kWarmBlocks blocks before it, run from a zero state, by
+// Windowed block starts.  A block's start state differs from the end state
+// of the kWarmBlocks blocks before it, run from a zero state, by
 // A^(kWarmBlocks kSpan) applied to the state there, i.e. by at most twice
 // kWindowDecay of the state's largest component when every entry of that
-// matrix power is below kWindowDecay (checked where the pipeline's table is
-// packed).  For the pre-emphasis filter (pole radius 0.973) the largest entry
-// of A^2048 is 3e-24, far below the float64 rounding of the recursion, so the backward's output
-// pass forms filter B's block start states itself (kWarmB) and needs no
-// aggregate pass for it.
+// matrix power is below kWindowDecay (checked for every section where the
+// pipeline's table is packed).  For the PESQ filters (pole radii up to 0.968
+// for the level alignment filter, 0.973 for the pre-emphasis filter) the
+// largest entry of A^2048 is 3e-24, far below the float64 rounding of the
+// recursion.  So an output wavefront takes its block start state from the
+// aggregates of the two blocks before it (kWindowStarts), with no prefix
+// pass, and the backward's output pass forms filter B's block start states
+// from that filter's inputs in those blocks (kWarmB), with no aggregate pass
+// for it.
 constexpr int kWarmBlocks = 2;
 constexpr double kWindowDecay = 1e-20;
 
@@ -294,6 +311,43 @@ __device__ __forceinline__ void block_start_load(const double *row_aggr, int nbl
         e0.v[k] = j0 >= 0 ? a.y : 0.0;
         e1.u[k] = j0 + 1 >= 0 ? b.x : 0.0;
         e1.v[k] = j0 + 1 >= 0 ? b.y : 0.0;
+    }
+}
+
+// Start state of block `blk` of a row from the zero start end states of the
+// kWarmBlocks = 2 blocks before it (windowed block starts, above):
+//     p = e_(blk-1) + M e_(blk-2),  M = A^kSpan per section.
+// The addresses are uniform over the wavefront.  e0 receives e_(blk-2), e1
+// e_(blk-1) (0 before the row start; sections NL .. NS - 1 take none);
+// block_window_start then leaves p in e0.
+template <int NS, int NL = NS>
+__device__ __forceinline__ void block_window_load(const double *row_aggr, int nblk, int blk,
+                                                  Bank<NS> &e0, Bank<NS> &e1) {
+    static_assert(kWarmBlocks == 2, "a window of two blocks");
+#pragma unroll
+    for (int k = NL; k < NS; ++k) e0.u[k] = e0.v[k] = e1.u[k] = e1.v[k] = 0.0;
+    const int c0 = blk >= 2 ? blk - 2 : 0, c1 = blk >= 1 ? blk - 1 : 0;
+#pragma unroll
+    for (int k = 0; k < NL; ++k) {
+        const double *sec = row_aggr + int64_t(k) * nblk * 2;
+        const double2 a = *reinterpret_cast<const double2 *>(sec + 2 * c0);
+        const double2 b = *reinterpret_cast<const double2 *>(sec + 2 * c1);
+        e0.u[k] = blk >= 2 ? a.x : 0.0;
+        e0.v[k] = blk >= 2 ? a.y : 0.0;
+        e1.u[k] = blk >= 1 ? b.x : 0.0;
+        e1.v[k] = blk >= 1 ? b.y : 0.0;
+    }
+}
+template <int NS>
+__device__ __forceinline__ void block_window_start(const IirTable &t, Bank<NS> &e0,
+                                                   const Bank<NS> &e1) {
+#pragma unroll
+    for (int k = 0; k < NS; ++k) {
+        const double *m = t.pw[kLevelBlock][k];
+        const double u = fma(m[0], e0.u[k], fma(m[1], e0.v[k], e1.u[k]));
+        const double v = fma(m[2], e0.u[k], fma(m[3], e0.v[k], e1.v[k]));
+        e0.u[k] = u;
+        e0.v[k] = v;
     }
 }
 
@@ -852,15 +906,16 @@ __global__ void __launch_bounds__(kWave *kPrefixWaves)
     }
 }
 
-template <int NA, int NB, class Mode, bool kLaneStates, bool kFusedPrefix, bool kWarmB = false>
+template <int NA, int NB, class Mode, bool kLaneStates, int kPrefix, bool kWarmB = false>
 __global__ void __launch_bounds__(kWave)
     iir_output_kernel(Mode m, const IirTable *__restrict__ table,
                       const double *__restrict__ aggr, const double *__restrict__ lanes,
                       int64_t len, int nblk) {
     constexpr int NS = NA + NB;
-    static_assert(kLaneStates || !kFusedPrefix, "the fused prefix is for small grids");
-    static_assert(!kWarmB || (kLaneStates && kFusedPrefix && NB == 1),
-                  "filter B warms up beside stored lane states of A and the fused prefix");
+    static_assert(kLaneStates || kPrefix == kStoredStarts,
+                  "grids that recompute the lane states take stored block starts");
+    static_assert(!kWarmB || (kLaneStates && kPrefix != kStoredStarts && NB == 1),
+                  "filter B warms up beside stored lane states of A and their block starts");
     const int row = blockIdx.x / nblk;
     const int blk = blockIdx.x - row * nblk;
     const int lane = threadIdx.x;
@@ -870,11 +925,13 @@ __global__ void __launch_bounds__(kWave)
     // states, the lane start states, the row constants and the raw inputs
     const double *row_aggr = aggr + int64_t(row) * NS * nblk * 2;
     BankPair<NA, NB> p;
-    Bank<NS> e0, e1;  // kFusedPrefix: the block aggregates this block starts from
+    Bank<NS> e0, e1;  // kFusedSums, kWindowStarts: the block aggregates this block starts from
     PairPowers<NS> pp;
-    if constexpr (kFusedPrefix) {
+    if constexpr (kPrefix == kFusedSums) {
         block_start_load<NS, kWarmB ? NA : NS>(row_aggr, nblk, blk, lane, e0, e1);
         pp.load(*table, lane);
+    } else if constexpr (kPrefix == kWindowStarts) {
+        block_window_load<NS, kWarmB ? NA : NS>(row_aggr, nblk, blk, e0, e1);
     } else {
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
@@ -933,9 +990,13 @@ __global__ void __launch_bounds__(kWave)
         m.setup(row, sh, lane);
     }
     const IirTable &t2 = *table;
-    if constexpr (kFusedPrefix) {
-        __shared__ double red[wave_sums_lds_doubles<2 * NS>()];
-        block_start_reduce<NS>(t2, pp, e0, e1, red, lane);
+    if constexpr (kPrefix != kStoredStarts) {
+        if constexpr (kPrefix == kFusedSums) {
+            __shared__ double red[wave_sums_lds_doubles<2 * NS>()];
+            block_start_reduce<NS>(t2, pp, e0, e1, red, lane);
+        } else {
+            block_window_start<NS>(t2, e0, e1);
+        }
 #pragma unroll
         for (int k = 0; k < NS; ++k) {
             p.u(k) = e0.u[k];
@@ -1041,11 +1102,16 @@ __global__ void __launch_bounds__(kWave)
 // Host side: aggregate, prefix and output launches of one scan pass over
 // `rows` rows; `ws` holds scan_workspace_doubles(rows, nblk, NA + NB).
 // split: the aggregate pass of lane-state grids by kSplitWaves wavefronts per
-// block (iir_aggregate_split_kernel).
+// block (iir_aggregate_split_kernel).  window: the table's sections decay
+// below kWindowDecay over kWarmBlocks blocks (the caller has checked it), so
+// the output pass of lane-state grids takes windowed block starts (no prefix
+// pass).  warm_b (lane-state grids with windowed or fused block starts): the
+// output pass warms filter B up itself, the aggregate pass need not have run
+// it.
 template <int NA, int NB, class Mode>
 int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, int64_t len,
                 bool aggregate, bool output, hipStream_t stream, bool split = false,
-                bool warm_b = false) {
+                bool warm_b = false, bool window = false) {
     constexpr int NS = NA + NB;
     static_assert(NS <= kMaxSections, "too many sections");
     const int64_t nblk = cdiv(len, kBlockSpan);
@@ -1055,7 +1121,8 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
     if (grid == 0) return PESQ_OK;
     const ScanPlan plan = scan_plan(rows, nblk);
     const bool lane_states = plan.lane_states;
-    const bool fused = plan.fused_prefix;
+    const bool windowed = window && lane_states;
+    const bool fused = !windowed && plan.fused_prefix;
     if (aggregate) {
         bool launched = false;
         if constexpr (NA + NB >= kSplitWaves) {
@@ -1076,7 +1143,7 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
                                static_cast<int>(nblk));
         }
         PESQ_CHECK_LAUNCH("iir aggregate");
-        if (!fused) {
+        if (!fused && !windowed) {
             const int64_t nseq = rows * NS;
             hipLaunchKernelGGL(iir_prefix_kernel<NS>,
                                dim3(static_cast<unsigned>(cdiv(nseq, kPrefixWaves))),
@@ -1091,23 +1158,30 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
         const int nb = static_cast<int>(nblk);
         bool launched = false;
         if constexpr (NB == 1 && Mode::kInputs == 2) {
-            if (fused && warm_b) {
-                // filter B's block starts from its own warm-up (no aggregates of B)
-                hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, true, true>),
+            // filter B's block starts from its own warm-up (no aggregates of B)
+            if (windowed && warm_b) {
+                hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, kWindowStarts, true>),
+                                   dim3(grid), dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
+                launched = true;
+            } else if (fused && warm_b) {
+                hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, kFusedSums, true>),
                                    dim3(grid), dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
                 launched = true;
             }
         }
         if (launched) {
+        } else if (windowed) {
+            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, kWindowStarts>),
+                               dim3(grid), dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
         } else if (fused) {
-            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, true>), dim3(grid),
+            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, kFusedSums>), dim3(grid),
                                dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
         } else if (lane_states) {
-            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, false>), dim3(grid),
-                               dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
+            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, kStoredStarts>),
+                               dim3(grid), dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
         } else {
-            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, false, false>), dim3(grid),
-                               dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
+            hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, false, kStoredStarts>),
+                               dim3(grid), dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
         }
         PESQ_CHECK_LAUNCH("iir output");
     }

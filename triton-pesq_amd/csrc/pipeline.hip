@@ -1719,10 +1719,15 @@ constexpr bool kSplitAggregate = PESQ_SPLIT_AGGREGATE != 0;
 static void scan_kernel_names(const ScanPlan &S, const char *mode, std::string &out,
                               bool host_power = false) {
     const char *lanes = S.lane_states ? "true" : "false";
+    const int prefix = kPipeWindow && S.lane_states
+                           ? kWindowStarts
+                           : (S.fused_prefix ? kFusedSums : kStoredStarts);
+    const std::string output = std::string("iir_output_kernel<5, 1, ") + mode + ", " + lanes +
+                               ", " + std::to_string(prefix) + ", ";
     if (host_power) {
         // no aggregate launch: the level alignment filter's ran in the forward's
         // chain kernel, the pre-emphasis filter warms up in the output pass
-        out += std::string("iir_output_kernel<5, 1, ") + mode + ", true, true, true>;";
+        out += output + "true>;";
         return;
     } else if (kSplitAggregate && S.lane_states) {
         out += "iir_aggregate_split_kernel<5, 1, " + std::to_string(kSplitWaves) + ", " + mode +
@@ -1730,9 +1735,8 @@ static void scan_kernel_names(const ScanPlan &S, const char *mode, std::string &
     } else {
         out += std::string("iir_aggregate_kernel<5, 1, ") + mode + ", " + lanes + ", 0, 6>;";
     }
-    if (!S.fused_prefix) out += "iir_prefix_kernel<6>;";
-    out += std::string("iir_output_kernel<5, 1, ") + mode + ", " + lanes + ", " +
-           (S.fused_prefix ? "true" : "false") + ", false>;";
+    if (prefix == kStoredStarts) out += "iir_prefix_kernel<6>;";
+    out += output + "false>;";
 }
 
 static int check_sizes(int64_t batch, int64_t len, const PipeLayout &L) {
@@ -1858,7 +1862,8 @@ extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, 
     if (stages & 3u) {
         if (int st = launch_scan<kPowerSections, kPreSections>(m, iir, aggr, L.rows, len,
                                                                stages & 1u, stages & 2u, stream,
-                                                               kSplitAggregate)) {
+                                                               kSplitAggregate, false,
+                                                               kPipeWindow)) {
             return st;
         }
     }
@@ -1969,14 +1974,16 @@ extern "C" int pesq_pipeline_backward_stages(const float *g_symm, const float *g
         double *aggr = region<double>(a.ws, L.aggr_b);
         if (stages & 8u) {
             return launch_scan<kPowerSections, kPreSections>(m, iir, aggr, L.nrg, len, false,
-                                                             true, stream, false, true);
+                                                             true, stream, false, true,
+                                                             kPipeWindow);
         }
         return PESQ_OK;
     }
     double *aggr = region<double>(a.bw, L.aggr_b);
     if (stages & 12u) {
         return launch_scan<kPowerSections, kPreSections>(m, iir, aggr, L.nrg, len, stages & 4u,
-                                                         stages & 8u, stream, kSplitAggregate);
+                                                         stages & 8u, stream, kSplitAggregate,
+                                                         false, kPipeWindow);
     }
     return PESQ_OK;
 }

@@ -12,6 +12,14 @@ namespace pesq {
 constexpr int kPowerSections = 5;  // order 10 band pass, parallel form
 constexpr int kPreSections = 1;    // pre-emphasis biquad
 constexpr int kPipeSections = kPowerSections + kPreSections;  // scanned in one pass
+#ifndef PESQ_WINDOW_STARTS
+#define PESQ_WINDOW_STARTS 1
+#endif
+// The pipeline's filters decay below kWindowDecay over kWarmBlocks blocks
+// (pesq_model_table_pack rejects tables whose filters do not), so its scans
+// on lane-state grids take windowed block starts (kWindowStarts) and have no
+// prefix pass.
+constexpr bool kPipeWindow = PESQ_WINDOW_STARTS != 0;
 constexpr int kTile = 16;          // frames per workgroup of the STFT / chain kernels
 constexpr int kBwdFrames = 8;      // frames per workgroup of the plain STFT backward
 constexpr int kBwdHops = kBwdFrames - 1;  // output hop blocks per such workgroup
