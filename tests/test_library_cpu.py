@@ -418,9 +418,9 @@ def test_graft_entry_exposes_build_and_smoke():
 #: up to 128 blocks (c2, c3), the forward's chain kernel also runs the
 #: backward's level alignment aggregate and the backward's output pass warms
 #: the pre-emphasis filter up itself, so the backward has no aggregate launch
-#: (the output kernel's last flag).  The aggregate pass of lane-state grids
-#: runs three wavefronts per block, each on its own sections
-#: (iir_aggregate_split_kernel).
+#: (iir_output_split_kernel: the two filters on two wavefronts per block).
+#: The aggregate pass of lane-state grids runs three wavefronts per block,
+#: each on its own sections (iir_aggregate_split_kernel).
 VARIANTS = {
     # BASELINE c2: 16 rows x 125 blocks, 8 x 32 tiles
     (8, 128000, 2): (
@@ -428,7 +428,7 @@ VARIANTS = {
          "iir_output_kernel<5, 1, PipeFwdMode, true, 2, false>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
-         "iir_output_kernel<5, 1, PipeBwdMode, true, 2, true>"],
+         "iir_output_split_kernel<5, 1, PipeBwdMode, true>"],
     ),
     # BASELINE c4: 938 blocks per row, 4 x 235 = 940 tiles, items
     # of 235 tiles (per item band totals)
@@ -476,7 +476,7 @@ VARIANTS = {
          "iir_output_kernel<5, 1, PipeFwdMode, true, 2, false>",
          "stft_fwd_kernel<float, false, 8>", "chain_fwd_kernel<8, 1>", "chain_final_kernel"],
         ["chain_bwd_kernel<16, 1>", "stft_bwd_kernel<float, 1, 9>",
-         "iir_output_kernel<5, 1, PipeBwdMode, true, 2, true>"],
+         "iir_output_split_kernel<5, 1, PipeBwdMode, true>"],
     ),
 }
 

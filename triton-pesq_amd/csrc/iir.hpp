@@ -61,6 +61,17 @@ constexpr int64_t kBlockSpan = kSpan;
 #endif
 // wavefronts per block of the split aggregate pass (each on its own sections)
 constexpr int kSplitWaves = PESQ_SPLIT_WAVES;
+#ifndef PESQ_SPLIT_OUTPUT
+#define PESQ_SPLIT_OUTPUT 1
+#endif
+// the output pass that warms filter B up (kWarmB) by kOutputWaves wavefronts
+// per block, filter A's sections on one, filter B's warm-up and recursion on
+// the other (iir_output_split_kernel)
+constexpr bool kSplitOutput = PESQ_SPLIT_OUTPUT != 0;
+#ifndef PESQ_OUTPUT_WAVES
+#define PESQ_OUTPUT_WAVES 2
+#endif
+constexpr int kOutputWaves = PESQ_OUTPUT_WAVES;
 constexpr int kMaxSections = PESQ_IIR_MAX_SECTIONS;
 // power levels: A^(kChunk 2^j); j = 0..5 in-wave, 6 = one block, 6..11 the
 // block level scan over 64 blocks
@@ -198,6 +209,17 @@ struct Coeffs {
             y += yk;
         }
         return y;
+    }
+    // the same step, each section's output kept apart (y[k] = y_k)
+    __device__ __forceinline__ void step_parts(Bank<NS> &s, double x,
+                                               double (&y)[NS > 0 ? NS : 1]) const {
+#pragma unroll
+        for (int k = 0; k < NS; ++k) {
+            const double yk = fma(b0[k], x, s.u[k]);
+            s.u[k] = fma(-a1[k], yk, fma(b1[k], x, s.v[k]));
+            s.v[k] = kB2 ? fma(b2[k], x, -a2[k] * yk) : -a2[k] * yk;
+            y[k] = yk;
+        }
     }
 };
 
@@ -338,12 +360,12 @@ __device__ __forceinline__ void block_window_load(const double *row_aggr, int nb
         e1.v[k] = blk >= 1 ? b.y : 0.0;
     }
 }
-template <int NS>
+template <int NS, int S0 = 0>
 __device__ __forceinline__ void block_window_start(const IirTable &t, Bank<NS> &e0,
                                                    const Bank<NS> &e1) {
 #pragma unroll
     for (int k = 0; k < NS; ++k) {
-        const double *m = t.pw[kLevelBlock][k];
+        const double *m = t.pw[kLevelBlock][S0 + k];
         const double u = fma(m[0], e0.u[k], fma(m[1], e0.v[k], e1.u[k]));
         const double v = fma(m[2], e0.u[k], fma(m[3], e0.v[k], e1.v[k]));
         e0.u[k] = u;
@@ -1099,6 +1121,282 @@ __global__ void __launch_bounds__(kWave)
     }
 }
 
+// ---------------------------------------------------------------------------
+// The output pass of lane-state grids with windowed block starts by
+// kOutputWaves wavefronts per block, each on its own sections (as the split
+// aggregate pass).  Filter A's sections are shared out in order over the
+// first OutputSplit::kAWaves wavefronts; the last wavefront also runs filter
+// B (with kWarmB, whose warm-up is the longest chain, it runs filter B alone)
+// and forms the Mode's outputs.  A's output c0 x + y_0 + ... + y_(NA-1) is
+// summed in section order as Coeffs::step sums it: the first wavefront's
+// running sums go through LDS to the next, which adds its sections' outputs,
+// and so on to the last, so the outputs are bitwise those of the one-wavefront
+// pass (iir_output_kernel).  The pipeline launches it for the backward's
+// output pass with filter B's warm-up (kWarmB, two wavefronts: the level
+// alignment filter on one, the pre-emphasis filter's warm-up, lane scan and
+// recursion on the other, where one wavefront ran both in turn); the forward's
+// output pass split over two or three wavefronts was no faster in the step.
+// ---------------------------------------------------------------------------
+template <int NA, int NB, bool kWarmB>
+struct OutputSplit {
+    static constexpr int kAWaves = kWarmB ? kOutputWaves - 1 : kOutputWaves;
+    static constexpr int kPer = (NA + kAWaves - 1) / kAWaves;
+    // filter A's sections of wavefront w: [lo(w), hi(w))
+    static constexpr int lo(int w) { return w * kPer < NA ? w * kPer : NA; }
+    static constexpr int hi(int w) { return w == kOutputWaves - 1 ? NA : lo(w + 1); }
+    // every A wavefront has a section
+    static constexpr bool kValid = kAWaves >= 1 && (kAWaves - 1) * kPer < NA;
+};
+
+// The recursion of one wavefront's sections over its lane's chunk: with
+// kFirst the running sums c0 x + y_lo + ... (yrun), else each A section's
+// output (ya[k]); with B sections B's output (yb, Coeffs::step).
+template <bool kGeneral, bool kFirst, int A0, int NAW, int NBW, class Mode>
+__device__ __forceinline__ void split_run(const Mode &m, const Coeffs<A0, NAW, Mode::kB2> &ca,
+                                          const Coeffs<A0 + NAW, NBW, Mode::kB2> &cb,
+                                          const typename Mode::In (&in)[kChunk][Mode::kInputs],
+                                          int64_t j0, int64_t len, BankPair<NAW, NBW, A0> &s,
+                                          double (&yrun)[kChunk],
+                                          double (&ya)[NAW > 0 ? NAW : 1][kChunk],
+                                          double (&yb)[kChunk]) {
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+        double w, xa, xb;
+        element_inputs<kGeneral>(m, in[i], j0 + i, len, w, xa, xb);
+        if constexpr (kFirst) {
+            yrun[i] = ca.step(s.a, xa);
+        } else if constexpr (NAW > 0) {
+            double y[NAW];
+            ca.step_parts(s.a, xa, y);
+#pragma unroll
+            for (int k = 0; k < NAW; ++k) ya[k][i] = y[k];
+        }
+        if constexpr (NBW > 0) yb[i] = cb.step(s.b, xb);
+    }
+}
+
+// the Mode's outputs of the lane's chunk from A's and B's outputs (the last
+// wavefront), as output_run forms them
+template <bool kGeneral, class Mode>
+__device__ __forceinline__ void split_finish(const Mode &m,
+                                             const typename Mode::In (&in)[kChunk][Mode::kInputs],
+                                             int64_t j0, int64_t len, const double *sh,
+                                             const double (&ya)[kChunk], const double (&yb)[kChunk],
+                                             typename Mode::Out (&out)[Mode::kOutputs][kChunk],
+                                             double &acc) {
+#pragma unroll
+    for (int i = 0; i < kChunk; ++i) {
+        const int64_t j = j0 + i;
+        double w, xa, xb;
+        element_inputs<kGeneral>(m, in[i], j, len, w, xa, xb);
+        typename Mode::Out o[Mode::kOutputs];
+        const double before = acc;
+        m.compute(w, ya[i], yb[i], acc, sh, o);
+        if constexpr (kGeneral) {
+            if (j >= len) acc = before;  // past the end of the row
+        }
+#pragma unroll
+        for (int q = 0; q < Mode::kOutputs; ++q) {
+            out[q][i] = (!kGeneral || j < len) ? o[q] : typename Mode::Out(0);
+        }
+    }
+}
+
+template <int NA, int NB, class Mode, bool kWarmB, int W>
+__device__ __forceinline__ void output_split_wave(const Mode &m, const IirTable &t,
+                                                  const double *aggr, const double *lanes,
+                                                  int64_t len, int nblk, int row, int blk,
+                                                  int lane, int w, double *run) {
+    if (w != W) {
+        if constexpr (W + 1 < kOutputWaves) {
+            output_split_wave<NA, NB, Mode, kWarmB, W + 1>(m, t, aggr, lanes, len, nblk, row,
+                                                            blk, lane, w, run);
+        }
+        return;
+    }
+    using Plan = OutputSplit<NA, NB, kWarmB>;
+    static_assert(Plan::kValid, "every A wavefront has a section");
+    constexpr int NS = NA + NB;
+    constexpr bool kLast = W == kOutputWaves - 1;
+    constexpr int A0 = Plan::lo(W);
+    constexpr int NAW = Plan::hi(W) - A0;  // filter A's sections here
+    constexpr int NBW = kLast ? NB : 0;    // filter B's sections here
+    constexpr int N = NAW + NBW;           // sections A0 .. A0 + N - 1
+    constexpr int NL = kWarmB && kLast ? NAW : N;  // of them with aggregates and lane states
+    static_assert(!kWarmB || (NB == 1 && Mode::kInputs == 2), "filter B warms up on input 1");
+    static_assert(!kWarmB || !kLast || NAW == 0, "with kWarmB filter B has a wavefront alone");
+    const int64_t j0 = int64_t(blk) * kSpan + int64_t(lane) * kChunk;
+
+    // this wavefront's loads, all requested before the first wait: the
+    // aggregates of the two blocks before this one, the lane states, filter
+    // B's warm-up inputs, the row constants and the raw inputs
+    Bank<N> e0, e1;
+    block_window_load<N, NL>(aggr + (int64_t(row) * NS + A0) * nblk * 2, nblk, blk, e0, e1);
+    BankPair<NAW, NBW, A0> s;
+    {
+        const double2 *src = reinterpret_cast<const double2 *>(lanes) +
+                             ((int64_t(row) * nblk + blk) * NS + A0) * kWave;
+#pragma unroll
+        for (int k = 0; k < NL; ++k) {
+            const double2 v = src[k * kWave + lane];
+            s.u(k) = v.x;
+            s.v(k) = v.y;
+        }
+    }
+    typename Mode::In warm[kWarmB && kLast ? kWarmBlocks : 1][kChunk][Mode::kInputs];
+    if constexpr (kWarmB && kLast) {
+        const typename Mode::In *b_src = m.src(row, 1);
+#pragma unroll
+        for (int q = 1; q <= kWarmBlocks; ++q) {
+            const int64_t jw = blk - q >= 0 ? j0 - int64_t(q) * kSpan : int64_t(lane) * kChunk;
+            const int64_t lo = chunk_lo<Mode::kReverse>(jw, len);  // full chunks
+            typename Mode::In buf[kChunk];
+#pragma unroll
+            for (int r = 0; r < kChunk / 4; ++r) {
+                __builtin_memcpy(buf + 4 * r, b_src + lo + 4 * r, 4 * sizeof(typename Mode::In));
+            }
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i) {
+                warm[q - 1][i][0] = typename Mode::In(0);
+                warm[q - 1][i][1] = buf[Mode::kReverse ? kChunk - 1 - i : i];
+            }
+        }
+    }
+    typename Mode::In in[kChunk][Mode::kInputs];
+    double sh[4];
+    if constexpr (kLast && HasPre<Mode>::value) {
+        typename Mode::Pre pre;
+        m.prefetch(row, lane, pre);
+        load_chunk(m, row, j0, len, in);
+        m.setup(row, sh, lane, pre);
+    } else {
+        load_chunk(m, row, j0, len, in);
+        if constexpr (kLast) m.setup(row, sh, lane);
+    }
+
+    // block start states (windowed), filter B's by warm-up
+    BankPair<NAW, NBW, A0> p;
+    block_window_start<N, A0>(t, e0, e1);
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        p.u(k) = e0.u[k];
+        p.v(k) = e0.v[k];
+    }
+    if constexpr (kWarmB && kLast) {
+        // as iir_output_kernel: filter B's chunk end states from zero in the
+        // previous blocks, carried to this block's start and summed in LDS,
+        // then its in-block lane start states by the aggregate pass's steps
+        Coeffs<A0, 0, Mode::kB2> none;
+        Coeffs<A0, NBW, Mode::kB2> wb;
+        wb.load(t, t.c0b);
+        const double *mk = t.pw[kLevelBlock][NA];
+        double vu = 0.0, vv = 0.0;
+#pragma unroll
+        for (int q = kWarmBlocks; q >= 1; --q) {
+            if (blk - q < 0) continue;  // wave uniform
+            const double u = vu, v = vv;
+            vu = fma(mk[0], u, mk[1] * v);
+            vv = fma(mk[2], u, mk[3] * v);
+            BankPair<0, NBW, A0> e;
+            e.zero();
+            zero_run<false, true>(m, t, none, wb, warm[q - 1], j0 - int64_t(q) * kSpan, len, e);
+            vu += e.b.u[0];
+            vv += e.b.v[0];
+        }
+        __shared__ double red_b[wave_sums_lds_doubles<2>()];
+        const double *lp = t.lane_pw[NA][kWave - 1 - lane];
+        const double wsum[2] = {fma(lp[0], vu, lp[1] * vv), fma(lp[2], vu, lp[3] * vv)};
+        const double sum = wave_sums_lds(wsum, red_b, lane);  // component j in lane 4 j
+        if (lane % 4 == 0 && lane / 4 < 2) red_b[lane / 4] = sum;
+        wave_lds_fence();
+        p.b.u[0] = red_b[0];
+        p.b.v[0] = red_b[1];
+        wave_lds_fence();
+        BankPair<0, NBW, A0> sb;
+        sb.zero();
+        if (general_chunk(j0, len)) {
+            zero_run<true, false>(m, t, none, wb, in, j0, len, sb);
+        } else {
+            zero_run<false, false>(m, t, none, wb, in, j0, len, sb);
+        }
+        sb.scan_chunks(t, lane);
+        s.b.u[0] = dpp_move<0x138, 0xF>(sb.b.u[0]);  // wave_shr:1 (lane 0 reads 0)
+        s.b.v[0] = dpp_move<0x138, 0xF>(sb.b.v[0]);
+    }
+    // lane start state = (start state given a zero block start) + A^(kChunk lane) p
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const double *lp = t.lane_pw[A0 + k][lane];
+        const double pu = p.u(k), pv = p.v(k);
+        s.u(k) = fma(lp[0], pu, fma(lp[1], pv, s.u(k)));
+        s.v(k) = fma(lp[2], pu, fma(lp[3], pv, s.v(k)));
+    }
+
+    // the recursion over this wavefront's sections
+    Coeffs<A0, NAW, Mode::kB2> ca;
+    Coeffs<A0 + NAW, NBW, Mode::kB2> cb;
+    ca.load(t, W == 0 ? t.c0a : 0.0);
+    if constexpr (NBW > 0) cb.load(t, t.c0b);
+    double yrun[kChunk], ya[NAW > 0 ? NAW : 1][kChunk], yb[kChunk];
+    if (general_chunk(j0, len)) {
+        split_run<true, W == 0>(m, ca, cb, in, j0, len, s, yrun, ya, yb);
+    } else {
+        split_run<false, W == 0>(m, ca, cb, in, j0, len, s, yrun, ya, yb);
+    }
+
+    // A's running sums from wavefront to wavefront (every wavefront passes
+    // every barrier; run is [kChunk][kWave])
+#pragma unroll
+    for (int b = 1; b < kOutputWaves; ++b) {
+        if (W == b - 1) {
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i) run[i * kWave + lane] = yrun[i];
+        }
+        __syncthreads();
+        if (W == b) {
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i) {
+                double y = run[i * kWave + lane];
+#pragma unroll
+                for (int k = 0; k < NAW; ++k) y += ya[k][i];
+                yrun[i] = y;
+            }
+        }
+    }
+
+    if constexpr (kLast) {
+        typename Mode::Out out[Mode::kOutputs][kChunk];
+        double acc = 0.0;
+        if (general_chunk(j0, len)) {
+            split_finish<true>(m, in, j0, len, sh, yrun, yb, out, acc);
+        } else {
+            split_finish<false>(m, in, j0, len, sh, yrun, yb, out, acc);
+        }
+#pragma unroll
+        for (int q = 0; q < Mode::kOutputs; ++q) {
+            typename Mode::Out *dst = m.dst(row, q);
+            if (dst != nullptr) store_chunk(dst, out[q], Mode::kReverse, j0, len);
+        }
+        if constexpr (Mode::kAccumulates) {
+            acc = wave_sum(acc);
+            if (lane == 0) m.finish(row, blk, acc);
+        }
+    }
+}
+
+template <int NA, int NB, class Mode, bool kWarmB>
+__global__ void __launch_bounds__(kOutputWaves * kWave)
+    iir_output_split_kernel(Mode m, const IirTable *__restrict__ table,
+                            const double *__restrict__ aggr, const double *__restrict__ lanes,
+                            int64_t len, int nblk) {
+    __shared__ double run[kChunk * kWave];
+    const int row = blockIdx.x / nblk;
+    const int blk = blockIdx.x - row * nblk;
+    output_split_wave<NA, NB, Mode, kWarmB, 0>(m, *table, aggr, lanes, len, nblk, row, blk,
+                                               static_cast<int>(threadIdx.x) % kWave,
+                                               wave_index(), run);
+}
+
 // Host side: aggregate, prefix and output launches of one scan pass over
 // `rows` rows; `ws` holds scan_workspace_doubles(rows, nblk, NA + NB).
 // split: the aggregate pass of lane-state grids by kSplitWaves wavefronts per
@@ -1157,9 +1455,19 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
         const double *cl = lanes;
         const int nb = static_cast<int>(nblk);
         bool launched = false;
+        if constexpr (kSplitOutput && NB == 1 && Mode::kInputs == 2 &&
+                      OutputSplit<NA, NB, true>::kValid) {
+            if (windowed && warm_b) {
+                hipLaunchKernelGGL((iir_output_split_kernel<NA, NB, Mode, true>), dim3(grid),
+                                   dim3(kOutputWaves * kWave), 0, stream, m, table, ca, cl, len,
+                                   nb);
+                launched = true;
+            }
+        }
         if constexpr (NB == 1 && Mode::kInputs == 2) {
             // filter B's block starts from its own warm-up (no aggregates of B)
-            if (windowed && warm_b) {
+            if (launched) {
+            } else if (windowed && warm_b) {
                 hipLaunchKernelGGL((iir_output_kernel<NA, NB, Mode, true, kWindowStarts, true>),
                                    dim3(grid), dim3(kWave), 0, stream, m, table, ca, cl, len, nb);
                 launched = true;

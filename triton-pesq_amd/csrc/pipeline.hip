@@ -1727,7 +1727,9 @@ static void scan_kernel_names(const ScanPlan &S, const char *mode, std::string &
     if (host_power) {
         // no aggregate launch: the level alignment filter's ran in the forward's
         // chain kernel, the pre-emphasis filter warms up in the output pass
-        out += output + "true>;";
+        out += kSplitOutput && prefix == kWindowStarts
+                   ? std::string("iir_output_split_kernel<5, 1, ") + mode + ", true>;"
+                   : output + "true>;";
         return;
     } else if (kSplitAggregate && S.lane_states) {
         out += "iir_aggregate_split_kernel<5, 1, " + std::to_string(kSplitWaves) + ", " + mode +
