@@ -890,10 +890,12 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
 constexpr int kFinalMaxThreads = 1024;
 
 // Threads per workgroup of chain_final_kernel: one PSQM window per thread up to
-// 1024 windows (a second window per thread doubles the kernel's latency), at
-// least 256.
+// 1024 windows (a second window per thread doubles the kernel's latency), in
+// whole wavefronts (a single one, at most 64 windows, needs no barrier wait on
+// others).
 static unsigned final_threads(int64_t nwin) {
-    return nwin <= 256 ? 256u : (nwin <= 512 ? 512u : 1024u);
+    const int64_t waves = (nwin + kWave - 1) / kWave;
+    return static_cast<unsigned>(kWave * (waves < 1 ? 1 : (waves > 16 ? 16 : waves)));
 }
 
 // both frame arrays (symmetric, asymmetric) in the same pass over the PSQM
