@@ -1344,8 +1344,11 @@ __device__ __forceinline__ void output_split_wave(const Mode &m, const IirTable 
         split_run<false, W == 0>(m, ca, cb, in, j0, len, s, yrun, ya, yb);
     }
 
-    // A's running sums from wavefront to wavefront (every wavefront passes
-    // every barrier; run is [kChunk][kWave])
+    // A's running sums from wavefront to wavefront (run is [kChunk][kWave]).
+    // The barriers sit in wavefront specific code, but the branch to it is
+    // uniform per wavefront and every wavefront passes all kOutputWaves - 1
+    // of them, in the same order, outside any lane divergent branch, so each
+    // s_barrier is met by the whole workgroup.
 #pragma unroll
     for (int b = 1; b < kOutputWaves; ++b) {
         if (W == b - 1) {
