@@ -415,7 +415,7 @@ def test_graft_entry_exposes_build_and_smoke():
 #: others a prefix kernel (0, kStoredStarts); the STFT and chain kernels of
 #: grids above 512 chain tiles take four frames per wavefront (the STFT
 #: backward two).  Where the backward scan stores lane states and has rows of
-#: up to 128 blocks (c2, c3), the forward's chain kernel also runs the
+#: up to 128 blocks (c2, c3), the forward's STFT kernel also runs the
 #: backward's level alignment aggregate and the backward's output pass warms
 #: the pre-emphasis filter up itself, so the backward has no aggregate launch
 #: (iir_output_split_kernel: the two filters on two wavefronts per block).

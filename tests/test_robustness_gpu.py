@@ -116,7 +116,7 @@ def _generic_sizes():
 @pytest.mark.parametrize(
     "batch,samples",
     # small grid (lane states, windowed block starts, the backward's level
-    # alignment aggregate in the chain forward); 293 blocks per row (windowed
+    # alignment aggregate in the STFT forward); 293 blocks per row (windowed
     # block starts, the backward's own aggregate launch); 320 x 63 forward and
     # 160 x 63 backward scan wavefronts (lane states recomputed, prefix
     # kernel) with 2560 frame tiles (four frames per wavefront)

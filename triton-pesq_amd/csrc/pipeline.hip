@@ -168,7 +168,7 @@ struct PipeBwdMode {
 };
 
 // The level alignment filter (power^T on f) of the backward scan alone, for
-// its aggregate pass inside the forward's chain kernel (iir.hpp
+// its aggregate pass inside the forward's STFT kernel (iir.hpp
 // aggregate_block over sections 0 .. 4); same input and time order as
 // PipeBwdMode, no outputs.
 struct PipeBwdPowerMode {
@@ -440,6 +440,24 @@ __global__ void __launch_bounds__(kWave *kWaves, kLean ? 4 : 1) stft_fwd_kernel(
     const int t0 = tile * kTile;
     const int wave = wave_index();
     const int lane = threadIdx.x % kWave;
+    if constexpr (!kLean) {
+        if (L.host_power && blockIdx.x >= L.batch * L.ntile) {
+            // workgroups past the transform's: the aggregate pass of the
+            // backward's level alignment filter on f (which the scan has just
+            // written), a block of a gradient row per wavefront
+            const int64_t g = int64_t(blockIdx.x - L.batch * L.ntile) * kWaves + wave;
+            if (g < L.nrg * L.nblk) {
+                const int row = static_cast<int>(g / L.nblk);
+                const int blk = static_cast<int>(g - int64_t(row) * L.nblk);
+                double *aggr = region<double>(a.ws, L.aggr_b);
+                double *lanes = aggr + scan_aggr_doubles(L.nrg, L.nblk, kPipeSections);
+                const PipeBwdPowerMode m{region<float>(a.ws, L.f), L.len};
+                aggregate_block<kPowerSections, 0, 0, kPipeSections>(
+                    m, t.iir, aggr, lanes, L.len, static_cast<int>(L.nblk), row, blk, lane);
+            }
+            return;
+        }
+    }
     const int side = wave / kSideWaves;          // 0 = reference, 1 = degraded
     const int row = side * L.batch + item;
 
@@ -661,21 +679,6 @@ __global__ void __launch_bounds__(kWave *kWaves) chain_fwd_kernel(PipeArgs a) {
     const PipeLayout &L = a.L;
     const int wave = wave_index();
     const int lane = threadIdx.x % kWave;
-    if (L.host_power && blockIdx.x >= L.batch * L.ntile) {
-        // workgroups past the chain's: the aggregate pass of the backward's
-        // level alignment filter on f, a block of a gradient row per wavefront
-        const int64_t g = int64_t(blockIdx.x - L.batch * L.ntile) * kWaves + wave;
-        if (g < L.nrg * L.nblk) {
-            const int row = static_cast<int>(g / L.nblk);
-            const int blk = static_cast<int>(g - int64_t(row) * L.nblk);
-            double *aggr = region<double>(a.ws, L.aggr_b);
-            double *lanes = aggr + scan_aggr_doubles(L.nrg, L.nblk, kPipeSections);
-            const PipeBwdPowerMode m{region<float>(a.ws, L.f), L.len};
-            aggregate_block<kPowerSections, 0, 0, kPipeSections>(
-                m, t.iir, aggr, lanes, L.len, static_cast<int>(L.nblk), row, blk, lane);
-        }
-        return;
-    }
     const int nb = L.nb;  // bands: band lane + kWave k is slot k of a lane
     const int item = blockIdx.x / L.ntile;
     const int tile = blockIdx.x - item * L.ntile;
@@ -1686,10 +1689,6 @@ static PipePlan pipe_plan(const PipeLayout &L) {
 
 static void launch_chain_fwd(const PipeArgs &a, unsigned grid, hipStream_t stream) {
     const PipePlan P = pipe_plan(a.L);
-    if (a.L.host_power) {
-        // and the backward's level alignment aggregate blocks, a wavefront each
-        grid += static_cast<unsigned>(cdiv(a.L.nrg * a.L.nblk, P.chain_fwd_waves));
-    }
     if (P.chain_bpl == 2) {
         hipLaunchKernelGGL((chain_fwd_kernel<4, 2>), dim3(grid), dim3(kWave * 4), 0, stream, a);
     } else if (P.chain_fwd_waves == 8) {
@@ -1872,7 +1871,9 @@ extern "C" int pesq_pipeline_forward_stages(const float *ref, const float *deg, 
         }
     }
     if (stages & 4u) {
-        const unsigned grid = static_cast<unsigned>(batch * L.ntile);
+        unsigned grid = static_cast<unsigned>(batch * L.ntile);
+        // and the backward's level alignment aggregate blocks, a wavefront each
+        if (L.host_power) grid += static_cast<unsigned>(cdiv(L.nrg * L.nblk, kStftWaves));
         if (!pipe_plan(L).stft_lean) {
             hipLaunchKernelGGL((stft_fwd_kernel<StftFusedReal, false>), dim3(grid),
                                dim3(kWave * kStftWaves), 0, stream, a);

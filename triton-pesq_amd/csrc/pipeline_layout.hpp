@@ -62,9 +62,11 @@ struct PipeLayout {
     int bwd_fpw = 1;            // frames per wavefront of the fused STFT backward (1 or 2)
     int bwd_waves = kBwdWaves;  // wavefronts per workgroup of the fused STFT backward
     int totals = 0;             // per item band totals (items of more than kTotalsTiles tiles)
-    // The forward's chain kernel also runs the aggregate pass of the backward's
+    // The forward's STFT kernel also runs the aggregate pass of the backward's
     // level alignment filter (power^T on f, which only needs forward data), on
-    // grids whose backward scan stores lane states and fuses its block prefix;
+    // grids whose backward scan stores lane states, with rows of up to
+    // kFusedPrefixBlocks blocks and up to kWideTiles chain tiles (the STFT
+    // forward's variant for more tiles keeps its lean register budget);
     // the backward's output launch then warms the pre-emphasis filter's block
     // start states up from the two previous blocks, and there is no aggregate launch.
     // The backward scan's workspace (aggr_b) then lies in the forward workspace.
@@ -126,7 +128,8 @@ struct PipeLayout {
         take(loud, loud_store ? kChainTermBytes * batch * frames * nb : 0);
         take(bandtot, totals ? size_t(2) * batch * nb * sizeof(double) : 0);
         const ScanPlan bwd_scan = scan_plan(nrg, nblk);
-        host_power = nrg > 0 && bwd_scan.lane_states && bwd_scan.fused_prefix;
+        host_power = nrg > 0 && bwd_scan.lane_states && bwd_scan.fused_prefix &&
+                     b * ntile <= kWideTiles;
         const size_t bwd_scan_bytes =
             size_t(scan_workspace_doubles(nrg, nblk, kPipeSections)) * sizeof(double);
         size_t aggr_f = 0;
