@@ -308,6 +308,22 @@ int pesq_resample_plan_backward(const float *grad_y, float *grad_x, int64_t rows
                                 int64_t n_out, const pesq_resample_plan_info *info,
                                 const void *plan, hipStream_t stream);
 
+/* The two calls above for two signals of one shape at once (x0 -> y0 and
+ * x1 -> y1, each [rows, n]), in one launch over 2 rows: the same outputs as
+ * two single calls, bit for bit, without stacking the signals into one
+ * tensor first.  Replaces the resampling of the stacked reference and
+ * degraded batch in PesqLossTriton.raw (triton_ops/loss.py:130-136) and its
+ * adjoint. */
+int pesq_resample_plan_forward_pair(const float *x0, float *y0, const float *x1, float *y1,
+                                    int64_t rows, int64_t n_in, int64_t n_out,
+                                    const pesq_resample_plan_info *info, const void *plan,
+                                    hipStream_t stream);
+
+int pesq_resample_plan_backward_pair(const float *grad_y0, float *grad_x0, const float *grad_y1,
+                                     float *grad_x1, int64_t rows, int64_t n_in, int64_t n_out,
+                                     const pesq_resample_plan_info *info, const void *plan,
+                                     hipStream_t stream);
+
 /* ----------------------------------------------------------------------- */
 /* STFT / Bark (TritonStftBark, torch_pesq/triton_ops/spectral.py:584-774)  */
 /* ----------------------------------------------------------------------- */

@@ -146,12 +146,13 @@ def test_config3_full_batch_forward_and_backward():
     batch = ref_np.shape[0]
     length = O.resample_length(ref_np.shape[1], fs, 16000)
     _assert_pipeline_variants(kernels, batch, length)
-    # the forward of both signals (34 taps per phase, the 36-tap instantiation
-    # with float samples) and the adjoint (the transposed bank, a resampler from
-    # 16 kHz to 44.1 kHz with 13 taps per phase: 16 taps, double samples)
+    # the forward of both signals in one launch (34 taps per phase, the 36-tap
+    # instantiation with float samples) and the adjoint (the transposed bank, a
+    # resampler from 16 kHz to 44.1 kHz with 13 taps per phase: 16 taps, double
+    # samples)
     resamplers = {k: v for k, v in kernels.items() if k.startswith("resample")}
     assert resamplers == {
-        "resample_phase_major<36,float>": 2,
+        "resample_phase_major<36,float>": 1,
         "resample_phase_major<16,double>": 1,
     }, resamplers
     _compare_with_oracle(ref_np, deg_np, fs, weights, outputs, g_deg, range(batch))

@@ -10,6 +10,7 @@ The exact torchaudio taps themselves are parity unpinned (see
 ``oracle/pesq_oracle.py``).
 """
 
+import ctypes
 import math
 
 import numpy as np
@@ -70,6 +71,50 @@ def test_planned_forward_matches_untiled_kernel(orig, new, length):
     )
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("orig,new", [(44100, 16000), (48000, 16000), (22050, 16000), (8000, 16000)])
+@pytest.mark.parametrize("length", [37, 1001, 44101])
+def test_pair_calls_match_single_calls(orig, new, length):
+    """pesq_resample_plan_forward_pair / _backward_pair (the reference and the
+    degraded signal in one launch, as the loss resamples them) against two
+    single calls: each row is computed by the same code from its own signal,
+    so the outputs are bitwise equal."""
+
+    from torch_pesq import _lib
+
+    mod = HipResample(orig, new).cuda()
+    lib = _lib.library()
+    gen = torch.Generator().manual_seed(length + orig)
+    x0 = torch.randn(3, length, generator=gen).cuda()
+    x1 = torch.randn(3, length, generator=gen).cuda()
+    n_out = O.resample_length(length, orig, new)
+    info = ctypes.byref(mod.plan_info)
+    stream = _lib.stream_handle(x0.device)
+    pair = [torch.empty(3, n_out, device="cuda") for _ in range(2)]
+    single = [torch.empty(3, n_out, device="cuda") for _ in range(2)]
+    _lib.check(lib.pesq_resample_plan_forward_pair(
+        _lib.ptr(x0), _lib.ptr(pair[0]), _lib.ptr(x1), _lib.ptr(pair[1]), 3, length, n_out, info,
+        _lib.ptr(mod.plan), stream), "pesq_resample_plan_forward_pair")
+    for x, y in zip((x0, x1), single):
+        _lib.check(lib.pesq_resample_plan_forward(
+            _lib.ptr(x), _lib.ptr(y), 3, length, n_out, info, _lib.ptr(mod.plan), stream),
+            "pesq_resample_plan_forward")
+    g0 = torch.randn(3, n_out, generator=gen).cuda()
+    g1 = torch.randn(3, n_out, generator=gen).cuda()
+    gpair = [torch.empty(3, length, device="cuda") for _ in range(2)]
+    gsingle = [torch.empty(3, length, device="cuda") for _ in range(2)]
+    _lib.check(lib.pesq_resample_plan_backward_pair(
+        _lib.ptr(g0), _lib.ptr(gpair[0]), _lib.ptr(g1), _lib.ptr(gpair[1]), 3, length, n_out,
+        info, _lib.ptr(mod.plan), stream), "pesq_resample_plan_backward_pair")
+    for g, gx in zip((g0, g1), gsingle):
+        _lib.check(lib.pesq_resample_plan_backward(
+            _lib.ptr(g), _lib.ptr(gx), 3, length, n_out, info, _lib.ptr(mod.plan), stream),
+            "pesq_resample_plan_backward")
+    torch.cuda.synchronize()
+    for a, b in zip(pair + gpair, single + gsingle):
+        assert torch.equal(a, b)
+    assert _close(pair[1], O.resample(x1.double().cpu(), orig, new))
 
 
 @pytest.mark.parametrize("orig", [32000, 48000, 64000, 96000])

@@ -21,8 +21,22 @@ namespace pesq {
 
 constexpr int kResampleThreads = 256;
 
+// The rows of one launch: rows below `split` are rows of p, the others rows
+// of p2 (split = the row count for one signal; two signals of one shape, the
+// reference and the degraded signal, can share a launch).
+template <typename T>
+struct Rows {
+    T *p, *p2;
+    int64_t split;
+    __host__ __device__ __forceinline__ T *row(int64_t r, int64_t n) const {
+        return r < split ? p + r * n : p2 + (r - split) * n;
+    }
+};
+using InRows = Rows<const float>;
+using OutRows = Rows<float>;
+
 __global__ void __launch_bounds__(kResampleThreads)
-    resample_fwd_kernel(const float *__restrict__ x, float *__restrict__ y, int64_t n_in,
+    resample_fwd_kernel(InRows x, OutRows y, int64_t n_in,
                         int64_t n_out, const float *__restrict__ kernel,
                         const int32_t *__restrict__ tap_lo, const int32_t *__restrict__ tap_hi,
                         int64_t orig, int64_t nstep, int64_t width, int64_t wtotal,
@@ -32,7 +46,7 @@ __global__ void __launch_bounds__(kResampleThreads)
     if (m >= n_out) return;
     const int64_t l = m / nstep;
     const int64_t j = m - l * nstep;
-    const float *xr = x + row * n_in;
+    const float *xr = x.row(row, n_in);
     const float *kr = kernel + j * wtotal;
     const int64_t base = l * orig - width;
     const int lo = tap_lo[j], hi = tap_hi[j];
@@ -41,11 +55,11 @@ __global__ void __launch_bounds__(kResampleThreads)
         const int64_t i = base + k;
         if (i >= 0 && i < n_in) acc = fma(static_cast<double>(kr[k]), static_cast<double>(xr[i]), acc);
     }
-    y[row * n_out + m] = static_cast<float>(acc);
+    y.row(row, n_out)[m] = static_cast<float>(acc);
 }
 
 __global__ void __launch_bounds__(kResampleThreads)
-    resample_bwd_kernel(const float *__restrict__ gy, float *__restrict__ gx, int64_t n_in,
+    resample_bwd_kernel(InRows gy, OutRows gx, int64_t n_in,
                         int64_t n_out, const float *__restrict__ kernel,
                         const int32_t *__restrict__ phase_lo, const int32_t *__restrict__ phase_hi,
                         int64_t orig, int64_t nstep, int64_t width, int64_t wtotal,
@@ -53,7 +67,7 @@ __global__ void __launch_bounds__(kResampleThreads)
     const int64_t row = blockIdx.x / blocks_per_row;
     const int64_t i = (blockIdx.x - row * blocks_per_row) * int64_t(blockDim.x) + threadIdx.x;
     if (i >= n_in) return;
-    const float *gr = gy + row * n_out;
+    const float *gr = gy.row(row, n_out);
     const int64_t shifted = i + width;
     const int64_t l0 = shifted / orig;
     const int64_t rho = shifted - l0 * orig;
@@ -68,7 +82,7 @@ __global__ void __launch_bounds__(kResampleThreads)
             }
         }
     }
-    gx[row * n_in + i] = static_cast<float>(acc);
+    gx.row(row, n_in)[i] = static_cast<float>(acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -223,7 +237,7 @@ enum TapSource { kTapsGlobal = 0, kTapsLds = 1, kTapsUniform = 2 };
 
 template <int kSource>
 __global__ void __launch_bounds__(kResampleThreads)
-    resample_fwd_tiled(const float *__restrict__ x, float *__restrict__ y, int64_t n_in,
+    resample_fwd_tiled(InRows x, OutRows y, int64_t n_in,
                        int64_t n_out, const float *__restrict__ taps,
                        const double *__restrict__ taps64, const int32_t *__restrict__ offs,
                        int orig, int nstep, int ntaps, int off_min, int span,
@@ -235,7 +249,7 @@ __global__ void __launch_bounds__(kResampleThreads)
     const int64_t m0 = (blockIdx.x - row * blocks_per_row) * kTileOut;
     const int64_t l_first = m0 / nstep;
     const int64_t in_lo = l_first * orig + off_min;
-    const float *xr = x + row * n_in;
+    const float *xr = x.row(row, n_in);
     stage_row4<0, kStageBatch / 4>(xs, xr, in_lo, n_in, span);
     if constexpr (kSource == kTapsLds) stage_table(tl, taps, ntaps * nstep);
     __syncthreads();
@@ -269,7 +283,7 @@ __global__ void __launch_bounds__(kResampleThreads)
             }
         }
     }
-    float *yr = y + row * n_out;
+    float *yr = y.row(row, n_out);
 #pragma unroll
     for (int q = 0; q < kTileQ; ++q) {
         const int64_t m = m0 + threadIdx.x + int64_t(kResampleThreads) * q;
@@ -335,7 +349,7 @@ __device__ __forceinline__ void stage_row_as(S *__restrict__ dst, const float *_
 // LDS reads before the next tap's), and the staged window covers kTaps.
 template <int kTaps, typename S>
 __global__ void __launch_bounds__(kPhaseMaxThreads)
-    resample_phase_major(const float *__restrict__ x, float *__restrict__ y, int64_t n_in,
+    resample_phase_major(InRows x, OutRows y, int64_t n_in,
                          int64_t n_out, const float *__restrict__ taps,
                          const int32_t *__restrict__ offs, int orig, int nstep, int ntaps,
                          int off_min, int groups, int span, int64_t blocks_per_row) {
@@ -357,7 +371,7 @@ __global__ void __launch_bounds__(kPhaseMaxThreads)
     }
     const int base = offs[jj] - off_min;
     const int64_t l0 = blk * groups * kPhasePeriods;  // first period of the workgroup
-    stage_row_as<S>(xs_phase, x + row * n_in, l0 * orig + off_min, n_in, span);
+    stage_row_as<S>(xs_phase, x.row(row, n_in), l0 * orig + off_min, n_in, span);
     __syncthreads();
     if (!active) return;
     double acc[kPhasePeriods];
@@ -381,7 +395,7 @@ __global__ void __launch_bounds__(kPhaseMaxThreads)
             for (int q = 0; q < kPhasePeriods; ++q) asm volatile("" : "+v"(acc[q]));
         }
     }
-    float *yr = y + row * n_out;
+    float *yr = y.row(row, n_out);
 #pragma unroll
     for (int q = 0; q < kPhasePeriods; ++q) {
         const int64_t m = (l0 + h * kPhasePeriods + q) * nstep + j;
@@ -411,7 +425,7 @@ static int phase_groups(int nstep) {
 // Launches resample_phase_major when the pair suits it (false otherwise):
 // y [rows, n_out] from x [rows, n_in] with the table taps [ntaps][nstep] and
 // offsets offs[nstep] in off_min .. off_max.
-static bool launch_phase_major(const float *x, float *y, int64_t rows, int64_t n_in,
+static bool launch_phase_major(InRows x, OutRows y, int64_t rows, int64_t n_in,
                                int64_t n_out, const float *taps, const int32_t *offs, int orig,
                                int nstep, int ntaps, int off_min, int off_max,
                                hipStream_t stream) {
@@ -483,7 +497,7 @@ constexpr int kMaxWindowLds = 65536;  // bytes of LDS a window kernel may stage
 
 template <int kOrig>
 __global__ void __launch_bounds__(kResampleThreads)
-    resample_fwd_window(const float *__restrict__ x, float *__restrict__ y, int64_t n_in,
+    resample_fwd_window(InRows x, OutRows y, int64_t n_in,
                         int64_t n_out, const double *__restrict__ taps64, int ntaps, int off_min,
                         int span, int64_t blocks_per_row) {
     constexpr int kR = kWinOut;
@@ -497,7 +511,7 @@ __global__ void __launch_bounds__(kResampleThreads)
     const int64_t row = blockIdx.x / blocks_per_row;
     const int64_t m0 = (blockIdx.x - row * blocks_per_row) * kTile;
     const int64_t in_lo = m0 * kOrig + off_min;
-    const float *xr = x + row * n_in;
+    const float *xr = x.row(row, n_in);
     stage_row4<kStride, fwd_window_batch4(kOrig)>(xs, xr, in_lo, n_in, span);
     __syncthreads();
     // staged sample kStride u + o of lane u sits at xl[o + o / kStride]; a
@@ -546,7 +560,7 @@ __global__ void __launch_bounds__(kResampleThreads)
         group(xg, tg, std::false_type{}, kStride);
     }
     if (ntaps > full * kStride) group(xg, tg, std::true_type{}, ntaps - full * kStride);
-    float *yr = y + row * n_out;
+    float *yr = y.row(row, n_out);
     float res[kR];
 #pragma unroll
     for (int r = 0; r < kR; ++r) res[r] = static_cast<float>(acc[r]);
@@ -588,7 +602,7 @@ static int64_t window_lds(int64_t span, int orig) {
 constexpr int kUniQ = 2;
 
 __global__ void __launch_bounds__(kResampleThreads)
-    resample_bwd_uniform(const float *__restrict__ gy, float *__restrict__ gx, int64_t n_in,
+    resample_bwd_uniform(InRows gy, OutRows gx, int64_t n_in,
                          int64_t n_out, const double *__restrict__ row, int orig, int width,
                          int sweeps, int span, int64_t blocks_per_row) {
     extern __shared__ float lds[];
@@ -598,7 +612,7 @@ __global__ void __launch_bounds__(kResampleThreads)
     const int64_t row_id = blockIdx.x / blocks_per_row;
     const int64_t i0 = (blockIdx.x - row_id * blocks_per_row) * per_block;
     const int64_t l_lo = (i0 + width) / orig - (sweeps - 1);
-    const float *gr = gy + row_id * n_out;
+    const float *gr = gy.row(row_id, n_out);
     stage_row4<0, kStageBatch / 4>(gs, gr, l_lo, n_out, span);
     __syncthreads();
     for (int c = 0; c < orig; ++c) {
@@ -623,7 +637,7 @@ __global__ void __launch_bounds__(kResampleThreads)
         }
     }
     __syncthreads();
-    float *gxr = gx + row_id * n_in;
+    float *gxr = gx.row(row_id, n_in);
     for (int s = threadIdx.x; s < per_block; s += kResampleThreads) {
         if (i0 + s < n_in) gxr[i0 + s] = out[s];
     }
@@ -646,7 +660,7 @@ constexpr int kBwdWindowBatch4 = 2;  // staging: float4 loads per thread, 2048 s
 
 template <int kOrig>
 __global__ void __launch_bounds__(kResampleThreads)
-    resample_bwd_window(const float *__restrict__ gy, float *__restrict__ gx, int64_t n_in,
+    resample_bwd_window(InRows gy, OutRows gx, int64_t n_in,
                         int64_t n_out, const double *__restrict__ row, int width, int sweeps,
                         int64_t l_min, int span, int64_t blocks_per_row) {
     constexpr int kV = kWinIn;
@@ -658,7 +672,7 @@ __global__ void __launch_bounds__(kResampleThreads)
     const int64_t row_id = blockIdx.x / blocks_per_row;
     const int64_t l_b = l_min + (blockIdx.x - row_id * blocks_per_row) * kPerBlock;
     const int64_t g_lo = l_b - sweeps + 1;
-    const float *gr = gy + row_id * n_out;
+    const float *gr = gy.row(row_id, n_out);
     stage_row4<0, kBwdWindowBatch4>(gs, gr, g_lo, n_out, span);
     __syncthreads();
     // gy[l_u + p] is staged sample kV u + sweeps - 1 + p, p = v - s
@@ -697,7 +711,7 @@ __global__ void __launch_bounds__(kResampleThreads)
     __syncthreads();
     // input of result k: kOrig l_b - width + k
     const int64_t i_b = kOrig * l_b - width;
-    float *gxr = gx + row_id * n_in;
+    float *gxr = gx.row(row_id, n_in);
     constexpr int kResults = kPerBlock * kOrig;
     static_assert(kResults % 4 == 0, "results in groups of four");
     if (i_b >= 0 && i_b + kResults <= n_in) {
@@ -727,7 +741,7 @@ static int64_t bwd_window_lds(int64_t span, int orig) {
 
 template <bool kLds>
 __global__ void __launch_bounds__(kResampleThreads)
-    resample_bwd_tiled(const float *__restrict__ gy, float *__restrict__ gx, int64_t n_in,
+    resample_bwd_tiled(InRows gy, OutRows gx, int64_t n_in,
                        int64_t n_out, const float *__restrict__ cols,
                        const int32_t *__restrict__ col_lo, int orig, int nstep, int width,
                        int nphases, int sweeps, int ncols, int span, int64_t blocks_per_row) {
@@ -739,7 +753,7 @@ __global__ void __launch_bounds__(kResampleThreads)
     const int64_t i0 = (blockIdx.x - row * blocks_per_row) * kTileOut;
     const int64_t l_lo = (i0 + width) / orig - (sweeps - 1);
     const int64_t m_lo = l_lo * nstep;  // may be negative: those outputs read as zero
-    const float *gr = gy + row * n_out;
+    const float *gr = gy.row(row, n_out);
     stage_row4<0, kStageBatch / 4>(gs, gr, m_lo, n_out, span);
     if constexpr (kLds) {
         for (int s = threadIdx.x; s < nphases * ncols; s += kResampleThreads) cl[s] = cols[s];
@@ -748,7 +762,7 @@ __global__ void __launch_bounds__(kResampleThreads)
     __syncthreads();
     const float *cc = kLds ? cl : cols;
     const int32_t *cq = kLds ? clo : col_lo;
-    float *gxr = gx + row * n_in;
+    float *gxr = gx.row(row, n_in);
 #pragma unroll
     for (int q = 0; q < kTileQ; ++q) {
         const int64_t i = i0 + threadIdx.x + int64_t(kResampleThreads) * q;
@@ -790,8 +804,9 @@ extern "C" int pesq_resample_forward(const float *x, float *y, int64_t rows, int
     const int64_t bpr = cdiv(n_out, kResampleThreads);
     PESQ_CHECK_ARG(rows * bpr < (int64_t(1) << 31), "too many rows x blocks for one launch");
     hipLaunchKernelGGL(resample_fwd_kernel, dim3(static_cast<unsigned>(rows * bpr)),
-                       dim3(kResampleThreads), 0, stream, x, y, n_in, n_out, kernel, tap_lo,
-                       tap_hi, orig_step, new_step, width, width_total, bpr);
+                       dim3(kResampleThreads), 0, stream, InRows{x, x, rows}, OutRows{y, y, rows},
+                       n_in, n_out, kernel, tap_lo, tap_hi, orig_step, new_step, width,
+                       width_total, bpr);
     PESQ_CHECK_LAUNCH("resample forward");
     return PESQ_OK;
 }
@@ -807,8 +822,9 @@ extern "C" int pesq_resample_backward(const float *grad_y, float *grad_x, int64_
     const int64_t bpr = cdiv(n_in, kResampleThreads);
     PESQ_CHECK_ARG(rows * bpr < (int64_t(1) << 31), "too many rows x blocks for one launch");
     hipLaunchKernelGGL(resample_bwd_kernel, dim3(static_cast<unsigned>(rows * bpr)),
-                       dim3(kResampleThreads), 0, stream, grad_y, grad_x, n_in, n_out, kernel,
-                       phase_lo, phase_hi, orig_step, new_step, width, width_total, bpr);
+                       dim3(kResampleThreads), 0, stream, InRows{grad_y, grad_y, rows},
+                       OutRows{grad_x, grad_x, rows}, n_in, n_out, kernel, phase_lo, phase_hi,
+                       orig_step, new_step, width, width_total, bpr);
     PESQ_CHECK_LAUNCH("resample backward");
     return PESQ_OK;
 }
@@ -963,9 +979,10 @@ extern "C" int pesq_resample_plan(const float *kernel, const int32_t *tap_lo,
     return PESQ_OK;
 }
 
-extern "C" int pesq_resample_plan_forward(const float *x, float *y, int64_t rows, int64_t n_in,
-                                          int64_t n_out, const pesq_resample_plan_info *info,
-                                          const void *plan, hipStream_t stream) {
+// y rows from x rows (rows in all) with the plan's kernels
+static int plan_forward(InRows x, OutRows y, int64_t rows, int64_t n_in, int64_t n_out,
+                        const pesq_resample_plan_info *info, const void *plan,
+                        hipStream_t stream) {
     PESQ_CHECK_ARG(info != nullptr, "null plan info");
     const pesq_resample_plan_info &r = *info;
     if (int st = check_resample(rows, n_in, n_out, r.orig_step, r.new_step, r.width, r.width_total)) {
@@ -973,7 +990,7 @@ extern "C" int pesq_resample_plan_forward(const float *x, float *y, int64_t rows
     }
     PESQ_CHECK_ARG(r.fwd_span > 0, "this rate pair has no tiled forward (window too wide)");
     if (rows == 0 || n_out == 0) return PESQ_OK;
-    PESQ_CHECK_ARG(x && y && plan, "null pointer argument");
+    PESQ_CHECK_ARG(x.p && x.p2 && y.p && y.p2 && plan, "null pointer argument");
     // the base index of an output inside the staged window fits int32
     PESQ_CHECK_ARG(n_in < (int64_t(1) << 31) && n_out < (int64_t(1) << 31), "signal too long");
     const int64_t bpr = cdiv(n_out, kTileOut);
@@ -1045,10 +1062,10 @@ extern "C" int pesq_resample_plan_forward(const float *x, float *y, int64_t rows
     return PESQ_OK;
 }
 
-extern "C" int pesq_resample_plan_backward(const float *grad_y, float *grad_x, int64_t rows,
-                                           int64_t n_in, int64_t n_out,
-                                           const pesq_resample_plan_info *info, const void *plan,
-                                           hipStream_t stream) {
+// grad_x rows from grad_y rows (rows in all) with the plan's kernels
+static int plan_backward(InRows grad_y, OutRows grad_x, int64_t rows, int64_t n_in,
+                         int64_t n_out, const pesq_resample_plan_info *info, const void *plan,
+                         hipStream_t stream) {
     PESQ_CHECK_ARG(info != nullptr, "null plan info");
     const pesq_resample_plan_info &r = *info;
     if (int st = check_resample(rows, n_in, n_out, r.orig_step, r.new_step, r.width, r.width_total)) {
@@ -1056,7 +1073,8 @@ extern "C" int pesq_resample_plan_backward(const float *grad_y, float *grad_x, i
     }
     PESQ_CHECK_ARG(r.bwd_span > 0, "this rate pair has no tiled adjoint (window too wide)");
     if (rows == 0 || n_in == 0) return PESQ_OK;
-    PESQ_CHECK_ARG(grad_y && grad_x && plan, "null pointer argument");
+    PESQ_CHECK_ARG(grad_y.p && grad_y.p2 && grad_x.p && grad_x.p2 && plan,
+                   "null pointer argument");
     PESQ_CHECK_ARG(n_in < (int64_t(1) << 31) && n_out < (int64_t(1) << 31), "signal too long");
     const int64_t bpr = cdiv(n_in, kTileOut);
     PESQ_CHECK_ARG(rows * bpr < (int64_t(1) << 31), "too many rows x blocks for one launch");
@@ -1147,4 +1165,40 @@ extern "C" int pesq_resample_plan_backward(const float *grad_y, float *grad_x, i
     }
     PESQ_CHECK_LAUNCH("resample backward (tiled)");
     return PESQ_OK;
+}
+
+extern "C" int pesq_resample_plan_forward(const float *x, float *y, int64_t rows, int64_t n_in,
+                                          int64_t n_out, const pesq_resample_plan_info *info,
+                                          const void *plan, hipStream_t stream) {
+    return plan_forward(InRows{x, x, rows}, OutRows{y, y, rows}, rows, n_in, n_out, info, plan,
+                        stream);
+}
+
+extern "C" int pesq_resample_plan_forward_pair(const float *x0, float *y0, const float *x1,
+                                               float *y1, int64_t rows, int64_t n_in,
+                                               int64_t n_out, const pesq_resample_plan_info *info,
+                                               const void *plan, hipStream_t stream) {
+    PESQ_CHECK_ARG(rows >= 0 && rows < (int64_t(1) << 40), "invalid row count %lld",
+                   (long long)rows);
+    return plan_forward(InRows{x0, x1, rows}, OutRows{y0, y1, rows}, 2 * rows, n_in, n_out, info,
+                        plan, stream);
+}
+
+extern "C" int pesq_resample_plan_backward(const float *grad_y, float *grad_x, int64_t rows,
+                                           int64_t n_in, int64_t n_out,
+                                           const pesq_resample_plan_info *info, const void *plan,
+                                           hipStream_t stream) {
+    return plan_backward(InRows{grad_y, grad_y, rows}, OutRows{grad_x, grad_x, rows}, rows, n_in,
+                         n_out, info, plan, stream);
+}
+
+extern "C" int pesq_resample_plan_backward_pair(const float *grad_y0, float *grad_x0,
+                                                const float *grad_y1, float *grad_x1,
+                                                int64_t rows, int64_t n_in, int64_t n_out,
+                                                const pesq_resample_plan_info *info,
+                                                const void *plan, hipStream_t stream) {
+    PESQ_CHECK_ARG(rows >= 0 && rows < (int64_t(1) << 40), "invalid row count %lld",
+                   (long long)rows);
+    return plan_backward(InRows{grad_y0, grad_y1, rows}, OutRows{grad_x0, grad_x1, rows},
+                         2 * rows, n_in, n_out, info, plan, stream);
 }

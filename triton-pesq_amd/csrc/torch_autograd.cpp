@@ -203,6 +203,26 @@ void resample_enqueue(const float *x, float *y, int64_t rows, int64_t n_in, int6
     }
 }
 
+// resample_enqueue of two signals of one shape (x0 -> y0, x1 -> y1), in one
+// launch where the bank has the tiled kernels
+void resample_enqueue_pair(const float *x0, float *y0, const float *x1, float *y1, int64_t rows,
+                           int64_t n_in, int64_t n_out, const ResampleBank &b, bool forward,
+                           hipStream_t stream) {
+    const pesq_resample_plan_info &info = b.plan_info();
+    if (forward && info.fwd_span > 0) {
+        check(pesq_resample_plan_forward_pair(x0, y0, x1, y1, rows, n_in, n_out, &info,
+                                              b.plan.data_ptr(), stream),
+              "pesq_resample_plan_forward_pair");
+    } else if (!forward && info.bwd_span > 0) {
+        check(pesq_resample_plan_backward_pair(x0, y0, x1, y1, rows, n_in, n_out, &info,
+                                               b.plan.data_ptr(), stream),
+              "pesq_resample_plan_backward_pair");
+    } else {
+        resample_enqueue(x0, y0, rows, n_in, n_out, b, forward, stream);
+        resample_enqueue(x1, y1, rows, n_in, n_out, b, forward, stream);
+    }
+}
+
 // forward: src [rows, n_in] -> [rows, n_other]; adjoint: src [rows, n_out] -> [rows, n_other]
 at::Tensor resample_launch(const at::Tensor &src, int64_t n_other, const ResampleBank &b,
                            bool forward) {
@@ -250,6 +270,56 @@ variable_list Resample::backward(AutogradContext *ctx, variable_list grads) {
     const int64_t n_in = ctx->saved_data["n_in"].toInt();
     return {ResampleAdjoint::apply(grads[0].to(at::kFloat), n_in, b), at::Tensor(), at::Tensor()};
 }
+
+// Resample of the reference and the degraded signal (two [batch, n_in]
+// tensors of one shape) as one node: one launch forward, and one for the
+// adjoints when both signals take a gradient.  An output whose input takes
+// no gradient is marked non-differentiable, so the pipeline after it forms
+// only the gradients the caller asks for.  Under a double backward (grad
+// mode on in the backward) the adjoints are the differentiable
+// ResampleAdjoint nodes of the single signal path.
+struct ResamplePair : public torch::autograd::Function<ResamplePair> {
+    static variable_list forward(AutogradContext *ctx, const at::Tensor &x0, const at::Tensor &x1,
+                                 int64_t n_out, const ResampleBank &b) {
+        b.save(ctx);
+        // an output nothing differentiates gets no zero filled gradient
+        ctx->set_materialize_grads(false);
+        const int64_t rows = x0.size(0), n_in = x0.size(1);
+        ctx->saved_data["n_in"] = n_in;
+        const c10::DeviceGuard guard(x0.device());
+        at::Tensor y0 = at::empty({rows, n_out}, x0.options());
+        at::Tensor y1 = at::empty({rows, n_out}, x0.options());
+        resample_enqueue_pair(x0.data_ptr<float>(), y0.data_ptr<float>(), x1.data_ptr<float>(),
+                              y1.data_ptr<float>(), rows, n_in, n_out, b, true,
+                              current_stream(x0));
+        if (!x0.requires_grad()) ctx->mark_non_differentiable({y0});
+        if (!x1.requires_grad()) ctx->mark_non_differentiable({y1});
+        return {y0, y1};
+    }
+    static variable_list backward(AutogradContext *ctx, variable_list grads) {
+        const bool want0 = grads[0].defined() && ctx->needs_input_grad(0);
+        const bool want1 = grads[1].defined() && ctx->needs_input_grad(1);
+        variable_list out(4);
+        if (!want0 && !want1) return out;
+        const ResampleBank b = ResampleBank::load(ctx);
+        const int64_t n_in = ctx->saved_data["n_in"].toInt();
+        if (torch::autograd::GradMode::is_enabled() || !(want0 && want1)) {
+            if (want0) out[0] = ResampleAdjoint::apply(grads[0].to(at::kFloat), n_in, b);
+            if (want1) out[1] = ResampleAdjoint::apply(grads[1].to(at::kFloat), n_in, b);
+            return out;
+        }
+        const at::Tensor g0 = grads[0].to(at::kFloat).contiguous();
+        const at::Tensor g1 = grads[1].to(at::kFloat).contiguous();
+        const c10::DeviceGuard guard(g0.device());
+        const int64_t rows = g0.size(0), n_out = g0.size(1);
+        out[0] = at::empty({rows, n_in}, g0.options());
+        out[1] = at::empty({rows, n_in}, g0.options());
+        resample_enqueue_pair(g0.data_ptr<float>(), out[0].data_ptr<float>(), g1.data_ptr<float>(),
+                              out[1].data_ptr<float>(), rows, n_in, n_out, b, false,
+                              current_stream(g0));
+        return out;
+    }
+};
 
 // checks the bank's tensors against a signal on `device` and bundles them
 ResampleBank make_bank(int device, const at::Tensor &kernel, const at::Tensor &tap_lo,
@@ -328,8 +398,9 @@ std::vector<at::Tensor> pipeline(const at::Tensor &ref, const at::Tensor &deg,
 }
 
 // pipeline() of the two signals resampled to 16 kHz (n_out samples per row):
-// the same autograd nodes (two resampler nodes, the pipeline node) as the
-// Python calls make one at a time, without their Python in between.  bank:
+// the computation the Python calls make one at a time (each signal resampled,
+// then the pipeline node), with both resamplings in one node and one launch
+// and no Python in between.  bank:
 // the resampler's (kernel, tap_lo, tap_hi, phase_lo, phase_hi, plan, info),
 // steps its (orig_step, new_step, width).
 std::vector<at::Tensor> pipeline_resampled(const at::Tensor &ref, const at::Tensor &deg,
@@ -346,7 +417,8 @@ std::vector<at::Tensor> pipeline_resampled(const at::Tensor &ref, const at::Tens
     TORCH_CHECK(n_out >= 0, "pipeline_resampled: negative output length");
     const ResampleBank b = make_bank(ref.get_device(), bank[0], bank[1], bank[2], bank[3],
                                      bank[4], bank[5], bank[6], steps[0], steps[1], steps[2]);
-    return pipeline(Resample::apply(ref, n_out, b), Resample::apply(deg, n_out, b), table, factor);
+    const variable_list r16 = ResamplePair::apply(ref, deg, n_out, b);
+    return pipeline(r16[0], r16[1], table, factor);
 }
 
 // ---------------------------------------------------------------------------
@@ -431,8 +503,8 @@ struct GraphedLoss : torch::CustomClassHolder {
 
     void enqueue_forward(const float *ref_in, const float *deg_in, hipStream_t stream) const {
         if (resampled) {
-            resample_enqueue(ref_in, ref16.data_ptr<float>(), batch, n_src, n16, bank, true, stream);
-            resample_enqueue(deg_in, deg16.data_ptr<float>(), batch, n_src, n16, bank, true, stream);
+            resample_enqueue_pair(ref_in, ref16.data_ptr<float>(), deg_in, deg16.data_ptr<float>(),
+                                  batch, n_src, n16, bank, true, stream);
             ref_in = ref16.data_ptr<float>();
             deg_in = deg16.data_ptr<float>();
         }
@@ -478,7 +550,11 @@ struct GraphedLoss : torch::CustomClassHolder {
                                      data_or_null<float>(g_ref16), data_or_null<float>(g_deg16),
                                      ws.data_ptr(), scratch.data_ptr(), stream),
               "pesq_pipeline_backward");
-        if (resampled) {
+        if (resampled && g_ref.defined() && g_deg.defined()) {
+            resample_enqueue_pair(g_ref16.data_ptr<float>(), g_ref.data_ptr<float>(),
+                                  g_deg16.data_ptr<float>(), g_deg.data_ptr<float>(), batch, n_src,
+                                  n16, bank, false, stream);
+        } else if (resampled) {
             if (g_ref.defined())
                 resample_enqueue(g_ref16.data_ptr<float>(), g_ref.data_ptr<float>(), batch, n_src,
                                  n16, bank, false, stream);

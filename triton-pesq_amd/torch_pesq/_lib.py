@@ -190,6 +190,14 @@ SIGNATURES = {
         _INT,
         [_P, _P, _I64, _I64, _I64, ctypes.POINTER(ResamplePlanInfo), _P, _P],
     ),
+    "pesq_resample_plan_forward_pair": (
+        _INT,
+        [_P, _P, _P, _P, _I64, _I64, _I64, ctypes.POINTER(ResamplePlanInfo), _P, _P],
+    ),
+    "pesq_resample_plan_backward_pair": (
+        _INT,
+        [_P, _P, _P, _P, _I64, _I64, _I64, ctypes.POINTER(ResamplePlanInfo), _P, _P],
+    ),
 }
 
 _LIB = None
