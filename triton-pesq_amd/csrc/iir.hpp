@@ -619,11 +619,11 @@ __device__ __forceinline__ void chunk_end_state(const IirTable &t, const double 
 
 // zero state run over the lane's chunk: the state after it.  With kWeighted,
 // interior chunks form it as weighted sums of the inputs (chunk_end_state):
-// fewer and independent operations, which large grids (throughput bound)
-// gain from (14 us at BASELINE c5); small grids (latency bound) lose about
-// 1 us to the weights' scalar loads and keep the recursion.  Chunks at a row
-// end always run the recursion, with the ramp weights and bounds of
-// element_inputs.
+// fewer and independent operations (14 us at BASELINE c5; at c2 the split
+// aggregate pass, two sections per wavefront and issue bound, gained 0.6 us,
+// where the one-wavefront pass over six sections had lost 1 us to the
+// weights' scalar loads).  Chunks at a row end always run the recursion,
+// with the ramp weights and bounds of element_inputs.
 template <bool kGeneral, bool kWeighted, int NA, int NB, class Mode, int kBase = 0>
 __device__ __forceinline__ void zero_run(const Mode &m, const IirTable &t,
                                          const Coeffs<kBase, NA, Mode::kB2> &ca,
@@ -733,7 +733,7 @@ __device__ __forceinline__ void aggregate_block(const Mode &m, const IirTable &t
     if (general_chunk(j0, len)) {
         zero_run<true, false>(m, t, ca, cb, in, j0, len, s);
     } else {
-        zero_run<false, false>(m, t, ca, cb, in, j0, len, s);
+        zero_run<false, true>(m, t, ca, cb, in, j0, len, s);
     }
     s.scan_chunks(t, lane);
     if (lane == kWave - 1) {
