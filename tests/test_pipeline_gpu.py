@@ -189,6 +189,41 @@ def test_intermediates_match_oracle(model):
     assert float(frame_err) < 5e-7
 
 
+def test_scan_outputs_of_long_rows_with_a_quiet_part(model):
+    """The scan outputs of rows of 196 blocks against float64 lfilter, with the
+    second half of every row 1e-5 as loud as the first: the output pass takes
+    each block's start state from the two blocks before it, exact to 3e-24 of
+    the state two blocks back, so the quiet half keeps the float32 accuracy
+    of its own level (the error is measured against the quiet half's peak)
+    after the loud half's state has passed through the window.  p (both
+    signals), f (the gradient rows) and the float64 row energies."""
+
+    batch, n = 2, 200000
+    ref, deg = speech_like_pair(batch, n, seed=31, noise=0.2)
+    for x in (ref, deg):
+        x[:, n // 2 :] *= 1e-5
+    r, d = torch.from_numpy(ref).cuda(), torch.from_numpy(deg).cuda()
+    _, ws = pipeline_forward(r, d, model.model_table, 0.5, 2)
+
+    def region(name, dtype, shape):
+        off, size = pipeline_region(batch, n, 2, name)
+        count = int(np.prod(shape))
+        return ws[off : off + size].view(dtype)[:count].view(shape).double().cpu()
+
+    c = O.constants()
+    s = np.concatenate([ref, deg]).astype(np.float64)
+    fx = torch.from_numpy(O.lfilter64(s, c["power_b"], c["power_a"]))
+    px = torch.from_numpy(O.lfilter64(O.edge_ramp(torch.from_numpy(s)).numpy(), c["pre_b"], c["pre_a"]))
+    p = region("p", torch.float32, (2 * batch, n))
+    f = region("f", torch.float32, (batch, n))
+    tail = slice(n // 2 + 4096, n)  # past the loud half's influence on the float32 outputs
+    for got, want in ((p, px), (f, fx[batch:])):
+        assert _grad_err(got[:, : n // 2], want[:, : n // 2]) < 2e-7
+        assert _grad_err(got[:, tail], want[:, tail]) < 2e-7
+    energy = region("rowconst", torch.float64, (2 * batch, 4))[:, 1]
+    assert _rel(energy, (fx**2).sum(1)) < 1e-9
+
+
 def test_deterministic(model):
     ref, deg = speech_like_pair(3, 20000, seed=8, noise=0.1)
     r = torch.from_numpy(ref).cuda().requires_grad_(True)
