@@ -1424,6 +1424,8 @@ int launch_scan(const Mode &m, const IirTable *table, double *ws, int64_t rows, 
     const bool lane_states = plan.lane_states;
     const bool windowed = window && lane_states;
     const bool fused = !windowed && plan.fused_prefix;
+    PESQ_CHECK_ARG(!warm_b || (NB == 1 && Mode::kInputs == 2 && (windowed || fused)),
+                   "filter B warms up only beside windowed or fused block starts");
     if (aggregate) {
         bool launched = false;
         if constexpr (NA + NB >= kSplitWaves) {
