@@ -1014,11 +1014,19 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
     const int64_t fo = int64_t(item) * L.frames;
     const int64_t lbase = t0 / kStride - 1;
 
-    // Bark values of this wavefront's frames (slot q = local frame wave kPer + q)
+    // Bark values of this wavefront's frames (slot q = local frame wave kPer
+    // + q) and, with one frame per wavefront, the forward's per (frame, band)
+    // terms too: requested before the barrier, which would hold back loads
+    // issued after it.  The variants of more frames per wavefront load the
+    // terms where they use them: held in registers they would cost a
+    // wavefront per SIMD.
+    constexpr bool kEarlyTerms = kPer == 1;
     float R[kBPL][kPer + 1], G[kBPL][kPer + 1];
+    ChainTerms cts[kEarlyTerms ? kBPL : 1][kEarlyTerms ? kPer + 1 : 1];
     {
         const float *bref = a.bark_ref + int64_t(item) * L.frames * nb;
         const float *bdeg = a.bark_deg + int64_t(item) * L.frames * nb;
+        const ChainTerms *terms = chain_terms(a);
 #pragma unroll
         for (int k = 0; k < kBPL; ++k) {
             const int band = live[k] ? lane + kWave * k : nb - 1;
@@ -1028,6 +1036,7 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
                 const int64_t fc = frame < L.frames ? frame : L.frames - 1;
                 R[k][q] = bref[fc * nb + band];
                 G[k][q] = bdeg[fc * nb + band];
+                if constexpr (kEarlyTerms) cts[k][q] = terms[(fo + fc) * nb + band];
             }
         }
     }
@@ -1119,8 +1128,10 @@ __global__ void __launch_bounds__(kWave *kWaves, kWaves == 4 && kBPL == 1 ? 4 : 
                 const BandConsts &ck = c[k];
                 const double Rq = R[k][q], Gq = G[k][q];
                 const double er = r[k] * Rq, ed = fpr * Gq;
-                // the forward's terms of this (frame, band) (ChainTerms)
-                const ChainTerms ct = chain_terms(a)[(fo + frame) * nb + lane + kWave * k];
+                // the forward's terms of this (frame, band)
+                const ChainTerms ct = kEarlyTerms
+                                          ? cts[kEarlyTerms ? k : 0][kEarlyTerms ? q : 0]
+                                          : chain_terms(a)[(fo + frame) * nb + lane + kWave * k];
                 const double dst = ct.dist;
                 const double asc = fabs(static_cast<double>(ct.asc));
                 const double su = sgn(dst);
