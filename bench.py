@@ -271,8 +271,19 @@ def capture_step(model, ref, deg):
     )
 
 
-def _stage_times(model, ref, deg, repeats: int = 50):
-    """Average device time of every fused stage, HIP events on the launch stream."""
+def _stage_times(model, ref, deg, repeats: int = 100):
+    """Average device time of every fused stage, HIP events on the launch stream.
+
+    Returns ``(in_step, alone, step)``, seconds.  ``step``: full steps run
+    stage by stage through the ``_stages`` entry points (the kernels and order
+    of the forward and backward entry points), events around the whole loop
+    only (an event between the stages would hold every launch back by a few
+    microseconds).  ``in_step``: per stage, what it adds to that step (the step
+    time less that of steps without the stage, which run on the previous
+    step's data): its kernels and launch gaps with the caches as the step
+    leaves them.  ``alone``: each stage launched again and again on its own,
+    its code and tables staying cached.
+    """
 
     import torch
     from torch_pesq import _lib
@@ -301,6 +312,28 @@ def _stage_times(model, ref, deg, repeats: int = 50):
 
     run("fwd", 0x1F)
     run("bwd", 0xF)
+    order = list(STAGES.items())
+
+    def steps_time(skip=None):
+        # seconds per step of full steps, launched stage by stage, without `skip`
+        def step():
+            for name, (pass_, bits) in order:
+                if name != skip:
+                    run(pass_, bits)
+
+        for _ in range(3):
+            step()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(repeats):
+            step()
+        stop.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop) / repeats * 1e-3
+
+    full = steps_time()
+    in_step = {name: full - steps_time(name) for name, _ in order}
     times = {}
     for name, (pass_, bits) in STAGES.items():
         for _ in range(3):
@@ -313,7 +346,7 @@ def _stage_times(model, ref, deg, repeats: int = 50):
         stop.record()
         torch.cuda.synchronize()
         times[name] = start.elapsed_time(stop) / repeats * 1e-3  # seconds
-    return times
+    return in_step, times, full
 
 
 def cpu_baseline(ref_np, deg_np, gpu_outputs, budget_s: float = 12.0, unsaturated=None):
@@ -444,14 +477,16 @@ def profiled_traffic(config: int):
     return {}
 
 
-def stage_report(stage_s, per_stage, traffic, kernels):
+def stage_report(stage_s, per_stage, traffic, kernels, alone_s=None):
     """Per stage device time, model-bytes roofline and counter-bytes roofline.
 
-    ``frac`` is the canonical model's bytes (every stage of the reference's
-    decomposition reads its inputs and writes its outputs once) over the
-    event time; a fused kernel that never writes the intermediate tensors of
-    the stages it covers can exceed 1 on it.  ``traffic_frac`` is the bytes
-    the kernels moved (counters) over the same time: the physical fraction.
+    ``us`` is the stage's time inside the step (``_stage_times``), ``alone_us``
+    its time launched on its own.  ``frac`` is the canonical model's bytes
+    (every stage of the reference's decomposition reads its inputs and writes
+    its outputs once) over the in-step time; a fused kernel that never writes
+    the intermediate tensors of the stages it covers can exceed 1 on it.
+    ``traffic_frac`` is the bytes the kernels moved (counters) over the same
+    time: the physical fraction.
     """
 
     out = {}
@@ -459,6 +494,7 @@ def stage_report(stage_s, per_stage, traffic, kernels):
         t = stage_s[name]
         entry = {
             "us": round(t * 1e6, 2),
+            "alone_us": round(alone_s[name] * 1e6, 2) if alone_s else None,
             "model_bytes": per_stage[name],
             "achieved_GBps": round(per_stage[name] / t / 1e9, 1),
             "frac": round(per_stage[name] / t / HBM_PEAK, 4),
@@ -562,10 +598,12 @@ def diagnose(config: int, steps: int, warmup: int, copy_calibration: bool = Fals
             "fwd_hbm_frac": round((src_bytes + dst_bytes) / (fwd_ms / 1e3) / HBM_PEAK, 4),
             "bwd_hbm_frac": round((src_bytes + dst_bytes) / (bwd_ms / 1e3) / HBM_PEAK, 4),
         }
-    stage_s = _stage_times(model, ref16.contiguous(), deg16.contiguous(), repeats=steps)
+    stage_s, alone_s, staged_step = _stage_times(model, ref16.contiguous(), deg16.contiguous(),
+                                                 repeats=steps)
     per_stage, total = model_bytes(ref16.shape[0], ref16.shape[1])
     out["stages"] = stage_report(stage_s, per_stage, profiled_traffic(config),
-                                 stage_kernels(ref16.shape[0], ref16.shape[1]))
+                                 stage_kernels(ref16.shape[0], ref16.shape[1]), alone_s)
+    out["staged_step_ms"] = round(staged_step * 1e3, 4)
     out["model_bytes_16k"] = total
     return out
 
@@ -703,11 +741,11 @@ def main(argv=None):
     with torch.no_grad():
         outputs = [o.double().cpu() for o in model._run(ref, deg.detach())]
 
-    stage_s = _stage_times(model, ref, deg.detach())
+    stage_s, alone_s, staged_step = _stage_times(model, ref, deg.detach())
     per_stage, total_bytes = model_bytes(batch, samples)
     kernels = stage_kernels(batch, samples)
     traffic = profiled_traffic(2)
-    stages = stage_report(stage_s, per_stage, traffic, kernels)
+    stages = stage_report(stage_s, per_stage, traffic, kernels, alone_s)
     dominant = max(stage_s, key=stage_s.get)
     achieved = per_stage[dominant] / stage_s[dominant]
     roofline = {
@@ -721,7 +759,9 @@ def main(argv=None):
         "kernel": " + ".join(kernels[dominant]),
         "stage": dominant,
         "model_bytes_per_launch": per_stage[dominant],
+        # what the stage adds to a full step, and the stage launched alone
         "avg_launch_us": round(stage_s[dominant] * 1e6, 2),
+        "alone_us": round(alone_s[dominant] * 1e6, 2),
     }
 
     line = {
@@ -754,6 +794,8 @@ def main(argv=None):
         "step_model_bytes": total_bytes,
         "step_hbm_frac": round(total_bytes / (ms / 1e3) / HBM_PEAK, 4),
         "roofline": roofline,
+        # the step launched stage by stage (the sum the in-step stage times split)
+        "staged_step_ms": round(staged_step * 1e3, 4),
         "stages": stages,
     }
     if not args.no_cpu_baseline:
